@@ -1,0 +1,159 @@
+/*
+ * rustane_hip.h -- C-ABI of librustane_hip.so, the MI355X (gfx950) forward
+ * token loop and greedy decode path for rustane's engine.
+ *
+ * This library takes the place of the reference's device bridge: the `ane`
+ * crate re-exported by crates/ane-bridge/src/lib.rs:1-9 (MIL graph build,
+ * Graph::compile, Executable::run_cached_direct, fp16 IOSurface TensorData)
+ * plus the Accelerate calls of crates/engine/src/cpu/vdsp.rs that the forward
+ * makes.  Above it, the engine's forward/loss API (full_model::forward,
+ * forward_ws, forward_only_ws, forward_losses) keeps its signatures and
+ * weight layout; a Rust `hip-bridge` crate binds these symbols.
+ *
+ * Conventions (mirroring the reference's full_model.rs / layer.rs):
+ *  - All functions return RH_OK (0) on success or a negative RH_E* code; the
+ *    message is available from rh_last_error().  Nothing throws across the
+ *    boundary.
+ *  - Host pointers are owned by the caller and are only read or written
+ *    during the call.  Device pointers (the *_dev entry points) must stay
+ *    valid until the context's stream has drained (rh_sync).
+ *  - A context owns one GPU, one HIP stream and all device memory (fp16
+ *    weights, KV cache, workspaces).  A context is driven by one thread at a
+ *    time; separate contexts may run concurrently (multistream.rs:54-161).
+ *  - Activations are token-major inside the library; the weight tensors come
+ *    in and go out in the reference orientation (layer.rs:52-63).
+ */
+#ifndef RUSTANE_HIP_H
+#define RUSTANE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RH_OK 0
+#define RH_EINVAL -1     /* bad argument / unsupported shape            */
+#define RH_ERANGE -2     /* token id >= vocab, batch or length too big   */
+#define RH_ENOMEM -3     /* device allocation failed                     */
+#define RH_EDEVICE -4    /* HIP runtime error                            */
+#define RH_ESTATE -5     /* call out of order (e.g. decode before prefill) */
+
+/* ModelConfig (crates/engine/src/model.rs:5-17).  MHA only: kv_heads must
+ * equal heads (the reference reshapes K/V with `heads`, sdpa_fwd.rs:162-181).
+ * head_dim is 64 or 128; dim % 128 == 0; hidden % 128 == 0; vocab % 4 == 0. */
+typedef struct rh_config {
+    int32_t dim, hidden, heads, kv_heads, head_dim, seq, nlayers, vocab;
+    float rms_eps;   /* 1e-5  (cpu/rmsnorm.rs:10)                */
+    float rope_base; /* 1e4   (kernels/sdpa_fwd.rs:29)           */
+    float softcap;   /* 0=off (full_model.rs:75, :569-576)       */
+} rh_config;
+
+typedef struct rh_ctx rh_ctx;
+
+/* Replaces CompiledKernels::{compile, try_compile, compile_forward_only}
+ * (layer.rs:843-969) + KernelBuffers::allocate* (layer.rs:170-641): binds a
+ * device, creates the stream, allocates fp16 weights and the KV cache for
+ * max_batch sequences of up to max_ctx positions (max_ctx = 0: no cache).
+ * No JIT: kernels are precompiled for gfx950. */
+int rh_create(const rh_config* cfg, int device, int max_batch, int max_ctx, rh_ctx** out);
+void rh_destroy(rh_ctx* ctx);
+const char* rh_last_error(const rh_ctx* ctx);
+
+/* Uploads ModelWeights (full_model.rs:19-23) in the reference orientation,
+ * fp32 -> fp16 for matrices, fp32 for gammas; replaces the per-call weight
+ * staging of layer.rs:4670-4705 (done once here).  layer_tensors holds
+ * nlayers*9 pointers in RSTK order (bin/train.rs:238-345):
+ *   wq[D,D] wk[D,D] wv[D,D] wo[D,D] w1[D,F] w3[D,F] w2[D,F] gamma1[D] gamma2[D]
+ * (wq/wk/wv/wo/w1/w3 are in x out; w2 is out x in, used transposed). */
+int rh_load_weights_f32(rh_ctx* ctx, const float* embed, const float* gamma_final,
+                        const float* const* layer_tensors);
+
+/* Downloads the device weights back into the reference orientation
+ * (fp16 widened to fp32); same argument layout as rh_load_weights_f32, but
+ * writable.  Any pointer may be NULL to skip that tensor. */
+int rh_read_weights_f32(rh_ctx* ctx, float* embed, float* gamma_final,
+                        float* const* layer_tensors);
+
+/* Synthetic weights generated on the device: every matrix (embed, wq..w2)
+ * i.i.d. N(0, std^2) from Philox4x32-10 keyed by (seed, tensor id), gammas
+ * = 1.  No counterpart in the reference, whose init is ModelWeights::random
+ * (full_model.rs:132-141); it exists so multi-GB configs need no host copy. */
+int rh_init_weights_normal(rh_ctx* ctx, uint64_t seed, float std);
+
+/* full_model::forward / forward_only_ws / forward_losses
+ * (full_model.rs:378-472, 915-991, 1603-1660) for `batch` independent
+ * sequences of `seq` tokens (multistream.rs semantics, one launch).
+ * tokens/targets [batch*seq] (targets may be NULL if no loss is wanted).
+ *   logits_out       nullable [batch, seq, vocab] fp32 (post-softcap)
+ *   token_losses_out nullable [batch, seq]  (forward_losses)
+ *   mean_loss_out    nullable [batch]        (forward: total/seq)     */
+int rh_forward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
+               float* logits_out, float* token_losses_out, float* mean_loss_out);
+
+/* Same as rh_forward with every pointer in device memory, enqueued on the
+ * context stream without synchronising (no counterpart in the reference:
+ * it is the HBM-resident form a serving loop uses).  Token ids are clamped to
+ * the vocabulary on the device and counted; rh_sync reports RH_ERANGE if any
+ * were out of range. */
+int rh_forward_dev(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch,
+                   int seq, float* logits_out, float* token_losses_out, float* mean_loss_out);
+
+/* Fills the KV cache from `batch` prompts of `len` tokens (planned
+ * metal-decode path, crates/metal-decode/src/lib.rs:1-8) and sets the decode
+ * position to len.  next_tok_out (nullable [batch]) receives the argmax of
+ * the last position's logits, last_logits_out (nullable [batch, vocab]) the
+ * logits themselves.  batch <= min(max_batch, 16). */
+int rh_prefill(rh_ctx* ctx, const uint32_t* tokens, int batch, int len, uint32_t* next_tok_out,
+               float* last_logits_out);
+
+/* One greedy decode step for the batch set by rh_prefill: embeds in_tok
+ * [batch] at the current position, appends K/V, returns the argmax token
+ * (ties -> lowest id) in out_tok [batch] and optionally logits [batch, vocab].
+ * Contract: logits equal the forward's logits at that position. */
+int rh_decode_step(rh_ctx* ctx, const uint32_t* in_tok, uint32_t* out_tok, float* logits_out);
+
+/* nsteps greedy steps run entirely on the device (each step's argmax is the
+ * next step's input); out_tokens [nsteps, batch].  Starts from in_tok. */
+int rh_decode(rh_ctx* ctx, const uint32_t* in_tok, int nsteps, uint32_t* out_tokens);
+
+/* Logit softcap c for later calls (c * tanh(z / c), 0 = off); the reference
+ * passes it per forward call (full_model.rs:569-576). */
+int rh_set_softcap(rh_ctx* ctx, float softcap);
+
+/* Current decode position (tokens in the cache). */
+int rh_decode_pos(rh_ctx* ctx, int* pos_out);
+
+/* Waits for the context stream; returns the first deferred device error. */
+int rh_sync(rh_ctx* ctx);
+/* The context's hipStream_t, for callers that time or order work on it. */
+void* rh_stream(rh_ctx* ctx);
+
+/* Per-kernel-class timing with HIP events on the context stream: while
+ * enabled, every launch of `kernel_class` in the forward, prefill and decode calls is
+ * bracketed by an event pair; rh_profile_read returns the summed time and
+ * the launch count since rh_profile_enable.  Classes: */
+#define RH_K_GEMM_QKV 0
+#define RH_K_GEMM_WO 1
+#define RH_K_GEMM_W13 2
+#define RH_K_GEMM_W2 3
+#define RH_K_GEMM_LOGITS 4
+#define RH_K_ATTN 5
+#define RH_K_GEMV_QKV 6
+#define RH_K_GEMV_WO 7
+#define RH_K_GEMV_W13 8
+#define RH_K_GEMV_W2 9
+#define RH_K_GEMV_LOGITS 10
+#define RH_K_DECODE_ATTN 11
+#define RH_K_NCLASSES 12
+int rh_profile_enable(rh_ctx* ctx, int kernel_class, int enable);
+int rh_profile_read(rh_ctx* ctx, int kernel_class, double* total_ms, int64_t* launches);
+
+/* Decode steps as a captured HIP graph (1, default) or eager launches (0). */
+int rh_set_graphs(rh_ctx* ctx, int enable);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,172 @@
+"""ctypes binding of the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY.  This is the parity checker for the HIP path and
+the timed CPU baseline; only tests/, the smoke check and the benchmark's
+CPU-baseline leg import it.  The product package (rustane_amd) never does.
+
+The C restatement lives in oracle.cpp; each function there cites the
+reference file:line it follows.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+
+
+class OrcConfig(ctypes.Structure):
+    _fields_ = [
+        ("dim", ctypes.c_int32), ("hidden", ctypes.c_int32), ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("nlayers", ctypes.c_int32), ("vocab", ctypes.c_int32),
+        ("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float), ("softcap", ctypes.c_float),
+    ]
+
+
+class OrcWeights(ctypes.Structure):
+    _fields_ = [("embed", _f32p), ("gamma_final", _f32p), ("layers", ctypes.POINTER(_f32p))]
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the committed Makefile."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-C", HERE] + (["-B"] if force else []),
+                       check=True, stdout=subprocess.DEVNULL)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        sz = ctypes.c_size_t
+        L.orc_vsma.argtypes = [_f32p, ctypes.c_float, _f32p, _f32p, sz]
+        L.orc_vsub.argtypes = [_f32p, _f32p, _f32p, sz]
+        L.orc_mtrans.argtypes = [_f32p, sz, _f32p, sz, sz, sz]
+        L.orc_sgemm_at.argtypes = [_f32p, sz, sz, _f32p, sz, _f32p]
+        L.orc_random_vec.argtypes = [_f32p, sz, ctypes.c_float]
+        L.orc_embedding_forward.argtypes = [_f32p, sz, _u32p, sz, _f32p]
+        L.orc_rmsnorm_forward.argtypes = [_f32p, _f32p, _f32p, sz, ctypes.c_float]
+        L.orc_rmsnorm_forward.restype = ctypes.c_float
+        L.orc_rmsnorm_forward_channel_first.argtypes = [_f32p, _f32p, _f32p, _f32p, sz, sz,
+                                                        ctypes.c_float]
+        L.orc_silu_gate.argtypes = [_f32p, _f32p, _f32p, sz]
+        L.orc_cross_entropy_forward.argtypes = [_f32p, sz, ctypes.c_uint32, _f32p]
+        L.orc_cross_entropy_forward.restype = ctypes.c_float
+        L.orc_cross_entropy_forward_backward_batch.argtypes = [_f32p, _u32p, sz, sz, _f32p,
+                                                               ctypes.c_float]
+        L.orc_cross_entropy_forward_backward_batch.restype = ctypes.c_float
+        L.orc_rope_table.argtypes = [sz, sz, ctypes.c_float, _f32p, _f32p]
+        L.orc_sdpa_fwd.argtypes = [ctypes.POINTER(OrcConfig), sz, _f32p, _f32p, _f32p, _f32p,
+                                   _f32p, _f32p, _f32p, _f32p]
+        L.orc_layer_forward.argtypes = [ctypes.POINTER(OrcConfig), sz, ctypes.POINTER(_f32p),
+                                        _f32p, _f32p]
+        L.orc_forward.argtypes = [ctypes.POINTER(OrcConfig), ctypes.POINTER(OrcWeights), _u32p,
+                                  _u32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p, _f32p]
+        L.orc_forward.restype = ctypes.c_int
+        L.orc_kv_create.argtypes = [ctypes.POINTER(OrcConfig), ctypes.c_int]
+        L.orc_kv_create.restype = ctypes.c_void_p
+        L.orc_kv_destroy.argtypes = [ctypes.c_void_p]
+        L.orc_kv_pos.argtypes = [ctypes.c_void_p]
+        L.orc_prefill.argtypes = [ctypes.POINTER(OrcConfig), ctypes.POINTER(OrcWeights),
+                                  ctypes.c_void_p, _u32p, ctypes.c_int, _f32p]
+        L.orc_decode_step.argtypes = [ctypes.POINTER(OrcConfig), ctypes.POINTER(OrcWeights),
+                                      ctypes.c_void_p, ctypes.c_uint32, _f32p]
+        L.orc_num_threads.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def fp(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_f32p)
+
+
+def up(a: np.ndarray):
+    assert a.dtype == np.uint32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_u32p)
+
+
+def make_config(dim, hidden, heads, nlayers, vocab, head_dim=None, rms_eps=1e-5,
+                rope_base=1e4, softcap=0.0) -> OrcConfig:
+    hd = head_dim if head_dim is not None else dim // heads
+    return OrcConfig(dim, hidden, heads, hd, nlayers, vocab, rms_eps, rope_base, softcap)
+
+
+class Weights:
+    """Holds numpy fp32 arrays (reference orientation) and the ctypes view."""
+
+    def __init__(self, embed, gamma_final, layers):
+        self.embed = np.ascontiguousarray(embed, dtype=np.float32)
+        self.gamma_final = np.ascontiguousarray(gamma_final, dtype=np.float32)
+        self.layers = [[np.ascontiguousarray(t, dtype=np.float32) for t in lw] for lw in layers]
+        flat = [t for lw in self.layers for t in lw]
+        self._ptrs = (_f32p * len(flat))(*[fp(t) for t in flat])
+        self.c = OrcWeights(fp(self.embed), fp(self.gamma_final), self._ptrs)
+
+
+def forward(cfg: OrcConfig, w: Weights, tokens: np.ndarray, targets: np.ndarray | None,
+            want_logits: bool = True):
+    """Returns (logits [B,S,V] | None, token_losses [B,S] | None, mean_loss [B] | None)."""
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+    if tokens.ndim == 1:
+        tokens = tokens[None, :]
+    B, S = tokens.shape
+    logits = np.zeros((B, S, cfg.vocab), np.float32) if want_logits else None
+    tl = ml = None
+    tg = None
+    if targets is not None:
+        tg = np.ascontiguousarray(targets, dtype=np.uint32).reshape(B, S)
+        tl = np.zeros((B, S), np.float32)
+        ml = np.zeros((B,), np.float32)
+    rc = lib().orc_forward(ctypes.byref(cfg), ctypes.byref(w.c), up(tokens),
+                           up(tg) if tg is not None else None, B, S,
+                           fp(logits) if logits is not None else None,
+                           fp(tl) if tl is not None else None, fp(ml) if ml is not None else None)
+    if rc != 0:
+        raise ValueError(f"orc_forward failed: {rc}")
+    return logits, tl, ml
+
+
+class KV:
+    def __init__(self, cfg: OrcConfig, max_ctx: int):
+        self.cfg = cfg
+        self.h = lib().orc_kv_create(ctypes.byref(cfg), max_ctx)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_kv_destroy(self.h)
+            self.h = None
+
+    @property
+    def pos(self):
+        return lib().orc_kv_pos(self.h)
+
+    def prefill(self, w: Weights, tokens: np.ndarray) -> np.ndarray:
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        out = np.zeros(self.cfg.vocab, np.float32)
+        rc = lib().orc_prefill(ctypes.byref(self.cfg), ctypes.byref(w.c), self.h, up(tokens),
+                               len(tokens), fp(out))
+        if rc != 0:
+            raise ValueError(f"orc_prefill failed: {rc}")
+        return out
+
+    def step(self, w: Weights, token: int):
+        out = np.zeros(self.cfg.vocab, np.float32)
+        best = lib().orc_decode_step(ctypes.byref(self.cfg), ctypes.byref(w.c), self.h,
+                                     int(token), fp(out))
+        if best < 0:
+            raise ValueError(f"orc_decode_step failed: {best}")
+        return best, out

@@ -1,0 +1,127 @@
+/*
+ * oracle.h -- CPU fp32 restatement of rustane's transformer forward token loop.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * path (librustane_hip.so) and the timed CPU baseline.  Only the test suite,
+ * the smoke check and the benchmark's CPU-baseline leg load it.  The product
+ * path never links, loads or calls anything in this directory.
+ *
+ * Every function follows a file of the reference (whiskeypolitik/rustane,
+ * crates/engine/src/...), cited next to its declaration.  The reference keeps
+ * activations channel-first [D, S] (x[d*S + s]); the oracle does the same for
+ * the functions that mirror the reference's CPU ops, and uses token-major
+ * [S, *] internally where that only changes the loop order, not the
+ * arithmetic.
+ *
+ * vDSP / cblas calls in the reference (cpu/vdsp.rs) map to portable C++
+ * loops with the same contracts: vsma out = a*s + b, vsub out = b - a,
+ * sgemm_at C += A * B^T (beta = 1), mtrans.
+ *
+ * Parity pins (what checks each function; see tests/test_oracle_*.py):
+ *   orc_random_vec            bit-exact vs an independent numpy LCG; golden losses
+ *   orc_embedding_forward     reference KATs (cpu/embedding.rs:46-94)
+ *   orc_rmsnorm_*             reference KATs + closed form (cpu/rmsnorm.rs:244-369)
+ *   orc_silu_gate             reference KATs + closed form (cpu/silu.rs:48-109)
+ *   orc_cross_entropy_*       reference KATs, gradients sum to 0, numerical gradient
+ *                             (cpu/cross_entropy.rs:98-155), logsumexp via numpy
+ *   orc_vsma/vsub/mtrans/sgemm_at  reference KATs (cpu/vdsp.rs:404-483) + numpy matmul
+ *   orc_rope_table / orc_sdpa_fwd  textbook brute force in float64 on tiny shapes;
+ *                             p = 0 identity; norm preservation; causality
+ *   orc_forward (tail)        reference-held golden losses (results/forward_utilization/
+ *                             scale_ladder.json, results/2026-03-18_1830_param-sweep.md)
+ *   orc_forward (body)        layer = independent numpy float64 restatement on tiny shapes;
+ *                             FFN/attention branch linearity in Wo and W2
+ *   orc_decode_*              decode logits at position p == orc_forward logits at p
+ */
+#ifndef RUSTANE_ORACLE_H
+#define RUSTANE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ModelConfig (crates/engine/src/model.rs:5-17); MHA only (kv_heads == heads). */
+typedef struct {
+    int32_t dim, hidden, heads, head_dim, nlayers, vocab;
+    float rms_eps;   /* 1e-5, cpu/rmsnorm.rs:10 */
+    float rope_base; /* 1e4,  kernels/sdpa_fwd.rs:29 */
+    float softcap;   /* 0 = off, full_model.rs:75 */
+} orc_config;
+
+/* ModelWeights (full_model.rs:19-23) + LayerWeights (layer.rs:52-63), fp32 host
+ * arrays in the reference orientation.  layers[9*l + j], j in RSTK order:
+ *   0 wq [D, D] (in x out)   1 wk [D, D]   2 wv [D, D]   3 wo [D, D] (q_dim x D)
+ *   4 w1 [D, F]              5 w3 [D, F]   6 w2 [D, F] (out x in, used transposed)
+ *   7 gamma1 [D]             8 gamma2 [D]                                       */
+typedef struct {
+    const float* embed;       /* [V, D] */
+    const float* gamma_final; /* [D]    */
+    const float* const* layers;
+} orc_weights;
+
+/* ---- vDSP / cblas contracts (cpu/vdsp.rs:150-402) ---- */
+void orc_vsma(const float* a, float s, const float* b, float* out, size_t n);
+void orc_vsub(const float* a, const float* b, float* out, size_t n);
+void orc_mtrans(const float* a, size_t a_cols, float* c, size_t c_cols, size_t m, size_t n);
+void orc_sgemm_at(const float* a, size_t m, size_t k, const float* b, size_t n, float* c);
+
+/* ---- CPU ops ---- */
+void orc_random_vec(float* out, size_t n, float scale);
+void orc_embedding_forward(const float* table, size_t dim, const uint32_t* ids, size_t seq,
+                           float* out);
+float orc_rmsnorm_forward(const float* x, const float* gamma, float* out, size_t dim, float eps);
+void orc_rmsnorm_forward_channel_first(const float* x, const float* gamma, float* out,
+                                       float* rms_inv, size_t dim, size_t seq, float eps);
+void orc_silu_gate(const float* gate, const float* up, float* out, size_t n);
+float orc_cross_entropy_forward(const float* logits, size_t vocab, uint32_t target,
+                                float* log_sm /* nullable [vocab] */);
+float orc_cross_entropy_forward_backward_batch(const float* logits, const uint32_t* targets,
+                                               size_t seq, size_t vocab, float* dlogits,
+                                               float inv_seq);
+
+/* ---- attention (kernels/sdpa_fwd.rs) ---- */
+void orc_rope_table(size_t seq, size_t hd, float base, float* cos_buf, float* sin_buf);
+/* xnorm [D, S] channel-first; outputs [D, S] channel-first (q_rope, k_rope, v
+ * nullable). */
+void orc_sdpa_fwd(const orc_config* cfg, size_t seq, const float* xnorm, const float* wq,
+                  const float* wk, const float* wv, float* attn_out, float* q_rope,
+                  float* k_rope, float* v);
+
+/* ---- layer / model ---- */
+/* layer::forward (layer.rs:4409-4624): x [D, S] -> x_next [D, S]. */
+void orc_layer_forward(const orc_config* cfg, size_t seq, const float* const* lw,
+                       const float* x, float* x_next);
+/* full_model::forward / forward_losses (full_model.rs:915-991, 1603-1660) for
+ * `batch` independent sequences of length `seq` (the multistream model,
+ * multistream.rs:54-161).  Returns 0 on success.
+ *   logits_out        nullable [B, S, V]
+ *   token_losses_out  nullable [B, S]
+ *   mean_loss_out     nullable [B]   (total / S, cross_entropy.rs:58-96 + full_model.rs:987) */
+int orc_forward(const orc_config* cfg, const orc_weights* w, const uint32_t* tokens,
+                const uint32_t* targets, int batch, int seq, float* logits_out,
+                float* token_losses_out, float* mean_loss_out);
+
+/* ---- single-token decode with a KV cache (no reference implementation;
+ *      contract: logits at step p equal the forward's logits at position p) ---- */
+typedef struct orc_kv orc_kv;
+orc_kv* orc_kv_create(const orc_config* cfg, int max_ctx);
+void orc_kv_destroy(orc_kv* kv);
+int orc_kv_pos(const orc_kv* kv);
+/* Runs the prompt through the model, filling the cache; logits of the last
+ * prompt position into last_logits (nullable [V]). */
+int orc_prefill(const orc_config* cfg, const orc_weights* w, orc_kv* kv, const uint32_t* tokens,
+                int len, float* last_logits);
+/* One token at position kv->pos; logits_out [V]; returns argmax (ties -> lowest). */
+int orc_decode_step(const orc_config* cfg, const orc_weights* w, orc_kv* kv, uint32_t token,
+                    float* logits_out);
+
+/* Threads the oracle's OpenMP loops use. */
+int orc_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

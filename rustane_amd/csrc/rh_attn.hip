@@ -1,0 +1,293 @@
+// rh_attn.hip -- causal attention for the forward (prefill) and decode paths.
+//
+// Semantics follow the sdpaFwd graph (kernels/sdpa_fwd.rs:62-287): scores =
+// (q_rope . k_rope) * 1/sqrt(hd), keys after the query masked out (the
+// reference adds -65504, whose exp is exactly 0 after the row max is
+// subtracted), row softmax, P.V.  Q/K are RoPE'd by the QKV GEMM epilogue.
+//
+// Prefill: flash-style online softmax.  A block owns 64 queries of one
+// (sequence, head), 4 waves x 16 queries, and walks 64-key blocks up to the
+// causal limit with K and V^T resident in LDS.  The MFMAs compute the
+// transposed problem (S^T = K Q^T, O^T = V^T P^T) so that every lane owns one
+// query column throughout: the softmax row statistics, the rescaling of O and
+// the fp16 P operand all stay lane-local, and the row reductions are two
+// xor-shuffles over the 4 lane groups that share a query.
+//
+// Decode: split-context.  One block per (sequence, head, 256-position chunk)
+// scores its chunk with 16-byte K loads (hd/8 lanes per position), keeps
+// (max, sum, P.V) partials, and a combine kernel merges the chunks.  The
+// position is read from device memory so the step can be replayed as a graph.
+#include "rh_device.h"
+#include "rh_kernels.h"
+
+namespace rh {
+namespace {
+
+constexpr float LOG2E = 1.4426950408889634f;
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict__ Q,
+                                                           const f16* __restrict__ Kc,
+                                                           const f16* __restrict__ Vc,
+                                                           f16* __restrict__ out, int H, int S,
+                                                           int ctx, float scale_log2) {
+    constexpr int KB = 64;             // keys per block
+    constexpr int LDK = HD + 8;        // padded K row (halfs)
+    constexpr int LDV = KB + 8;        // padded V^T row (halfs)
+    constexpr int NKK = HD / 32;       // 32-wide k steps for Q.K
+    constexpr int NHT = HD / 16;       // 16-row hd tiles of O^T
+    __shared__ __attribute__((aligned(16))) f16 sK[KB * LDK];
+    __shared__ __attribute__((aligned(16))) f16 sVt[HD * LDV];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4;
+    const int nqt = (S + 63) / 64;
+    const int qt = nqt - 1 - (int)blockIdx.x;  // longest rows first
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int q0 = qt * 64;
+    const int qi = q0 + w * 16 + (lane & 15);  // this lane's query
+    const size_t bh = (size_t)b * H + h;
+    const f16* Kb = Kc + bh * ctx * HD;
+    const f16* Vb = Vc + bh * ctx * HD;
+
+    f16x8 qf[NKK];
+    {
+        const f16x8 z = {};
+        const f16* qp = Q + (bh * S + (qi < S ? qi : 0)) * HD + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) qf[kk] = qi < S ? *(const f16x8*)(qp + kk * 32) : z;
+    }
+    f32x4 o[NHT];
+#pragma unroll
+    for (int j = 0; j < NHT; ++j) o[j] = f32x4{};
+    float m_run = -INFINITY, l_run = 0.f;
+
+    const int kend = min(S, q0 + 64);
+    const int nkb = (kend + KB - 1) / KB;
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int k0 = kb * KB;
+        __syncthreads();
+        // K block -> sK[key][hd]
+#pragma unroll
+        for (int p = 0; p < KB * HD / 8 / 256; ++p) {
+            const int c = tid + 256 * p, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+            const int key = k0 + row;
+            f16x8 v = {};
+            if (key < S) v = *(const f16x8*)(Kb + (size_t)key * HD + col);
+            *(f16x8*)&sK[row * LDK + col] = v;
+        }
+        // V block -> sVt[hd][key], two keys per 32-bit LDS store
+#pragma unroll
+        for (int p = 0; p < (KB / 2) * (HD / 8) / 256; ++p) {
+            const int u = tid + 256 * p, kp = u & 31, col = (u >> 5) * 8;
+            const int key0 = k0 + 2 * kp;
+            f16x8 va = {}, vb = {};
+            if (key0 < S) va = *(const f16x8*)(Vb + (size_t)key0 * HD + col);
+            if (key0 + 1 < S) vb = *(const f16x8*)(Vb + (size_t)(key0 + 1) * HD + col);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+                *(f16x2*)&sVt[(col + e) * LDV + 2 * kp] = f16x2{va[e], vb[e]};
+            }
+        }
+        __syncthreads();
+
+        // S^T tiles: chunk c (32 keys) x half u; tile row r -> key
+        // 32c + 8(r/4) + 4u + r%4, so lane group g holds keys 32c + 8g + (0..7).
+        f32x4 sc[2][2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int r = lane & 15;
+                const int krow = 32 * c + 8 * (r >> 2) + 4 * u + (r & 3);
+                f32x4 acc = {};
+#pragma unroll
+                for (int kk = 0; kk < NKK; ++kk) {
+                    const f16x8 ka = *(const f16x8*)&sK[krow * LDK + kk * 32 + 8 * g];
+                    acc = mfma16(ka, qf[kk], acc);
+                }
+                sc[c][u] = acc;
+            }
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int key = k0 + 32 * c + 8 * g + 4 * u + i;
+                    float s = sc[c][u][i] * scale_log2;
+                    if (key > qi || key >= S) s = -INFINITY;
+                    sc[c][u][i] = s;
+                    mloc = fmaxf(mloc, s);
+                }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, RH_WAVE));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, RH_WAVE));
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = exp2f(m_run - m_new);
+        m_run = m_new;
+        float psum = 0.f;
+        f16x8 pf[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = exp2f(sc[c][u][i] - m_new);
+                    psum += p;
+                    pf[c][4 * u + i] = (f16)p;
+                }
+        l_run = l_run * alpha + psum;
+#pragma unroll
+        for (int j = 0; j < NHT; ++j) o[j] *= alpha;
+        // O^T[hd][q] += V^T[hd][keys] . P^T[keys][q]
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int j = 0; j < NHT; ++j) {
+                const f16x8 va = *(const f16x8*)&sVt[(16 * j + (lane & 15)) * LDV + 32 * c + 8 * g];
+                o[j] = mfma16(va, pf[c], o[j]);
+            }
+    }
+    float lt = l_run + __shfl_xor(l_run, 16, RH_WAVE);
+    lt += __shfl_xor(lt, 32, RH_WAVE);
+    if (qi < S) {
+        const float inv = 1.0f / lt;
+        f16* op = out + ((size_t)b * S + qi) * ((size_t)H * HD) + (size_t)h * HD + 4 * g;
+#pragma unroll
+        for (int j = 0; j < NHT; ++j)
+            *(f16x4*)(op + 16 * j) = f16x4{(f16)(o[j][0] * inv), (f16)(o[j][1] * inv),
+                                           (f16)(o[j][2] * inv), (f16)(o[j][3] * inv)};
+    }
+}
+
+constexpr int DCH = 256;  // decode positions per chunk
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict__ Q,
+                                                          const f16* __restrict__ Kc,
+                                                          const f16* __restrict__ Vc,
+                                                          const int* __restrict__ pos,
+                                                          float* part_m, float* part_l,
+                                                          float* part_o, int H, int ctx,
+                                                          float scale) {
+    constexpr int LPP = HD / 8;          // lanes per position
+    constexpr int NSLOT = 256 / LPP;     // positions scored concurrently per block
+    __shared__ float sS[DCH];
+    __shared__ float sO[NSLOT][HD + 4];
+    __shared__ float red[4];
+    const int tid = threadIdx.x, j = tid % LPP, slot = tid / LPP;
+    const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int nch = gridDim.x;
+    const int nctx = *pos + 1;
+    const int t0 = chunk * DCH, t1 = min(nctx, t0 + DCH);
+    const size_t bh = (size_t)b * H + h;
+    const size_t pidx = bh * nch + chunk;
+    if (t0 >= t1) {
+        if (tid == 0) { part_m[pidx] = -INFINITY; part_l[pidx] = 0.f; }
+        if (tid < HD) part_o[pidx * HD + tid] = 0.f;
+        return;
+    }
+    const f16x8 qv = *(const f16x8*)(Q + (size_t)b * H * HD + (size_t)h * HD + 8 * j);
+    const f16* Kb = Kc + bh * ctx * HD;
+    const f16* Vb = Vc + bh * ctx * HD;
+    for (int t = t0 + slot; t < t1; t += NSLOT) {
+        const f16x8 kv = *(const f16x8*)(Kb + (size_t)t * HD + 8 * j);
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d += (float)qv[e] * (float)kv[e];
+#pragma unroll
+        for (int o = LPP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, RH_WAVE);
+        if (j == 0) sS[t - t0] = d * scale;
+    }
+    __syncthreads();
+    const int n = t1 - t0;
+    float mx = -INFINITY;
+    for (int i = tid; i < n; i += 256) mx = fmaxf(mx, sS[i]);
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float ls = 0.f;
+    for (int i = tid; i < n; i += 256) {
+        const float p = __expf(sS[i] - mx);
+        sS[i] = p;
+        ls += p;
+    }
+    ls = block_sum_256(ls, red);  // includes a barrier: sS is complete after it
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int t = t0 + slot; t < t1; t += NSLOT) {
+        const float p = sS[t - t0];
+        const f16x8 vv = *(const f16x8*)(Vb + (size_t)t * HD + 8 * j);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += p * (float)vv[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sO[slot][8 * j + e] = acc[e];
+    __syncthreads();
+    if (tid < HD) {
+        float s = 0.f;
+        for (int k = 0; k < NSLOT; ++k) s += sO[k][tid];
+        part_o[pidx * HD + tid] = s;
+    }
+    if (tid == 0) { part_m[pidx] = mx; part_l[pidx] = ls; }
+}
+
+__global__ void attn_combine_kernel(const float* part_m, const float* part_l,
+                                    const float* part_o, f16* out, int H, int HD, int nch) {
+    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const size_t bh = (size_t)b * H + h;
+    float M = -INFINITY;
+    for (int c = 0; c < nch; ++c) M = fmaxf(M, part_m[bh * nch + c]);
+    float l = 0.f, o = 0.f;
+    for (int c = 0; c < nch; ++c) {
+        const float mc = part_m[bh * nch + c];
+        if (mc == -INFINITY) continue;
+        const float wgt = __expf(mc - M);
+        l += part_l[bh * nch + c] * wgt;
+        if (d < HD) o += part_o[(bh * nch + c) * HD + d] * wgt;
+    }
+    if (d < HD) out[bh * HD + d] = (f16)(o / l);
+}
+
+}  // namespace
+
+hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* out, int B, int H,
+                               int S, int hd, int ctx, hipStream_t st) {
+    const dim3 grid((S + 63) / 64, H, B);
+    const float sl2 = (1.0f / sqrtf((float)hd)) * LOG2E;
+    if (hd == 128)
+        hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(256), 0, st, q, k, v, out, H, S, ctx, sl2);
+    else if (hd == 64)
+        hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(256), 0, st, q, k, v, out, H, S, ctx, sl2);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+int attn_decode_chunks(int ctx) { return (ctx + DCH - 1) / DCH; }
+
+hipError_t launch_attn_decode(const f16* q, const f16* k, const f16* v, const int* pos,
+                              float* part_m, float* part_l, float* part_o, f16* out, int B, int H,
+                              int hd, int ctx, hipStream_t st) {
+    const int nch = attn_decode_chunks(ctx);
+    const dim3 grid(nch, H, B);
+    const float scale = 1.0f / sqrtf((float)hd);
+    if (hd == 128)
+        hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, st, q, k, v, pos, part_m,
+                           part_l, part_o, H, ctx, scale);
+    else if (hd == 64)
+        hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(256), 0, st, q, k, v, pos, part_m,
+                           part_l, part_o, H, ctx, scale);
+    else
+        return hipErrorInvalidValue;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(H, B), dim3(hd), 0, st, part_m, part_l, part_o,
+                       out, H, hd, nch);
+    return hipGetLastError();
+}
+
+}  // namespace rh

@@ -1,0 +1,56 @@
+// rh_device.h -- device types and helpers shared by the gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define RH_WAVE 64
+
+// 16x16x32 and 32x32x16 fp16 MFMA (gfx950).  For both, lane l holds 8
+// consecutive-k elements of row (l % M) of A and of column (l % N) of B, in k
+// group l / M; the output tile has column = l % N and rows
+//   16x16: 4*(l/16) + v            (v = 0..3)
+//   32x32: 8*(v/4) + 4*(l/32) + v%4 (v = 0..15).
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, RH_WAVE);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, RH_WAVE));
+    return v;
+}
+
+// Block-wide sum for blockDim.x == 256 (4 waves); every thread gets the result.
+__device__ __forceinline__ float block_sum_256(float v, float* red /* [4] shared */) {
+    v = wave_sum(v);
+    const int w = threadIdx.x / RH_WAVE, l = threadIdx.x % RH_WAVE;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// Blocks are dispatched round-robin over the 8 XCDs (block b -> XCD b % 8),
+// each with its own L2.  Remap so consecutive logical tiles land on the same
+// XCD: tiles that share a weight panel then hit the same L2.
+__device__ __forceinline__ int xcd_remap(int b, int total) {
+    const int q = total / 8, r = total % 8;
+    const int x = b % 8, k = b / 8;
+    return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + k;
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }

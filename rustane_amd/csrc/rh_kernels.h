@@ -1,0 +1,94 @@
+// rh_kernels.h -- host-side launchers for the gfx950 kernels (internal).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+typedef _Float16 f16;
+
+namespace rh {
+
+// ---------------- prefill GEMM:  Y[m][n] = sum_k X[m][k] * W[n][k] -------------
+enum GemmEpi { EPI_F32 = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
+
+struct GemmArgs {
+    const f16* W;  // [N, K] row-major (weights, "out x in")
+    const f16* X;  // [M, K] row-major (activations, token-major)
+    int M, N, K;
+    float* out_f32;  // EPI_F32: [M, ldo]; EPI_RESID: residual x [M, ldo], updated in place
+    f16* out_f16;    // EPI_SWIGLU: gate [M, ldo]
+    int ldo;
+    float alpha;     // EPI_RESID: x += alpha * acc
+    float softcap;   // EPI_F32: c * tanh(acc / c) when c > 0
+    // EPI_QKV: N = 3*D rows ordered q | k | v; RoPE on q and k.
+    f16* q;          // [B][H][S][hd]
+    f16* kc;         // [B][H][ctx][hd]
+    f16* vc;         // [B][H][ctx][hd]
+    const float2* rope;  // [pos][hd/2] (cos, sin)
+    int S, D, H, hd, ctx, pos0;
+};
+hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st);
+
+// ---------------- attention ----------------
+// Causal prefill attention: q [B][H][S][hd], k/v [B][H][ctx][hd] (positions
+// 0..S-1), out token-major [B*S][H*hd].
+hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* out, int B, int H,
+                               int S, int hd, int ctx, hipStream_t st);
+// Decode attention over positions 0..*pos (the current token is at *pos):
+// q [B][H*hd]; per (b, h, chunk) partial (m, l, o[hd]) then a combine.
+hipError_t launch_attn_decode(const f16* q, const f16* k, const f16* v, const int* pos,
+                              float* part_m, float* part_l, float* part_o, f16* out, int B, int H,
+                              int hd, int ctx, hipStream_t st);
+int attn_decode_chunks(int ctx);
+
+// ---------------- decode GEMV (B <= 16 tokens) ----------------
+enum GemvEpi { GV_F32 = 0, GV_RESID = 1, GV_SWIGLU = 2, GV_QKV = 3 };
+struct GemvArgs {
+    const f16* W;  // [N, K]
+    const f16* X;  // [B, K]
+    int B, N, K;
+    float* out_f32;  // GV_F32 [B, ldo], GV_RESID x [B, ldo]
+    f16* out_f16;    // GV_SWIGLU gate [B, ldo]; GV_QKV q [B, D]
+    int ldo;
+    float alpha, softcap;
+    f16* kc; f16* vc;  // GV_QKV: [B][H][ctx][hd]
+    const float2* rope;
+    const int* pos;    // device position
+    int D, H, hd, ctx;
+};
+hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t st);
+
+// ---------------- row ops ----------------
+hipError_t launch_embed(const uint32_t* tok, const f16* E, float* x, int rows, int D, int V,
+                        int* err, hipStream_t st);
+hipError_t launch_rmsnorm(const float* x, const float* gamma, f16* out, int rows, int D,
+                          float eps, hipStream_t st);
+// rmsnorm of rows x[(r*stride + offset)] -> out[r]  (last-position gather)
+hipError_t launch_rmsnorm_strided(const float* x, const float* gamma, f16* out, int rows, int D,
+                                  float eps, int stride_rows, int offset_rows, hipStream_t st);
+hipError_t launch_cross_entropy(const float* logits, const uint32_t* targets, float* loss,
+                                int rows, int V, int* err, hipStream_t st);
+hipError_t launch_mean_rows(const float* loss, float* mean, int B, int S, hipStream_t st);
+// argmax over [B][V]; writes out[b], next_in[b] and seq_out[step*B + b]
+// (step from state[1]); ties -> lowest index.
+hipError_t launch_argmax(const float* logits, int B, int V, uint32_t* out, uint32_t* next_in,
+                         uint32_t* seq_out, const int* state, hipStream_t st);
+// state[0] += 1 (position), state[1] += 1 (step)
+hipError_t launch_advance(int* state, hipStream_t st);
+hipError_t launch_set_state(int* state, int pos, int step, hipStream_t st);
+hipError_t launch_fill_f32(float* p, float v, size_t n, hipStream_t st);
+
+// ---------------- weight packing ----------------
+// dst[(row_map(c))*ldd + r] = half(src[r*C + c]) for a [R][C] fp32 source.
+// map: 0 identity rows (dst row = row_off + c), 1 = W1/W3 interleave
+// (dst row = 64*(c/32) + c%32 + row_off).
+hipError_t launch_pack_transpose(const float* src, f16* dst, int R, int C, int ldd, int map,
+                                 int row_off, hipStream_t st);
+hipError_t launch_unpack_transpose(const f16* src, float* dst, int R, int C, int lds, int map,
+                                   int row_off, hipStream_t st);
+hipError_t launch_convert_f32_f16(const float* src, f16* dst, size_t n, hipStream_t st);
+hipError_t launch_convert_f16_f32(const f16* src, float* dst, size_t n, hipStream_t st);
+hipError_t launch_init_normal(float* dst, size_t n, uint64_t seed, uint32_t tensor_id, float std,
+                              hipStream_t st);
+
+}  // namespace rh

@@ -1,0 +1,294 @@
+// rh_rowops.hip -- bandwidth-bound row kernels of the forward and decode paths
+// and the weight packing kernels.
+//
+//   embed      embedding::forward (cpu/embedding.rs:8-16), fp16 table -> fp32 rows
+//   rmsnorm    rmsnorm::forward_channel_first (cpu/rmsnorm.rs:149-183):
+//              r = 1/sqrt(sum(x^2) * (1/D) + eps), out = (x * r) * gamma  -> fp16
+//   ce         cross_entropy::forward_backward_batch (cpu/cross_entropy.rs:58-96),
+//              loss only: ln(sum exp(l - max)) - (l[t] - max), one block per row
+//   mean       total / S per sequence (full_model.rs:987)
+//   argmax     greedy token, ties -> lowest id
+//   pack/unpack  reference orientation (layer.rs:52-63) <-> device [out, in] fp16
+#include "rh_device.h"
+#include "rh_kernels.h"
+
+namespace rh {
+namespace {
+
+__global__ void embed_kernel(const uint32_t* tok, const f16* E, float* x, int D, int V, int* err) {
+    const int row = blockIdx.x;
+    uint32_t t = tok[row];
+    if (t >= (uint32_t)V) {
+        if (threadIdx.x == 0) atomicAdd(err, 1);
+        t = 0;
+    }
+    const f16* src = E + (size_t)t * D;
+    float* dst = x + (size_t)row * D;
+    for (int i = threadIdx.x * 4; i < D; i += blockDim.x * 4) {
+        const f16x4 v = *(const f16x4*)(src + i);
+        *(f32x4*)(dst + i) = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+    }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const float* gamma, f16* out,
+                                                      int D, float eps, int stride_rows,
+                                                      int offset_rows) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    const float* xr = x + ((size_t)row * stride_rows + offset_rows) * D;
+    float ss = 0.f;
+    for (int i = threadIdx.x * 4; i < D; i += 1024) {
+        const f32x4 v = *(const f32x4*)(xr + i);
+        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    }
+    ss = block_sum_256(ss, red);
+    const float r = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
+    f16* o = out + (size_t)row * D;
+    for (int i = threadIdx.x * 4; i < D; i += 1024) {
+        const f32x4 v = *(const f32x4*)(xr + i);
+        const f32x4 gm = *(const f32x4*)(gamma + i);
+        *(f16x4*)(o + i) = f16x4{(f16)(v[0] * r * gm[0]), (f16)(v[1] * r * gm[1]),
+                                 (f16)(v[2] * r * gm[2]), (f16)(v[3] * r * gm[3])};
+    }
+}
+
+__global__ __launch_bounds__(256) void ce_kernel(const float* logits, const uint32_t* targets,
+                                                 float* loss, int V, int* err) {
+    __shared__ float sm[4], ss[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float* l = logits + (size_t)row * V;
+    float m = -INFINITY, s = 0.f;
+    for (int i = tid * 4; i < V; i += 1024) {
+        const f32x4 v = *(const f32x4*)(l + i);
+        const float vm = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+        if (vm > m) { s *= __expf(m - vm); m = vm; }
+        s += __expf(v[0] - m) + __expf(v[1] - m) + __expf(v[2] - m) + __expf(v[3] - m);
+    }
+    // combine (m, s) across the wave, then across the 4 waves
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float om = __shfl_xor(m, o, RH_WAVE), os = __shfl_xor(s, o, RH_WAVE);
+        const float nm = fmaxf(m, om);
+        s = (m == -INFINITY ? 0.f : s * __expf(m - nm)) + (om == -INFINITY ? 0.f : os * __expf(om - nm));
+        m = nm;
+    }
+    if ((tid & 63) == 0) { sm[tid >> 6] = m; ss[tid >> 6] = s; }
+    __syncthreads();
+    if (tid == 0) {
+        float M = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+        float S = 0.f;
+        for (int w = 0; w < 4; ++w) S += ss[w] * __expf(sm[w] - M);
+        uint32_t t = targets[row];
+        if (t >= (uint32_t)V) { atomicAdd(err, 1); t = 0; }
+        loss[row] = logf(S) - (l[t] - M);
+    }
+}
+
+__global__ __launch_bounds__(256) void mean_kernel(const float* loss, float* mean, int S) {
+    __shared__ float red[4];
+    const int b = blockIdx.x;
+    float s = 0.f;
+    for (int i = threadIdx.x; i < S; i += 256) s += loss[(size_t)b * S + i];
+    s = block_sum_256(s, red);
+    if (threadIdx.x == 0) mean[b] = s / (float)S;
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int V, uint32_t* out,
+                                                     uint32_t* next_in, uint32_t* seq_out,
+                                                     const int* state, int B) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const float* l = logits + (size_t)b * V;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = tid; i < V; i += 256) {
+        const float v = l[i];
+        if (v > bv) { bv = v; bi = i; }  // strided scan: first hit is the lowest index
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, RH_WAVE);
+        const int oi = __shfl_xor(bi, o, RH_WAVE);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if ((tid & 63) == 0) { sv[tid >> 6] = bv; si[tid >> 6] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
+        if (bi >= V) bi = 0;
+        out[b] = (uint32_t)bi;
+        if (next_in) next_in[b] = (uint32_t)bi;
+        if (seq_out) seq_out[(size_t)state[1] * B + b] = (uint32_t)bi;
+    }
+}
+
+__global__ void advance_kernel(int* state) {
+    if (threadIdx.x == 0) { state[0] += 1; state[1] += 1; }
+}
+__global__ void set_state_kernel(int* state, int pos, int step) {
+    if (threadIdx.x == 0) { state[0] = pos; state[1] = step; }
+}
+__global__ void fill_kernel(float* p, float v, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+__device__ __forceinline__ int dst_row(int c, int map, int row_off) {
+    return map == 1 ? 64 * (c >> 5) + (c & 31) + row_off : c + row_off;
+}
+
+// 32x32 tiles through LDS: reads rows of src, writes rows of dst.
+__global__ void pack_transpose_kernel(const float* src, f16* dst, int R, int C, int ldd, int map,
+                                      int row_off) {
+    __shared__ float tile[32][33];
+    const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: 8 rows per pass
+    for (int y = ty; y < 32; y += 8) {
+        const int r = r0 + y, c = c0 + tx;
+        tile[y][tx] = (r < R && c < C) ? src[(size_t)r * C + c] : 0.f;
+    }
+    __syncthreads();
+    for (int y = ty; y < 32; y += 8) {
+        const int c = c0 + y, r = r0 + tx;
+        if (c < C && r < R) dst[(size_t)dst_row(c, map, row_off) * ldd + r] = (f16)tile[tx][y];
+    }
+}
+
+__global__ void unpack_transpose_kernel(const f16* src, float* dst, int R, int C, int lds, int map,
+                                        int row_off) {
+    __shared__ float tile[32][33];
+    const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int y = ty; y < 32; y += 8) {
+        const int c = c0 + y, r = r0 + tx;
+        tile[y][tx] = (c < C && r < R) ? (float)src[(size_t)dst_row(c, map, row_off) * lds + r] : 0.f;
+    }
+    __syncthreads();
+    for (int y = ty; y < 32; y += 8) {
+        const int r = r0 + y, c = c0 + tx;
+        if (r < R && c < C) dst[(size_t)r * C + c] = tile[tx][y];
+    }
+}
+
+__global__ void convert_f32_f16_kernel(const float* s, f16* d, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        d[i] = (f16)s[i];
+}
+__global__ void convert_f16_f32_kernel(const f16* s, float* d, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        d[i] = (float)s[i];
+}
+
+// Philox4x32-10 (Salmon et al., SC'11) with the published round constants.
+__device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1) {
+    const uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        const uint32_t hi0 = __umulhi(M0, c[0]), lo0 = M0 * c[0];
+        const uint32_t hi1 = __umulhi(M1, c[2]), lo1 = M1 * c[2];
+        const uint32_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+        c[0] = n0; c[1] = lo1; c[2] = n2; c[3] = lo0;
+        k0 += W0; k1 += W1;
+    }
+}
+
+// Element i of tensor `tid`: counter (i/4 pairs..) -> Box-Muller normals.
+__global__ void init_normal_kernel(float* dst, size_t n, uint32_t seed_lo, uint32_t seed_hi,
+                                   uint32_t tensor_id, float std) {
+    const size_t npair = (n + 1) / 2;
+    for (size_t p = blockIdx.x * (size_t)blockDim.x + threadIdx.x; p < npair;
+         p += (size_t)gridDim.x * blockDim.x) {
+        uint32_t c[4] = {(uint32_t)p, (uint32_t)(p >> 32), tensor_id, 0x52485354u};
+        philox4x32_10(c, seed_lo, seed_hi);
+        const float u1 = ((float)(c[0] >> 8) + 1.0f) * (1.0f / 16777216.0f);  // (0, 1]
+        const float u2 = (float)(c[1] >> 8) * (1.0f / 16777216.0f);           // [0, 1)
+        const float rad = sqrtf(-2.0f * logf(u1));
+        const float th = 6.283185307179586f * u2;
+        const size_t i = 2 * p;
+        dst[i] = std * rad * cosf(th);
+        if (i + 1 < n) dst[i + 1] = std * rad * sinf(th);
+    }
+}
+
+inline int grid_for(size_t n, int per_block) {
+    size_t g = (n + per_block - 1) / per_block;
+    if (g > 65536) g = 65536;
+    if (g < 1) g = 1;
+    return (int)g;
+}
+
+}  // namespace
+
+hipError_t launch_embed(const uint32_t* tok, const f16* E, float* x, int rows, int D, int V,
+                        int* err, hipStream_t st) {
+    hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(256), 0, st, tok, E, x, D, V, err);
+    return hipGetLastError();
+}
+hipError_t launch_rmsnorm(const float* x, const float* gamma, f16* out, int rows, int D, float eps,
+                          hipStream_t st) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps, 1, 0);
+    return hipGetLastError();
+}
+hipError_t launch_rmsnorm_strided(const float* x, const float* gamma, f16* out, int rows, int D,
+                                  float eps, int stride_rows, int offset_rows, hipStream_t st) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps,
+                       stride_rows, offset_rows);
+    return hipGetLastError();
+}
+hipError_t launch_cross_entropy(const float* logits, const uint32_t* targets, float* loss, int rows,
+                                int V, int* err, hipStream_t st) {
+    hipLaunchKernelGGL(ce_kernel, dim3(rows), dim3(256), 0, st, logits, targets, loss, V, err);
+    return hipGetLastError();
+}
+hipError_t launch_mean_rows(const float* loss, float* mean, int B, int S, hipStream_t st) {
+    hipLaunchKernelGGL(mean_kernel, dim3(B), dim3(256), 0, st, loss, mean, S);
+    return hipGetLastError();
+}
+hipError_t launch_argmax(const float* logits, int B, int V, uint32_t* out, uint32_t* next_in,
+                         uint32_t* seq_out, const int* state, hipStream_t st) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(256), 0, st, logits, V, out, next_in, seq_out,
+                       state, B);
+    return hipGetLastError();
+}
+hipError_t launch_advance(int* state, hipStream_t st) {
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, st, state);
+    return hipGetLastError();
+}
+hipError_t launch_set_state(int* state, int pos, int step, hipStream_t st) {
+    hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(64), 0, st, state, pos, step);
+    return hipGetLastError();
+}
+hipError_t launch_fill_f32(float* p, float v, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, p, v, n);
+    return hipGetLastError();
+}
+hipError_t launch_pack_transpose(const float* src, f16* dst, int R, int C, int ldd, int map,
+                                 int row_off, hipStream_t st) {
+    const dim3 grid((C + 31) / 32, (R + 31) / 32);
+    hipLaunchKernelGGL(pack_transpose_kernel, grid, dim3(256), 0, st, src, dst, R, C, ldd, map, row_off);
+    return hipGetLastError();
+}
+hipError_t launch_unpack_transpose(const f16* src, float* dst, int R, int C, int lds, int map,
+                                   int row_off, hipStream_t st) {
+    const dim3 grid((C + 31) / 32, (R + 31) / 32);
+    hipLaunchKernelGGL(unpack_transpose_kernel, grid, dim3(256), 0, st, src, dst, R, C, lds, map, row_off);
+    return hipGetLastError();
+}
+hipError_t launch_convert_f32_f16(const float* src, f16* dst, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(convert_f32_f16_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, src, dst, n);
+    return hipGetLastError();
+}
+hipError_t launch_convert_f16_f32(const f16* src, float* dst, size_t n, hipStream_t st) {
+    hipLaunchKernelGGL(convert_f16_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, st, src, dst, n);
+    return hipGetLastError();
+}
+hipError_t launch_init_normal(float* dst, size_t n, uint64_t seed, uint32_t tensor_id, float std,
+                              hipStream_t st) {
+    hipLaunchKernelGGL(init_normal_kernel, dim3(grid_for((n + 1) / 2, 256)), dim3(256), 0, st, dst, n,
+                       (uint32_t)seed, (uint32_t)(seed >> 32), tensor_id, std);
+    return hipGetLastError();
+}
+
+}  // namespace rh

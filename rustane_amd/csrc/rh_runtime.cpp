@@ -1,0 +1,748 @@
+// rh_runtime.cpp -- host runtime behind include/rustane_hip.h.
+//
+// Owns the device, one HIP stream, the fp16 weights (repacked once at upload
+// to the [out, in] layout the kernels stream), the KV cache and the
+// workspaces, and sequences the kernels of the forward token loop:
+//
+//   embed -> L x [rmsnorm -> QKV GEMM (+RoPE, K/V store) -> causal attention
+//                 -> Wo GEMM (+x += a*o) -> rmsnorm -> W1|W3 GEMM (+SwiGLU)
+//                 -> W2 GEMM (+x += a*f)] -> rmsnorm -> tied logits GEMM
+//   -> cross-entropy rows -> per-sequence mean
+//
+// which is layer::forward (layer.rs:4409-4624) and full_model::forward
+// (full_model.rs:915-991) with a = 1/sqrt(2L) (layer.rs:4640).  The decode
+// step runs the same chain on B <= 16 tokens with GEMV kernels and a KV cache,
+// and is replayed as a captured HIP graph.
+#include "../../include/rustane_hip.h"
+#include "rh_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+namespace {
+
+struct Layer {
+    f16 *wqkv = nullptr, *wo = nullptr, *w13 = nullptr, *w2 = nullptr;
+    float *g1 = nullptr, *g2 = nullptr;
+};
+
+struct Prof {
+    bool on = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
+    double ms = 0;
+    int64_t n = 0;
+};
+
+}  // namespace
+
+struct rh_ctx {
+    rh_config cfg{};
+    int device = 0, max_batch = 0, max_ctx = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    std::vector<void*> allocs;
+
+    f16* embed = nullptr;
+    float* gfinal = nullptr;
+    std::vector<Layer> L;
+    float2* rope = nullptr;
+    int rope_len = 0;
+
+    // forward / prefill workspace (grow-only, sized for M = B*S rows)
+    int ws_M = 0;
+    float *x = nullptr, *logits = nullptr, *tok_loss = nullptr, *mean = nullptr;
+    f16 *xn = nullptr, *q = nullptr, *kbuf = nullptr, *vbuf = nullptr, *attn = nullptr, *gate = nullptr;
+    uint32_t *d_tok = nullptr, *d_tgt = nullptr;
+    size_t logits_rows = 0;
+    int* d_err = nullptr;
+
+    // KV cache [L][max_batch][H][max_ctx][hd]
+    f16 *kcache = nullptr, *vcache = nullptr;
+    size_t kv_layer = 0;
+
+    // decode (B <= 16)
+    float *dx = nullptr, *dlogits = nullptr, *pm = nullptr, *pl = nullptr, *po = nullptr;
+    f16 *dxn = nullptr, *dq = nullptr, *dattn = nullptr, *dgate = nullptr;
+    int* dstate = nullptr;
+    uint32_t *dtok = nullptr, *dout = nullptr, *dseq = nullptr;
+    int dec_B = 0, host_pos = 0;
+    bool have_prefill = false;
+    bool use_graphs = true;
+    hipGraphExec_t dgraph = nullptr;
+    int dgraph_B = 0;
+    bool capturing = false;
+
+    float* staging = nullptr;
+    size_t staging_elems = 0;
+
+    Prof prof[RH_K_NCLASSES];
+};
+
+namespace {
+
+int fail(rh_ctx* c, int code, const std::string& m) {
+    if (c) c->err = m;
+    return code;
+}
+
+#define HCK(expr)                                                                     \
+    do {                                                                              \
+        hipError_t e_ = (expr);                                                       \
+        if (e_ != hipSuccess)                                                         \
+            return fail(ctx, RH_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+template <typename T>
+int dalloc(rh_ctx* ctx, T** p, size_t elems) {
+    void* q = nullptr;
+    if (elems == 0) elems = 1;
+    if (hipMalloc(&q, elems * sizeof(T)) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(ctx, RH_ENOMEM, "hipMalloc of " + std::to_string(elems * sizeof(T)) + " bytes failed");
+    }
+    ctx->allocs.push_back(q);
+    *p = (T*)q;
+    return RH_OK;
+}
+
+void dfree(rh_ctx* ctx, void* p) {
+    if (!p) return;
+    auto it = std::find(ctx->allocs.begin(), ctx->allocs.end(), p);
+    if (it != ctx->allocs.end()) ctx->allocs.erase(it);
+    (void)hipFree(p);
+}
+
+#define RCK(expr)                   \
+    do {                            \
+        int r_ = (expr);            \
+        if (r_ != RH_OK) return r_; \
+    } while (0)
+
+size_t D_(const rh_ctx* c) { return (size_t)c->cfg.dim; }
+size_t F_(const rh_ctx* c) { return (size_t)c->cfg.hidden; }
+size_t V_(const rh_ctx* c) { return (size_t)c->cfg.vocab; }
+
+// RoPE table, theta = p / base^(2i/hd) in fp32 (kernels/sdpa_fwd.rs:24-39).
+int ensure_rope(rh_ctx* ctx, int npos) {
+    if (npos <= ctx->rope_len) return RH_OK;
+    const int hd = ctx->cfg.head_dim;
+    std::vector<float2> t((size_t)npos * (hd / 2));
+    for (int p = 0; p < npos; ++p)
+        for (int i = 0; i < hd / 2; ++i) {
+            const float th = (float)p / std::pow(ctx->cfg.rope_base, 2.0f * (float)i / (float)hd);
+            t[(size_t)p * (hd / 2) + i] = make_float2(std::cos(th), std::sin(th));
+        }
+    HCK(hipStreamSynchronize(ctx->stream));
+    dfree(ctx, ctx->rope);
+    ctx->rope = nullptr;
+    RCK(dalloc(ctx, &ctx->rope, t.size()));
+    HCK(hipMemcpy(ctx->rope, t.data(), t.size() * sizeof(float2), hipMemcpyHostToDevice));
+    ctx->rope_len = npos;
+    return RH_OK;
+}
+
+int ensure_workspace(rh_ctx* ctx, int M) {
+    if (M <= ctx->ws_M) return RH_OK;
+    HCK(hipStreamSynchronize(ctx->stream));
+    void* olds[] = {ctx->x, ctx->xn, ctx->q, ctx->kbuf, ctx->vbuf, ctx->attn, ctx->gate,
+                    ctx->logits, ctx->tok_loss, ctx->mean, ctx->d_tok, ctx->d_tgt};
+    for (void* p : olds) dfree(ctx, p);
+    const size_t D = D_(ctx), F = F_(ctx), V = V_(ctx), m = (size_t)M;
+    RCK(dalloc(ctx, &ctx->x, m * D));
+    RCK(dalloc(ctx, &ctx->xn, m * D));
+    RCK(dalloc(ctx, &ctx->q, m * D));
+    RCK(dalloc(ctx, &ctx->kbuf, m * D));
+    RCK(dalloc(ctx, &ctx->vbuf, m * D));
+    RCK(dalloc(ctx, &ctx->attn, m * D));
+    RCK(dalloc(ctx, &ctx->gate, m * F));
+    RCK(dalloc(ctx, &ctx->logits, m * V));
+    RCK(dalloc(ctx, &ctx->tok_loss, m));
+    RCK(dalloc(ctx, &ctx->mean, m));
+    RCK(dalloc(ctx, &ctx->d_tok, m));
+    RCK(dalloc(ctx, &ctx->d_tgt, m));
+    ctx->ws_M = M;
+    return RH_OK;
+}
+
+int ensure_staging(rh_ctx* ctx, size_t elems) {
+    if (elems <= ctx->staging_elems) return RH_OK;
+    HCK(hipStreamSynchronize(ctx->stream));
+    dfree(ctx, ctx->staging);
+    ctx->staging = nullptr;
+    RCK(dalloc(ctx, &ctx->staging, elems));
+    ctx->staging_elems = elems;
+    return RH_OK;
+}
+
+// ---- timed launches -------------------------------------------------------
+template <typename Fn>
+int timed(rh_ctx* ctx, int cls, Fn&& fn) {
+    Prof& p = ctx->prof[cls];
+    const bool on = p.on && !ctx->capturing;
+    hipEvent_t a = nullptr, b = nullptr;
+    if (on) {
+        HCK(hipEventCreate(&a));
+        HCK(hipEventCreate(&b));
+        HCK(hipEventRecord(a, ctx->stream));
+    }
+    hipError_t e = fn();
+    if (e != hipSuccess) return fail(ctx, RH_EDEVICE, std::string("kernel launch: ") + hipGetErrorString(e));
+    if (on) {
+        HCK(hipEventRecord(b, ctx->stream));
+        p.ev.emplace_back(a, b);
+    }
+    return RH_OK;
+}
+
+#define LCK(expr)                                                                              \
+    do {                                                                                       \
+        hipError_t e_ = (expr);                                                                \
+        if (e_ != hipSuccess)                                                                  \
+            return fail(ctx, RH_EDEVICE, std::string("launch ") + #expr + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+// ---- the forward token loop -----------------------------------------------
+// kv_k/kv_v: per-layer K/V destination base and ctx stride.  For a plain
+// forward they are the scratch buffers (ctx = S); for a prefill they are the
+// cache layers (ctx = max_ctx).
+int enqueue_body(rh_ctx* ctx, int B, int S, bool to_cache) {
+    const rh_config& c = ctx->cfg;
+    const int M = B * S, D = c.dim, F = c.hidden;
+    const float alpha = 1.0f / std::sqrt(2.0f * (float)c.nlayers);
+    hipStream_t st = ctx->stream;
+    LCK(rh::launch_embed(ctx->d_tok, ctx->embed, ctx->x, M, D, c.vocab, ctx->d_err, st));
+    for (int l = 0; l < c.nlayers; ++l) {
+        const Layer& W = ctx->L[l];
+        f16* kc = to_cache ? ctx->kcache + (size_t)l * ctx->kv_layer : ctx->kbuf;
+        f16* vc = to_cache ? ctx->vcache + (size_t)l * ctx->kv_layer : ctx->vbuf;
+        const int kvctx = to_cache ? ctx->max_ctx : S;
+        LCK(rh::launch_rmsnorm(ctx->x, W.g1, ctx->xn, M, D, c.rms_eps, st));
+        rh::GemmArgs g{};
+        g.W = W.wqkv; g.X = ctx->xn; g.M = M; g.N = 3 * D; g.K = D;
+        g.q = ctx->q; g.kc = kc; g.vc = vc; g.rope = ctx->rope;
+        g.S = S; g.D = D; g.H = c.heads; g.hd = c.head_dim; g.ctx = kvctx; g.pos0 = 0;
+        RCK(timed(ctx, RH_K_GEMM_QKV, [&] { return rh::launch_gemm(rh::EPI_QKV, g, st); }));
+        RCK(timed(ctx, RH_K_ATTN, [&] {
+            return rh::launch_attn_prefill(ctx->q, kc, vc, ctx->attn, B, c.heads, S, c.head_dim, kvctx, st);
+        }));
+        g = rh::GemmArgs{};
+        g.W = W.wo; g.X = ctx->attn; g.M = M; g.N = D; g.K = D;
+        g.out_f32 = ctx->x; g.ldo = D; g.alpha = alpha;
+        RCK(timed(ctx, RH_K_GEMM_WO, [&] { return rh::launch_gemm(rh::EPI_RESID, g, st); }));
+        LCK(rh::launch_rmsnorm(ctx->x, W.g2, ctx->xn, M, D, c.rms_eps, st));
+        g = rh::GemmArgs{};
+        g.W = W.w13; g.X = ctx->xn; g.M = M; g.N = 2 * F; g.K = D;
+        g.out_f16 = ctx->gate; g.ldo = F;
+        RCK(timed(ctx, RH_K_GEMM_W13, [&] { return rh::launch_gemm(rh::EPI_SWIGLU, g, st); }));
+        g = rh::GemmArgs{};
+        g.W = W.w2; g.X = ctx->gate; g.M = M; g.N = D; g.K = F;
+        g.out_f32 = ctx->x; g.ldo = D; g.alpha = alpha;
+        RCK(timed(ctx, RH_K_GEMM_W2, [&] { return rh::launch_gemm(rh::EPI_RESID, g, st); }));
+    }
+    return RH_OK;
+}
+
+int enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss) {
+    const rh_config& c = ctx->cfg;
+    const int M = B * S, D = c.dim;
+    hipStream_t st = ctx->stream;
+    LCK(rh::launch_rmsnorm(ctx->x, ctx->gfinal, ctx->xn, M, D, c.rms_eps, st));
+    rh::GemmArgs g{};
+    g.W = ctx->embed; g.X = ctx->xn; g.M = M; g.N = c.vocab; g.K = D;
+    g.out_f32 = ctx->logits; g.ldo = c.vocab; g.softcap = c.softcap;
+    RCK(timed(ctx, RH_K_GEMM_LOGITS, [&] { return rh::launch_gemm(rh::EPI_F32, g, st); }));
+    if (with_loss) {
+        LCK(rh::launch_cross_entropy(ctx->logits, ctx->d_tgt, ctx->tok_loss, M, c.vocab, ctx->d_err, st));
+        LCK(rh::launch_mean_rows(ctx->tok_loss, ctx->mean, B, S, st));
+    }
+    return RH_OK;
+}
+
+// One decode step for B tokens at position dstate[0].
+int enqueue_decode_step(rh_ctx* ctx, int B) {
+    const rh_config& c = ctx->cfg;
+    const int D = c.dim, F = c.hidden;
+    const float alpha = 1.0f / std::sqrt(2.0f * (float)c.nlayers);
+    hipStream_t st = ctx->stream;
+    LCK(rh::launch_embed(ctx->dtok, ctx->embed, ctx->dx, B, D, c.vocab, ctx->d_err, st));
+    for (int l = 0; l < c.nlayers; ++l) {
+        const Layer& W = ctx->L[l];
+        f16* kc = ctx->kcache + (size_t)l * ctx->kv_layer;
+        f16* vc = ctx->vcache + (size_t)l * ctx->kv_layer;
+        LCK(rh::launch_rmsnorm(ctx->dx, W.g1, ctx->dxn, B, D, c.rms_eps, st));
+        rh::GemvArgs g{};
+        g.W = W.wqkv; g.X = ctx->dxn; g.B = B; g.N = 3 * D; g.K = D;
+        g.out_f16 = ctx->dq; g.kc = kc; g.vc = vc; g.rope = ctx->rope; g.pos = ctx->dstate;
+        g.D = D; g.H = c.heads; g.hd = c.head_dim; g.ctx = ctx->max_ctx;
+        RCK(timed(ctx, RH_K_GEMV_QKV, [&] { return rh::launch_gemv(rh::GV_QKV, g, st); }));
+        RCK(timed(ctx, RH_K_DECODE_ATTN, [&] {
+            return rh::launch_attn_decode(ctx->dq, kc, vc, ctx->dstate, ctx->pm, ctx->pl, ctx->po,
+                                          ctx->dattn, B, c.heads, c.head_dim, ctx->max_ctx, st);
+        }));
+        g = rh::GemvArgs{};
+        g.W = W.wo; g.X = ctx->dattn; g.B = B; g.N = D; g.K = D;
+        g.out_f32 = ctx->dx; g.ldo = D; g.alpha = alpha;
+        RCK(timed(ctx, RH_K_GEMV_WO, [&] { return rh::launch_gemv(rh::GV_RESID, g, st); }));
+        LCK(rh::launch_rmsnorm(ctx->dx, W.g2, ctx->dxn, B, D, c.rms_eps, st));
+        g = rh::GemvArgs{};
+        g.W = W.w13; g.X = ctx->dxn; g.B = B; g.N = 2 * F; g.K = D;
+        g.out_f16 = ctx->dgate; g.ldo = F;
+        RCK(timed(ctx, RH_K_GEMV_W13, [&] { return rh::launch_gemv(rh::GV_SWIGLU, g, st); }));
+        g = rh::GemvArgs{};
+        g.W = W.w2; g.X = ctx->dgate; g.B = B; g.N = D; g.K = F;
+        g.out_f32 = ctx->dx; g.ldo = D; g.alpha = alpha;
+        RCK(timed(ctx, RH_K_GEMV_W2, [&] { return rh::launch_gemv(rh::GV_RESID, g, st); }));
+    }
+    LCK(rh::launch_rmsnorm(ctx->dx, ctx->gfinal, ctx->dxn, B, D, c.rms_eps, st));
+    rh::GemvArgs g{};
+    g.W = ctx->embed; g.X = ctx->dxn; g.B = B; g.N = c.vocab; g.K = D;
+    g.out_f32 = ctx->dlogits; g.ldo = c.vocab; g.softcap = c.softcap;
+    RCK(timed(ctx, RH_K_GEMV_LOGITS, [&] { return rh::launch_gemv(rh::GV_F32, g, st); }));
+    LCK(rh::launch_argmax(ctx->dlogits, B, c.vocab, ctx->dout, ctx->dtok, ctx->dseq, ctx->dstate, st));
+    LCK(rh::launch_advance(ctx->dstate, st));
+    return RH_OK;
+}
+
+int run_decode_step(rh_ctx* ctx, int B) {
+    if (!ctx->use_graphs) return enqueue_decode_step(ctx, B);
+    if (!ctx->dgraph || ctx->dgraph_B != B) {
+        if (ctx->dgraph) {
+            HCK(hipGraphExecDestroy(ctx->dgraph));
+            ctx->dgraph = nullptr;
+        }
+        hipGraph_t graph = nullptr;
+        HCK(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        ctx->capturing = true;
+        const int rc = enqueue_decode_step(ctx, B);
+        ctx->capturing = false;
+        const hipError_t ec = hipStreamEndCapture(ctx->stream, &graph);
+        if (rc != RH_OK) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return rc;
+        }
+        HCK(ec);
+        const hipError_t ei = hipGraphInstantiate(&ctx->dgraph, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        HCK(ei);
+        ctx->dgraph_B = B;
+    }
+    HCK(hipGraphLaunch(ctx->dgraph, ctx->stream));
+    return RH_OK;
+}
+
+int check_err_flag(rh_ctx* ctx) {
+    int h = 0;
+    HCK(hipMemcpyAsync(&h, ctx->d_err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
+    HCK(hipStreamSynchronize(ctx->stream));
+    if (h != 0) {
+        const int z = 0;
+        HCK(hipMemcpy(ctx->d_err, &z, sizeof(int), hipMemcpyHostToDevice));
+        return fail(ctx, RH_ERANGE, std::to_string(h) + " token id(s) >= vocab were clamped to 0");
+    }
+    return RH_OK;
+}
+
+int check_tokens(rh_ctx* ctx, const uint32_t* t, size_t n) {
+    for (size_t i = 0; i < n; ++i)
+        if (t[i] >= (uint32_t)ctx->cfg.vocab)
+            return fail(ctx, RH_ERANGE, "token id " + std::to_string(t[i]) + " at index " +
+                                            std::to_string(i) + " >= vocab " + std::to_string(ctx->cfg.vocab));
+    return RH_OK;
+}
+
+struct TensorMap {
+    int R, C, map, row_off;  // reference orientation [R][C]; map 0/1 or -1 for plain
+    f16* dst;
+    int ldd;
+};
+
+TensorMap layer_map(rh_ctx* ctx, int l, int j) {
+    const int D = ctx->cfg.dim, F = ctx->cfg.hidden;
+    Layer& W = ctx->L[l];
+    switch (j) {
+        case 0: return {D, D, 0, 0, W.wqkv, D};
+        case 1: return {D, D, 0, D, W.wqkv, D};
+        case 2: return {D, D, 0, 2 * D, W.wqkv, D};
+        case 3: return {D, D, 0, 0, W.wo, D};
+        case 4: return {D, F, 1, 0, W.w13, D};
+        case 5: return {D, F, 1, 32, W.w13, D};
+        case 6: return {D, F, -1, 0, W.w2, F};
+    }
+    return {0, 0, -1, 0, nullptr, 0};
+}
+
+// staging (fp32, reference orientation) -> device fp16 layout
+int pack_from_staging(rh_ctx* ctx, const TensorMap& m) {
+    if (m.map < 0) {
+        LCK(rh::launch_convert_f32_f16(ctx->staging, m.dst, (size_t)m.R * m.C, ctx->stream));
+    } else {
+        LCK(rh::launch_pack_transpose(ctx->staging, m.dst, m.R, m.C, m.ldd, m.map, m.row_off, ctx->stream));
+    }
+    return RH_OK;
+}
+
+int unpack_to_staging(rh_ctx* ctx, const TensorMap& m) {
+    if (m.map < 0) {
+        LCK(rh::launch_convert_f16_f32(m.dst, ctx->staging, (size_t)m.R * m.C, ctx->stream));
+    } else {
+        LCK(rh::launch_unpack_transpose(m.dst, ctx->staging, m.R, m.C, m.ldd, m.map, m.row_off, ctx->stream));
+    }
+    return RH_OK;
+}
+
+void destroy_ctx(rh_ctx* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->dgraph) (void)hipGraphExecDestroy(ctx->dgraph);
+    for (auto& p : ctx->prof)
+        for (auto& e : p.ev) { (void)hipEventDestroy(e.first); (void)hipEventDestroy(e.second); }
+    for (void* p : ctx->allocs) (void)hipFree(p);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* rh_last_error(const rh_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+int rh_create(const rh_config* cfg, int device, int max_batch, int max_ctx, rh_ctx** out) {
+    if (!cfg || !out) return RH_EINVAL;
+    *out = nullptr;
+    const rh_config& c = *cfg;
+    if (c.dim <= 0 || c.dim % 128 || c.hidden <= 0 || c.hidden % 128 || c.heads <= 0 ||
+        c.kv_heads != c.heads || !(c.head_dim == 64 || c.head_dim == 128) ||
+        c.heads * c.head_dim != c.dim || c.nlayers <= 0 || c.vocab <= 0 || c.vocab % 4 ||
+        c.seq <= 0 || max_batch <= 0 || max_ctx < 0 || !(c.rms_eps > 0.f) || !(c.rope_base > 0.f) ||
+        c.softcap < 0.f)
+        return RH_EINVAL;
+    rh_ctx* ctx = new (std::nothrow) rh_ctx;
+    if (!ctx) return RH_ENOMEM;
+    ctx->cfg = c;
+    ctx->device = device;
+    ctx->max_batch = max_batch;
+    ctx->max_ctx = max_ctx;
+    auto bail = [&](int rc) { destroy_ctx(ctx); return rc; };
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) return bail(RH_EDEVICE);
+    if (hipSetDevice(device) != hipSuccess) return bail(RH_EDEVICE);
+    if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) return bail(RH_EDEVICE);
+
+    const size_t D = c.dim, F = c.hidden, V = c.vocab;
+    int rc = RH_OK;
+    if ((rc = dalloc(ctx, &ctx->embed, V * D)) || (rc = dalloc(ctx, &ctx->gfinal, D))) return bail(rc);
+    ctx->L.resize(c.nlayers);
+    for (auto& W : ctx->L) {
+        if ((rc = dalloc(ctx, &W.wqkv, 3 * D * D)) || (rc = dalloc(ctx, &W.wo, D * D)) ||
+            (rc = dalloc(ctx, &W.w13, 2 * F * D)) || (rc = dalloc(ctx, &W.w2, D * F)) ||
+            (rc = dalloc(ctx, &W.g1, D)) || (rc = dalloc(ctx, &W.g2, D)))
+            return bail(rc);
+    }
+    if ((rc = dalloc(ctx, &ctx->d_err, 1))) return bail(rc);
+    if (hipMemset(ctx->d_err, 0, sizeof(int)) != hipSuccess) return bail(RH_EDEVICE);
+    if ((rc = ensure_rope(ctx, std::max(c.seq, max_ctx)))) return bail(rc);
+    if (max_ctx > 0) {
+        const int Bd = std::min(max_batch, 16);
+        ctx->kv_layer = (size_t)max_batch * c.heads * (size_t)max_ctx * c.head_dim;
+        const int nch = rh::attn_decode_chunks(max_ctx);
+        if ((rc = dalloc(ctx, &ctx->kcache, ctx->kv_layer * c.nlayers)) ||
+            (rc = dalloc(ctx, &ctx->vcache, ctx->kv_layer * c.nlayers)) ||
+            (rc = dalloc(ctx, &ctx->dx, 16 * D)) || (rc = dalloc(ctx, &ctx->dxn, 16 * D)) ||
+            (rc = dalloc(ctx, &ctx->dq, 16 * D)) || (rc = dalloc(ctx, &ctx->dattn, 16 * D)) ||
+            (rc = dalloc(ctx, &ctx->dgate, 16 * F)) || (rc = dalloc(ctx, &ctx->dlogits, 16 * V)) ||
+            (rc = dalloc(ctx, &ctx->pm, (size_t)Bd * c.heads * nch)) ||
+            (rc = dalloc(ctx, &ctx->pl, (size_t)Bd * c.heads * nch)) ||
+            (rc = dalloc(ctx, &ctx->po, (size_t)Bd * c.heads * nch * c.head_dim)) ||
+            (rc = dalloc(ctx, &ctx->dstate, 2)) || (rc = dalloc(ctx, &ctx->dtok, 16)) ||
+            (rc = dalloc(ctx, &ctx->dout, 16)) || (rc = dalloc(ctx, &ctx->dseq, (size_t)max_ctx * 16)))
+            return bail(rc);
+        // GEMV B operand rows >= B are never read, but keep them defined.
+        if (hipMemset(ctx->dxn, 0, 16 * D * sizeof(f16)) != hipSuccess) return bail(RH_EDEVICE);
+    }
+    // weights start as N(0, 0.02) with unit gammas so a context is usable at once
+    if ((rc = rh_init_weights_normal(ctx, 0, 0.02f))) return bail(rc);
+    *out = ctx;
+    return RH_OK;
+}
+
+void rh_destroy(rh_ctx* ctx) { destroy_ctx(ctx); }
+
+int rh_load_weights_f32(rh_ctx* ctx, const float* embed, const float* gamma_final,
+                        const float* const* layer_tensors) {
+    if (!ctx || !embed || !gamma_final || !layer_tensors) return fail(ctx, RH_EINVAL, "null argument");
+    HCK(hipSetDevice(ctx->device));
+    const rh_config& c = ctx->cfg;
+    const size_t D = c.dim, F = c.hidden, V = c.vocab;
+    for (int i = 0; i < 9 * c.nlayers; ++i)
+        if (!layer_tensors[i]) return fail(ctx, RH_EINVAL, "null layer tensor " + std::to_string(i));
+    RCK(ensure_staging(ctx, std::max({V * D, D * F, D * D})));
+    hipStream_t st = ctx->stream;
+    HCK(hipMemcpyAsync(ctx->staging, embed, V * D * sizeof(float), hipMemcpyHostToDevice, st));
+    LCK(rh::launch_convert_f32_f16(ctx->staging, ctx->embed, V * D, st));
+    HCK(hipMemcpyAsync(ctx->gfinal, gamma_final, D * sizeof(float), hipMemcpyHostToDevice, st));
+    for (int l = 0; l < c.nlayers; ++l) {
+        const float* const* t = layer_tensors + 9 * l;
+        for (int j = 0; j < 7; ++j) {
+            const TensorMap m = layer_map(ctx, l, j);
+            HCK(hipMemcpyAsync(ctx->staging, t[j], (size_t)m.R * m.C * sizeof(float), hipMemcpyHostToDevice, st));
+            RCK(pack_from_staging(ctx, m));
+        }
+        HCK(hipMemcpyAsync(ctx->L[l].g1, t[7], D * sizeof(float), hipMemcpyHostToDevice, st));
+        HCK(hipMemcpyAsync(ctx->L[l].g2, t[8], D * sizeof(float), hipMemcpyHostToDevice, st));
+    }
+    HCK(hipStreamSynchronize(st));
+    return RH_OK;
+}
+
+int rh_read_weights_f32(rh_ctx* ctx, float* embed, float* gamma_final, float* const* layer_tensors) {
+    if (!ctx) return RH_EINVAL;
+    HCK(hipSetDevice(ctx->device));
+    const rh_config& c = ctx->cfg;
+    const size_t D = c.dim, F = c.hidden, V = c.vocab;
+    RCK(ensure_staging(ctx, std::max({V * D, D * F, D * D})));
+    hipStream_t st = ctx->stream;
+    if (embed) {
+        LCK(rh::launch_convert_f16_f32(ctx->embed, ctx->staging, V * D, st));
+        HCK(hipMemcpyAsync(embed, ctx->staging, V * D * sizeof(float), hipMemcpyDeviceToHost, st));
+        HCK(hipStreamSynchronize(st));
+    }
+    if (gamma_final) HCK(hipMemcpyAsync(gamma_final, ctx->gfinal, D * sizeof(float), hipMemcpyDeviceToHost, st));
+    if (layer_tensors) {
+        for (int l = 0; l < c.nlayers; ++l) {
+            float* const* t = layer_tensors + 9 * l;
+            for (int j = 0; j < 7; ++j) {
+                if (!t[j]) continue;
+                const TensorMap m = layer_map(ctx, l, j);
+                RCK(unpack_to_staging(ctx, m));
+                HCK(hipMemcpyAsync(t[j], ctx->staging, (size_t)m.R * m.C * sizeof(float), hipMemcpyDeviceToHost, st));
+                HCK(hipStreamSynchronize(st));
+            }
+            if (t[7]) HCK(hipMemcpyAsync(t[7], ctx->L[l].g1, D * sizeof(float), hipMemcpyDeviceToHost, st));
+            if (t[8]) HCK(hipMemcpyAsync(t[8], ctx->L[l].g2, D * sizeof(float), hipMemcpyDeviceToHost, st));
+        }
+    }
+    HCK(hipStreamSynchronize(st));
+    (void)F;
+    return RH_OK;
+}
+
+int rh_init_weights_normal(rh_ctx* ctx, uint64_t seed, float std_) {
+    if (!ctx) return RH_EINVAL;
+    HCK(hipSetDevice(ctx->device));
+    const rh_config& c = ctx->cfg;
+    const size_t D = c.dim, F = c.hidden, V = c.vocab;
+    RCK(ensure_staging(ctx, std::max({V * D, D * F, D * D})));
+    hipStream_t st = ctx->stream;
+    LCK(rh::launch_init_normal(ctx->staging, V * D, seed, 0u, std_, st));
+    LCK(rh::launch_convert_f32_f16(ctx->staging, ctx->embed, V * D, st));
+    LCK(rh::launch_fill_f32(ctx->gfinal, 1.0f, D, st));
+    for (int l = 0; l < c.nlayers; ++l) {
+        for (int j = 0; j < 7; ++j) {
+            const TensorMap m = layer_map(ctx, l, j);
+            LCK(rh::launch_init_normal(ctx->staging, (size_t)m.R * m.C, seed, 1u + 9u * l + j, std_, st));
+            RCK(pack_from_staging(ctx, m));
+        }
+        LCK(rh::launch_fill_f32(ctx->L[l].g1, 1.0f, D, st));
+        LCK(rh::launch_fill_f32(ctx->L[l].g2, 1.0f, D, st));
+    }
+    HCK(hipStreamSynchronize(st));
+    (void)F;
+    return RH_OK;
+}
+
+int rh_forward_dev(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
+                   float* logits_out, float* token_losses_out, float* mean_loss_out) {
+    if (!ctx || !tokens) return fail(ctx, RH_EINVAL, "null argument");
+    if (batch <= 0 || seq <= 0 || batch > ctx->max_batch)
+        return fail(ctx, RH_ERANGE, "batch must be in [1, max_batch] and seq >= 1");
+    if ((token_losses_out || mean_loss_out) && !targets)
+        return fail(ctx, RH_EINVAL, "losses requested without targets");
+    HCK(hipSetDevice(ctx->device));
+    const int M = batch * seq;
+    RCK(ensure_workspace(ctx, M));
+    RCK(ensure_rope(ctx, seq));
+    hipStream_t st = ctx->stream;
+    HCK(hipMemcpyAsync(ctx->d_tok, tokens, (size_t)M * sizeof(uint32_t), hipMemcpyDeviceToDevice, st));
+    if (targets)
+        HCK(hipMemcpyAsync(ctx->d_tgt, targets, (size_t)M * sizeof(uint32_t), hipMemcpyDeviceToDevice, st));
+    RCK(enqueue_body(ctx, batch, seq, false));
+    RCK(enqueue_tail(ctx, batch, seq, targets != nullptr));
+    const size_t V = V_(ctx);
+    if (logits_out)
+        HCK(hipMemcpyAsync(logits_out, ctx->logits, (size_t)M * V * sizeof(float), hipMemcpyDeviceToDevice, st));
+    if (token_losses_out)
+        HCK(hipMemcpyAsync(token_losses_out, ctx->tok_loss, (size_t)M * sizeof(float), hipMemcpyDeviceToDevice, st));
+    if (mean_loss_out)
+        HCK(hipMemcpyAsync(mean_loss_out, ctx->mean, (size_t)batch * sizeof(float), hipMemcpyDeviceToDevice, st));
+    return RH_OK;
+}
+
+int rh_forward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
+               float* logits_out, float* token_losses_out, float* mean_loss_out) {
+    if (!ctx || !tokens) return fail(ctx, RH_EINVAL, "null argument");
+    if (batch <= 0 || seq <= 0 || batch > ctx->max_batch)
+        return fail(ctx, RH_ERANGE, "batch must be in [1, max_batch] and seq >= 1");
+    if ((token_losses_out || mean_loss_out) && !targets)
+        return fail(ctx, RH_EINVAL, "losses requested without targets");
+    const size_t M = (size_t)batch * seq;
+    RCK(check_tokens(ctx, tokens, M));
+    if (targets) RCK(check_tokens(ctx, targets, M));
+    HCK(hipSetDevice(ctx->device));
+    RCK(ensure_workspace(ctx, (int)M));
+    RCK(ensure_rope(ctx, seq));
+    hipStream_t st = ctx->stream;
+    HCK(hipMemcpyAsync(ctx->d_tok, tokens, M * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    if (targets) HCK(hipMemcpyAsync(ctx->d_tgt, targets, M * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    RCK(enqueue_body(ctx, batch, seq, false));
+    RCK(enqueue_tail(ctx, batch, seq, targets != nullptr));
+    const size_t V = V_(ctx);
+    if (logits_out) HCK(hipMemcpyAsync(logits_out, ctx->logits, M * V * sizeof(float), hipMemcpyDeviceToHost, st));
+    if (token_losses_out)
+        HCK(hipMemcpyAsync(token_losses_out, ctx->tok_loss, M * sizeof(float), hipMemcpyDeviceToHost, st));
+    if (mean_loss_out) HCK(hipMemcpyAsync(mean_loss_out, ctx->mean, batch * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    return check_err_flag(ctx);
+}
+
+int rh_prefill(rh_ctx* ctx, const uint32_t* tokens, int batch, int len, uint32_t* next_tok_out,
+               float* last_logits_out) {
+    if (!ctx || !tokens) return fail(ctx, RH_EINVAL, "null argument");
+    if (ctx->max_ctx <= 0) return fail(ctx, RH_ESTATE, "context was created without a KV cache");
+    if (batch <= 0 || batch > std::min(ctx->max_batch, 16) || len <= 0 || len > ctx->max_ctx)
+        return fail(ctx, RH_ERANGE, "prefill needs 1 <= batch <= min(max_batch, 16), 1 <= len <= max_ctx");
+    const size_t M = (size_t)batch * len;
+    RCK(check_tokens(ctx, tokens, M));
+    HCK(hipSetDevice(ctx->device));
+    RCK(ensure_workspace(ctx, (int)M));
+    hipStream_t st = ctx->stream;
+    HCK(hipMemcpyAsync(ctx->d_tok, tokens, M * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    RCK(enqueue_body(ctx, batch, len, true));
+    const rh_config& c = ctx->cfg;
+    LCK(rh::launch_rmsnorm_strided(ctx->x, ctx->gfinal, ctx->dxn, batch, c.dim, c.rms_eps, len, len - 1, st));
+    rh::GemvArgs g{};
+    g.W = ctx->embed; g.X = ctx->dxn; g.B = batch; g.N = c.vocab; g.K = c.dim;
+    g.out_f32 = ctx->dlogits; g.ldo = c.vocab; g.softcap = c.softcap;
+    RCK(timed(ctx, RH_K_GEMV_LOGITS, [&] { return rh::launch_gemv(rh::GV_F32, g, st); }));
+    LCK(rh::launch_set_state(ctx->dstate, len, 0, st));
+    LCK(rh::launch_argmax(ctx->dlogits, batch, c.vocab, ctx->dout, ctx->dtok, nullptr, ctx->dstate, st));
+    if (next_tok_out) HCK(hipMemcpyAsync(next_tok_out, ctx->dout, batch * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    if (last_logits_out)
+        HCK(hipMemcpyAsync(last_logits_out, ctx->dlogits, (size_t)batch * c.vocab * sizeof(float),
+                           hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    ctx->dec_B = batch;
+    ctx->host_pos = len;
+    ctx->have_prefill = true;
+    return check_err_flag(ctx);
+}
+
+int rh_decode_step(rh_ctx* ctx, const uint32_t* in_tok, uint32_t* out_tok, float* logits_out) {
+    if (!ctx || !in_tok) return fail(ctx, RH_EINVAL, "null argument");
+    if (!ctx->have_prefill) return fail(ctx, RH_ESTATE, "rh_decode_step before rh_prefill");
+    if (ctx->host_pos >= ctx->max_ctx) return fail(ctx, RH_ERANGE, "KV cache is full");
+    const int B = ctx->dec_B;
+    RCK(check_tokens(ctx, in_tok, B));
+    HCK(hipSetDevice(ctx->device));
+    hipStream_t st = ctx->stream;
+    HCK(hipMemcpyAsync(ctx->dtok, in_tok, B * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    LCK(rh::launch_set_state(ctx->dstate, ctx->host_pos, 0, st));
+    RCK(run_decode_step(ctx, B));
+    if (out_tok) HCK(hipMemcpyAsync(out_tok, ctx->dout, B * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    if (logits_out)
+        HCK(hipMemcpyAsync(logits_out, ctx->dlogits, (size_t)B * ctx->cfg.vocab * sizeof(float),
+                           hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    ctx->host_pos += 1;
+    return check_err_flag(ctx);
+}
+
+int rh_decode(rh_ctx* ctx, const uint32_t* in_tok, int nsteps, uint32_t* out_tokens) {
+    if (!ctx || !in_tok || !out_tokens) return fail(ctx, RH_EINVAL, "null argument");
+    if (!ctx->have_prefill) return fail(ctx, RH_ESTATE, "rh_decode before rh_prefill");
+    if (nsteps <= 0 || ctx->host_pos + nsteps > ctx->max_ctx)
+        return fail(ctx, RH_ERANGE, "nsteps must be >= 1 and fit in the KV cache");
+    const int B = ctx->dec_B;
+    RCK(check_tokens(ctx, in_tok, B));
+    HCK(hipSetDevice(ctx->device));
+    hipStream_t st = ctx->stream;
+    HCK(hipMemcpyAsync(ctx->dtok, in_tok, B * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    LCK(rh::launch_set_state(ctx->dstate, ctx->host_pos, 0, st));
+    for (int s = 0; s < nsteps; ++s) RCK(run_decode_step(ctx, B));
+    HCK(hipMemcpyAsync(out_tokens, ctx->dseq, (size_t)nsteps * B * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    ctx->host_pos += nsteps;
+    return check_err_flag(ctx);
+}
+
+int rh_set_softcap(rh_ctx* ctx, float softcap) {
+    if (!ctx) return RH_EINVAL;
+    if (!(softcap >= 0.f)) return fail(ctx, RH_EINVAL, "softcap must be >= 0");
+    if (softcap != ctx->cfg.softcap && ctx->dgraph) {
+        (void)hipGraphExecDestroy(ctx->dgraph);  // the captured step bakes the softcap in
+        ctx->dgraph = nullptr;
+    }
+    ctx->cfg.softcap = softcap;
+    return RH_OK;
+}
+
+int rh_decode_pos(rh_ctx* ctx, int* pos_out) {
+    if (!ctx || !pos_out) return RH_EINVAL;
+    *pos_out = ctx->host_pos;
+    return RH_OK;
+}
+
+int rh_sync(rh_ctx* ctx) {
+    if (!ctx) return RH_EINVAL;
+    HCK(hipSetDevice(ctx->device));
+    HCK(hipStreamSynchronize(ctx->stream));
+    return check_err_flag(ctx);
+}
+
+void* rh_stream(rh_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int rh_profile_enable(rh_ctx* ctx, int cls, int enable) {
+    if (!ctx || cls < 0 || cls >= RH_K_NCLASSES) return RH_EINVAL;
+    Prof& p = ctx->prof[cls];
+    for (auto& e : p.ev) { (void)hipEventDestroy(e.first); (void)hipEventDestroy(e.second); }
+    p.ev.clear();
+    p.ms = 0;
+    p.n = 0;
+    p.on = enable != 0;
+    return RH_OK;
+}
+
+int rh_profile_read(rh_ctx* ctx, int cls, double* total_ms, int64_t* launches) {
+    if (!ctx || cls < 0 || cls >= RH_K_NCLASSES) return RH_EINVAL;
+    HCK(hipSetDevice(ctx->device));
+    HCK(hipStreamSynchronize(ctx->stream));
+    Prof& p = ctx->prof[cls];
+    for (auto& e : p.ev) {
+        float ms = 0.f;
+        HCK(hipEventElapsedTime(&ms, e.first, e.second));
+        p.ms += ms;
+        p.n += 1;
+        (void)hipEventDestroy(e.first);
+        (void)hipEventDestroy(e.second);
+    }
+    p.ev.clear();
+    if (total_ms) *total_ms = p.ms;
+    if (launches) *launches = p.n;
+    return RH_OK;
+}
+
+int rh_set_graphs(rh_ctx* ctx, int enable) {
+    if (!ctx) return RH_EINVAL;
+    ctx->use_graphs = enable != 0;
+    return RH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,237 @@
+"""ctypes binding of librustane_hip.so (include/rustane_hip.h).
+
+This is the Python face of the C-ABI that stands in for the reference's
+`ane-bridge` crate (crates/ane-bridge/src/lib.rs:1-9).  It loads the in-tree
+library and fails loudly when it is missing: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librustane_hip.so")
+HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "rustane_hip.h")
+
+RH_OK, RH_EINVAL, RH_ERANGE, RH_ENOMEM, RH_EDEVICE, RH_ESTATE = 0, -1, -2, -3, -4, -5
+ERR_NAMES = {RH_EINVAL: "RH_EINVAL", RH_ERANGE: "RH_ERANGE", RH_ENOMEM: "RH_ENOMEM",
+             RH_EDEVICE: "RH_EDEVICE", RH_ESTATE: "RH_ESTATE"}
+
+K_GEMM_QKV, K_GEMM_WO, K_GEMM_W13, K_GEMM_W2, K_GEMM_LOGITS, K_ATTN = range(6)
+K_GEMV_QKV, K_GEMV_WO, K_GEMV_W13, K_GEMV_W2, K_GEMV_LOGITS, K_DECODE_ATTN = range(6, 12)
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_vp = ctypes.c_void_p
+
+
+class HipBridgeError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{ERR_NAMES.get(code, code)}: {msg}")
+        self.code = code
+
+
+class RhConfig(ctypes.Structure):
+    _fields_ = [("dim", ctypes.c_int32), ("hidden", ctypes.c_int32), ("heads", ctypes.c_int32),
+                ("kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("seq", ctypes.c_int32), ("nlayers", ctypes.c_int32), ("vocab", ctypes.c_int32),
+                ("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float),
+                ("softcap", ctypes.c_float)]
+
+
+_lib = None
+
+
+def lib():
+    """Loads librustane_hip.so; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m rustane_amd.build` "
+                           "(there is no CPU fallback for the HIP path)")
+    L = ctypes.CDLL(LIB_PATH)
+    ctxp = ctypes.c_void_p
+    L.rh_create.argtypes = [ctypes.POINTER(RhConfig), ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                            ctypes.POINTER(ctxp)]
+    L.rh_destroy.argtypes = [ctxp]
+    L.rh_destroy.restype = None
+    L.rh_last_error.argtypes = [ctxp]
+    L.rh_last_error.restype = ctypes.c_char_p
+    L.rh_load_weights_f32.argtypes = [ctxp, _f32p, _f32p, ctypes.POINTER(_f32p)]
+    L.rh_read_weights_f32.argtypes = [ctxp, _f32p, _f32p, ctypes.POINTER(_f32p)]
+    L.rh_init_weights_normal.argtypes = [ctxp, ctypes.c_uint64, ctypes.c_float]
+    L.rh_forward.argtypes = [ctxp, _u32p, _u32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p, _f32p]
+    L.rh_forward_dev.argtypes = [ctxp, _vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]
+    L.rh_prefill.argtypes = [ctxp, _u32p, ctypes.c_int, ctypes.c_int, _u32p, _f32p]
+    L.rh_decode_step.argtypes = [ctxp, _u32p, _u32p, _f32p]
+    L.rh_decode.argtypes = [ctxp, _u32p, ctypes.c_int, _u32p]
+    L.rh_decode_pos.argtypes = [ctxp, ctypes.POINTER(ctypes.c_int)]
+    L.rh_set_softcap.argtypes = [ctxp, ctypes.c_float]
+    L.rh_sync.argtypes = [ctxp]
+    L.rh_stream.argtypes = [ctxp]
+    L.rh_stream.restype = ctypes.c_void_p
+    L.rh_profile_enable.argtypes = [ctxp, ctypes.c_int, ctypes.c_int]
+    L.rh_profile_read.argtypes = [ctxp, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                  ctypes.POINTER(ctypes.c_int64)]
+    L.rh_set_graphs.argtypes = [ctxp, ctypes.c_int]
+    _lib = L
+    return L
+
+
+def header_symbols() -> list[str]:
+    """Names of every function declared in include/rustane_hip.h."""
+    import re
+    text = open(HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rh_[a-z0-9_]+)\s*\(", text)))
+
+
+def _f(a):
+    return None if a is None else a.ctypes.data_as(_f32p)
+
+
+def _u(a):
+    return None if a is None else a.ctypes.data_as(_u32p)
+
+
+@dataclass
+class ForwardOut:
+    logits: np.ndarray | None        # [B, S, V]
+    token_losses: np.ndarray | None  # [B, S]
+    mean_loss: np.ndarray | None     # [B]
+
+
+class Context:
+    """One rh_ctx: a device, a stream, fp16 weights, KV cache and workspaces."""
+
+    def __init__(self, cfg: RhConfig, device: int = 0, max_batch: int = 1, max_ctx: int = 0):
+        self.cfg = cfg
+        self.max_batch, self.max_ctx = max_batch, max_ctx
+        h = ctypes.c_void_p()
+        rc = lib().rh_create(ctypes.byref(cfg), device, max_batch, max_ctx, ctypes.byref(h))
+        if rc != RH_OK:
+            raise HipBridgeError(rc, "rh_create failed")
+        self.h = h
+
+    # -- lifetime ---------------------------------------------------------
+    def close(self):
+        if getattr(self, "h", None):
+            lib().rh_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _ck(self, rc: int, what: str):
+        if rc != RH_OK:
+            msg = lib().rh_last_error(self.h)
+            raise HipBridgeError(rc, f"{what}: {msg.decode() if msg else ''}")
+
+    # -- weights ----------------------------------------------------------
+    def load_weights(self, embed, gamma_final, layers):
+        """layers: nlayers lists of 9 fp32 arrays in RSTK order (reference orientation)."""
+        keep = [np.ascontiguousarray(embed, np.float32), np.ascontiguousarray(gamma_final, np.float32)]
+        flat = [np.ascontiguousarray(t, np.float32) for lw in layers for t in lw]
+        ptrs = (_f32p * len(flat))(*[_f(t) for t in flat])
+        self._ck(lib().rh_load_weights_f32(self.h, _f(keep[0]), _f(keep[1]), ptrs), "rh_load_weights_f32")
+
+    def read_weights(self):
+        c = self.cfg
+        D, F, V, L = c.dim, c.hidden, c.vocab, c.nlayers
+        embed = np.empty((V, D), np.float32)
+        gf = np.empty(D, np.float32)
+        shapes = [(D, D)] * 4 + [(D, F)] * 3 + [(D,), (D,)]
+        layers = [[np.empty(s, np.float32) for s in shapes] for _ in range(L)]
+        flat = [t for lw in layers for t in lw]
+        ptrs = (_f32p * len(flat))(*[_f(t) for t in flat])
+        self._ck(lib().rh_read_weights_f32(self.h, _f(embed), _f(gf), ptrs), "rh_read_weights_f32")
+        return embed, gf, layers
+
+    def init_normal(self, seed: int, std: float = 0.02):
+        self._ck(lib().rh_init_weights_normal(self.h, seed, std), "rh_init_weights_normal")
+
+    def set_softcap(self, c: float):
+        self._ck(lib().rh_set_softcap(self.h, c), "rh_set_softcap")
+
+    # -- forward ----------------------------------------------------------
+    def forward(self, tokens, targets=None, want_logits=True, want_token_losses=True) -> ForwardOut:
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        if tokens.ndim == 1:
+            tokens = tokens[None]
+        B, S = tokens.shape
+        tg = None if targets is None else np.ascontiguousarray(targets, np.uint32).reshape(B, S)
+        logits = np.empty((B, S, self.cfg.vocab), np.float32) if want_logits else None
+        tl = np.empty((B, S), np.float32) if (tg is not None and want_token_losses) else None
+        ml = np.empty((B,), np.float32) if tg is not None else None
+        self._ck(lib().rh_forward(self.h, _u(tokens), _u(tg), B, S, _f(logits), _f(tl), _f(ml)),
+                 "rh_forward")
+        return ForwardOut(logits, tl, ml)
+
+    def forward_dev(self, tokens_ptr: int, targets_ptr: int | None, batch: int, seq: int,
+                    logits_ptr=None, token_losses_ptr=None, mean_ptr=None):
+        self._ck(lib().rh_forward_dev(self.h, tokens_ptr, targets_ptr, batch, seq, logits_ptr,
+                                      token_losses_ptr, mean_ptr), "rh_forward_dev")
+
+    # -- decode -----------------------------------------------------------
+    def prefill(self, tokens, want_logits=False):
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        if tokens.ndim == 1:
+            tokens = tokens[None]
+        B, n = tokens.shape
+        nxt = np.empty(B, np.uint32)
+        lg = np.empty((B, self.cfg.vocab), np.float32) if want_logits else None
+        self._ck(lib().rh_prefill(self.h, _u(tokens), B, n, _u(nxt), _f(lg)), "rh_prefill")
+        return nxt, lg
+
+    def decode_step(self, in_tok, want_logits=False):
+        in_tok = np.ascontiguousarray(in_tok, np.uint32).reshape(-1)
+        out = np.empty_like(in_tok)
+        lg = np.empty((len(in_tok), self.cfg.vocab), np.float32) if want_logits else None
+        self._ck(lib().rh_decode_step(self.h, _u(in_tok), _u(out), _f(lg)), "rh_decode_step")
+        return out, lg
+
+    def decode(self, in_tok, nsteps: int):
+        in_tok = np.ascontiguousarray(in_tok, np.uint32).reshape(-1)
+        out = np.empty((nsteps, len(in_tok)), np.uint32)
+        self._ck(lib().rh_decode(self.h, _u(in_tok), nsteps, _u(out)), "rh_decode")
+        return out
+
+    @property
+    def pos(self) -> int:
+        p = ctypes.c_int()
+        self._ck(lib().rh_decode_pos(self.h, ctypes.byref(p)), "rh_decode_pos")
+        return p.value
+
+    # -- misc -------------------------------------------------------------
+    def sync(self):
+        self._ck(lib().rh_sync(self.h), "rh_sync")
+
+    @property
+    def stream(self) -> int:
+        return lib().rh_stream(self.h)
+
+    def profile_enable(self, kclass: int, on: bool = True):
+        self._ck(lib().rh_profile_enable(self.h, kclass, int(on)), "rh_profile_enable")
+
+    def profile_read(self, kclass: int):
+        ms = ctypes.c_double()
+        n = ctypes.c_int64()
+        self._ck(lib().rh_profile_read(self.h, kclass, ctypes.byref(ms), ctypes.byref(n)),
+                 "rh_profile_read")
+        return ms.value, n.value
+
+    def set_graphs(self, on: bool):
+        self._ck(lib().rh_set_graphs(self.h, int(on)), "rh_set_graphs")
