@@ -51,6 +51,10 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--extra-batches", default="", help="e.g. 4,16: also time these prefill batches")
+    ap.add_argument("--decode-only", action="store_true", help="skip the prefill timing")
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="decode with eager launches instead of graph replay (profilers that "
+                         "cannot follow graph capture)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -101,6 +105,10 @@ def main():
             ctx.profile_enable(hb.K_GEMM_W13, False)
         loss = mean.numpy()
         return ms, wall, k_ms, k_n, loss
+
+    if args.decode_only:
+        print(json.dumps({"decode": run_decode(ctx, cfg, args, hb, E, hip_rt, stream)}), flush=True)
+        return
 
     B = args.batch
     ms, wall, k_ms, k_n, loss = run_prefill(B, args.steps, args.warmup)
@@ -172,6 +180,7 @@ def main():
 
 def run_decode(ctx, cfg, args, hb, E, hip_rt, stream):
     B = args.decode_batch
+    ctx.set_graphs(not args.decode_eager)
     rng = np.random.default_rng(7)
     prompt = rng.integers(0, cfg.vocab, size=(B, args.decode_ctx)).astype(np.uint32)
     t = time.time()
@@ -198,7 +207,7 @@ def run_decode(ctx, cfg, args, hb, E, hip_rt, stream):
     ctx.decode(nxt2, 8)
     k_ms, k_n = ctx.profile_read(hb.K_GEMV_W13)
     ctx.profile_enable(hb.K_GEMV_W13, False)
-    ctx.set_graphs(True)
+    ctx.set_graphs(not args.decode_eager)
     w13_bytes = 2 * cfg.hidden * cfg.dim * 2
     w13_gbs = w13_bytes / ((k_ms / k_n) / 1e3) / 1e9 if k_n else None
     out = {
@@ -212,6 +221,7 @@ def run_decode(ctx, cfg, args, hb, E, hip_rt, stream):
                      "mean_launch_us": round((k_ms / k_n) * 1e3, 2) if k_n else None,
                      "achieved_gbs": round(w13_gbs, 1) if w13_gbs else None},
         "first_tokens": [int(x) for x in toks[:8, 0]],
+        "launch": "eager" if args.decode_eager else "hip graph per step",
     }
     log(f"[bench] decode B={B}: {out}")
     return out

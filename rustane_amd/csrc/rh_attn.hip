@@ -13,10 +13,10 @@
 // the fp16 P operand all stay lane-local, and the row reductions are two
 // xor-shuffles over the 4 lane groups that share a query.
 //
-// Decode: split-context.  One block per (sequence, head, 256-position chunk)
-// scores its chunk with 16-byte K loads (hd/8 lanes per position), keeps
-// (max, sum, P.V) partials, and a combine kernel merges the chunks.  The
-// position is read from device memory so the step can be replayed as a graph.
+// Decode: split-context.  One block per (sequence, head, 128-position chunk)
+// scores its chunk with 16-byte K loads (hd/8 lanes per position) and keeps
+// (max, sum, P.V) partials; a small kernel merges them.  The position is read
+// from device memory so the step can be replayed as a graph.
 #include "rh_device.h"
 #include "rh_kernels.h"
 
@@ -162,8 +162,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
     }
 }
 
-constexpr int DCH = 256;  // decode positions per chunk
+constexpr int DCH = 128;  // decode positions per chunk block
 
+// One block per (chunk, head, sequence).  hd/8 lanes share a position (16-byte
+// K/V loads); every K and V load of a thread is issued before any of its
+// arithmetic so each block pays the memory latency about once.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict__ Q,
                                                           const f16* __restrict__ Kc,
@@ -172,8 +175,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict_
                                                           float* part_m, float* part_l,
                                                           float* part_o, int H, int ctx,
                                                           float scale) {
-    constexpr int LPP = HD / 8;          // lanes per position
-    constexpr int NSLOT = 256 / LPP;     // positions scored concurrently per block
+    constexpr int LPP = HD / 8;       // lanes per position
+    constexpr int NSLOT = 256 / LPP;  // positions per pass of the block
+    constexpr int PER = DCH / NSLOT;  // positions per thread
     __shared__ float sS[DCH];
     __shared__ float sO[NSLOT][HD + 4];
     __shared__ float red[4];
@@ -184,59 +188,72 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict_
     const int t0 = chunk * DCH, t1 = min(nctx, t0 + DCH);
     const size_t bh = (size_t)b * H + h;
     const size_t pidx = bh * nch + chunk;
-    if (t0 >= t1) {
+    if (t0 < t1) {
+        const f16x8 qv = *(const f16x8*)(Q + bh * HD + 8 * j);
+        const f16* Kb = Kc + bh * ctx * HD + 8 * j;
+        const f16* Vb = Vc + bh * ctx * HD + 8 * j;
+        const f16x8 z = {};
+        f16x8 kv[PER], vv[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int t = t0 + slot + i * NSLOT;
+            kv[i] = t < t1 ? *(const f16x8*)(Kb + (size_t)t * HD) : z;
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int t = t0 + slot + i * NSLOT;
+            vv[i] = t < t1 ? *(const f16x8*)(Vb + (size_t)t * HD) : z;
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            float d = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) d += (float)qv[e] * (float)kv[i][e];
+#pragma unroll
+            for (int o = LPP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, RH_WAVE);
+            const int t = t0 + slot + i * NSLOT;
+            if (j == 0 && t < t1) sS[t - t0] = d * scale;
+        }
+        __syncthreads();
+        const int n = t1 - t0;
+        float mx = tid < n ? sS[tid] : -INFINITY;  // n <= DCH < 256
+        mx = wave_max(mx);
+        if ((tid & 63) == 0) red[tid >> 6] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        __syncthreads();
+        float p = 0.f;
+        if (tid < n) {
+            p = __expf(sS[tid] - mx);
+            sS[tid] = p;
+        }
+        const float ls = block_sum_256(p, red);  // its barrier also publishes sS
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int t = t0 + slot + i * NSLOT;
+            const float pt = t < t1 ? sS[t - t0] : 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] += pt * (float)vv[i][e];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sO[slot][8 * j + e] = acc[e];
+        __syncthreads();
+        if (tid < HD) {
+            float o = 0.f;
+            for (int k = 0; k < NSLOT; ++k) o += sO[k][tid];
+            part_o[pidx * HD + tid] = o;
+        }
+        if (tid == 0) { part_m[pidx] = mx; part_l[pidx] = ls; }
+    } else {
         if (tid == 0) { part_m[pidx] = -INFINITY; part_l[pidx] = 0.f; }
         if (tid < HD) part_o[pidx * HD + tid] = 0.f;
-        return;
     }
-    const f16x8 qv = *(const f16x8*)(Q + (size_t)b * H * HD + (size_t)h * HD + 8 * j);
-    const f16* Kb = Kc + bh * ctx * HD;
-    const f16* Vb = Vc + bh * ctx * HD;
-    for (int t = t0 + slot; t < t1; t += NSLOT) {
-        const f16x8 kv = *(const f16x8*)(Kb + (size_t)t * HD + 8 * j);
-        float d = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) d += (float)qv[e] * (float)kv[e];
-#pragma unroll
-        for (int o = LPP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, RH_WAVE);
-        if (j == 0) sS[t - t0] = d * scale;
-    }
-    __syncthreads();
-    const int n = t1 - t0;
-    float mx = -INFINITY;
-    for (int i = tid; i < n; i += 256) mx = fmaxf(mx, sS[i]);
-    mx = wave_max(mx);
-    if ((tid & 63) == 0) red[tid >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    float ls = 0.f;
-    for (int i = tid; i < n; i += 256) {
-        const float p = __expf(sS[i] - mx);
-        sS[i] = p;
-        ls += p;
-    }
-    ls = block_sum_256(ls, red);  // includes a barrier: sS is complete after it
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int t = t0 + slot; t < t1; t += NSLOT) {
-        const float p = sS[t - t0];
-        const f16x8 vv = *(const f16x8*)(Vb + (size_t)t * HD + 8 * j);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += p * (float)vv[e];
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sO[slot][8 * j + e] = acc[e];
-    __syncthreads();
-    if (tid < HD) {
-        float s = 0.f;
-        for (int k = 0; k < NSLOT; ++k) s += sO[k][tid];
-        part_o[pidx * HD + tid] = s;
-    }
-    if (tid == 0) { part_m[pidx] = mx; part_l[pidx] = ls; }
 }
 
-__global__ void attn_combine_kernel(const float* part_m, const float* part_l,
-                                    const float* part_o, f16* out, int H, int HD, int nch) {
+// Merges the chunk partials of one (head, sequence).
+__global__ void attn_merge_kernel(const float* part_m, const float* part_l, const float* part_o,
+                                  f16* out, int H, int HD, int nch) {
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const size_t bh = (size_t)b * H + h;
     float M = -INFINITY;
@@ -247,9 +264,9 @@ __global__ void attn_combine_kernel(const float* part_m, const float* part_l,
         if (mc == -INFINITY) continue;
         const float wgt = __expf(mc - M);
         l += part_l[bh * nch + c] * wgt;
-        if (d < HD) o += part_o[(bh * nch + c) * HD + d] * wgt;
+        o += part_o[(bh * nch + c) * HD + d] * wgt;
     }
-    if (d < HD) out[bh * HD + d] = (f16)(o / l);
+    out[bh * HD + d] = (f16)(o / l);
 }
 
 }  // namespace
@@ -283,10 +300,10 @@ hipError_t launch_attn_decode(const f16* q, const f16* k, const f16* v, const in
                            part_l, part_o, H, ctx, scale);
     else
         return hipErrorInvalidValue;
-    hipError_t e = hipGetLastError();
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(H, B), dim3(hd), 0, st, part_m, part_l, part_o,
-                       out, H, hd, nch);
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(H, B), dim3(hd), 0, st, part_m, part_l, part_o, out,
+                       H, hd, nch);
     return hipGetLastError();
 }
 

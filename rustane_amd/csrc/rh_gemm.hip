@@ -1,6 +1,6 @@
 // rh_gemm.hip -- prefill GEMMs on fp16 MFMA (gfx950) with fused epilogues.
 //
-// One kernel shape serves every projection of the forward token loop
+// One kernel family serves every projection of the forward token loop
 // (kernels/sdpa_fwd.rs:115-117 QKV, dyn_matmul.rs:15-75 Wo, ffn_fused.rs:80-160
 // W1/W3/W2, full_model.rs:555-567 tied logits):
 //     Y[m][n] = sum_k X[m][k] * W[n][k]
@@ -10,129 +10,382 @@
 // accumulator then holds 4 consecutive output features of one token, which
 // makes the RoPE pairs (2i, 2i+1) and 16-byte fp32 stores lane-local.
 //
-// Block tile 128 (features) x BM (tokens) x 64 (k), 4 waves in 2 x 2, each
-// wave 64 x BM/2 as 32x32x16 MFMA tiles.  Global -> register prefetch of the
-// next k-slab overlaps the MFMAs of the current one; LDS is double-buffered
-// with rows padded by 16 bytes so the 16-byte fragment reads are
-// bank-conflict free.  Tiles are remapped so the BM-slices that share a
-// weight panel run on the same XCD (one L2).
+// Tile policies (all: 32x32x16 MFMA, 64-wide k-slabs, both operands staged
+// through LDS with rows padded by 16 bytes so the 16-byte fragment reads are
+// bank-conflict free, fragments double-buffered in registers):
+//   LdsTile<2,2>   128x128, 4 waves (2x2, 64x64 each), one slab of prefetch
+//   LdsTile2<2,2>  same tile, global loads issued two slabs ahead
+//   GTile<2,4,4,2> 256x256, 8 waves (2x4, 128x64 each, 2 per SIMD); half the
+//                  vector-L1 bytes per FLOP of the 128x128 tile
+// Out-of-range rows are clamped, not predicated (they only feed accumulator
+// entries the epilogue never stores), so the loads are branch-free.  Tiles are
+// remapped so blocks sharing a weight panel run on the same XCD (one L2).
+//
+// Stream-K: P blocks split the tiles x k-slabs iteration space evenly.  A
+// block whose range covers only part of a tile stores its fp32 partial; a
+// second kernel sums each split tile's partials in block order
+// (deterministic) and runs the epilogue.  Blocks never communicate inside a
+// kernel: on this multi-XCD part the per-XCD L2s are not coherent, and a
+// device-scope fence costs an L2 writeback + invalidate.
 #include "rh_device.h"
 #include "rh_kernels.h"
 
 namespace rh {
 namespace {
 
-constexpr int BN = 128, BK = 64, LDK = BK + 8;
+constexpr int BK = 64, LDK = BK + 8;
+constexpr int SK_P = 256;  // stream-K blocks: one per CU
 
-template <int BM, int EPI>
-__global__ __launch_bounds__(256) void gemm_nt_kernel(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) f16 sW[2][BN * LDK];
-    __shared__ __attribute__((aligned(16))) f16 sX[2][BM * LDK];
-    constexpr int WCH = BN * BK / 8 / 256;  // 16-byte chunks per thread, weight slab
-    constexpr int XCH = BM * BK / 8 / 256;  // 16-byte chunks per thread, token slab
-    constexpr int MT = BM / 64;             // 32-token MFMA tiles per wave
+template <int TN, int TM>
+struct Frag {
+    f32x16 v[TN][TM];
+};
 
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int wn = wv & 1, wm = wv >> 1;
-    const int N = a.N, M = a.M, K = a.K;
-    const int nbN = (N + BN - 1) / BN, nbM = (M + BM - 1) / BM;
-    const int logical = xcd_remap(blockIdx.x, nbN * nbM);
-    const int nb = logical / nbM, mb = logical - nb * nbM;
-    const int n0 = nb * BN, m0 = mb * BM;
+// ---------------------------------------------------------------------------
+// Tile policy 1 (LdsTile): both operands staged through LDS; 2 x 2 waves, each
+// TN x TM tiles of 32x32.  Block = (64 TN) features x (64 TM) tokens.
+// Rows past N or M are clamped to the last valid row instead of predicated:
+// they only feed accumulator rows/columns the epilogue never stores, and the
+// loads stay branch-free.  Fragments are double-buffered in registers so the
+// LDS reads of k-step kk+1 are in flight under the MFMAs of step kk.
+template <int TN, int TM>
+struct LdsTile {
+    static constexpr int BN = 64 * TN, BM = 64 * TM, NT = 256, FTN = TN, FTM = TM;
+    static constexpr int WCH = BN * BK / 8 / NT, XCH = BM * BK / 8 / NT;
+    using Acc = Frag<TN, TM>;
+    struct Smem {
+        f16 w[2][BN * LDK];
+        f16 x[2][BM * LDK];
+    };
+    __device__ static int nw(int n0) { return n0 + ((threadIdx.x >> 6) & 1) * 32 * TN; }
+    __device__ static int mw(int m0) { return m0 + (threadIdx.x >> 7) * 32 * TM; }
 
-    f16x8 rw[WCH], rx[XCH];
-    const f16x8 zero8 = {};
-    auto gload = [&](int k0) {
+    __device__ static void run(const GemmArgs& a, int n0, int m0, int kb, int ke, Acc& acc, Smem& sm) {
+        const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+        const int wn = wv & 1, wm = wv >> 1;
+        const int K = a.K;
+        const f16* wp[WCH];
+        const f16* xp[XCH];
+        int wo[WCH], xo[XCH];
 #pragma unroll
         for (int p = 0; p < WCH; ++p) {
-            const int c = tid + 256 * p, row = c >> 3, col = (c & 7) * 8;
-            const int n = n0 + row;
-            rw[p] = n < N ? *(const f16x8*)(a.W + (size_t)n * K + k0 + col) : zero8;
+            const int c = tid + NT * p, row = c >> 3, col = (c & 7) * 8;
+            wp[p] = a.W + (size_t)min(n0 + row, a.N - 1) * K + col;
+            wo[p] = row * LDK + col;
         }
 #pragma unroll
         for (int p = 0; p < XCH; ++p) {
-            const int c = tid + 256 * p, row = c >> 3, col = (c & 7) * 8;
-            const int m = m0 + row;
-            rx[p] = m < M ? *(const f16x8*)(a.X + (size_t)m * K + k0 + col) : zero8;
+            const int c = tid + NT * p, row = c >> 3, col = (c & 7) * 8;
+            xp[p] = a.X + (size_t)min(m0 + row, a.M - 1) * K + col;
+            xo[p] = row * LDK + col;
         }
-    };
-    auto sstore = [&](int buf) {
+        int ao[TN], bo[TM];
 #pragma unroll
-        for (int p = 0; p < WCH; ++p) {
-            const int c = tid + 256 * p, row = c >> 3, col = (c & 7) * 8;
-            *(f16x8*)&sW[buf][row * LDK + col] = rw[p];
-        }
+        for (int i = 0; i < TN; ++i) ao[i] = (wn * 32 * TN + i * 32 + (lane & 31)) * LDK + 8 * (lane >> 5);
 #pragma unroll
-        for (int p = 0; p < XCH; ++p) {
-            const int c = tid + 256 * p, row = c >> 3, col = (c & 7) * 8;
-            *(f16x8*)&sX[buf][row * LDK + col] = rx[p];
-        }
-    };
-
-    f32x16 acc[2][MT];
+        for (int j = 0; j < TM; ++j) bo[j] = (wm * 32 * TM + j * 32 + (lane & 31)) * LDK + 8 * (lane >> 5);
+        f16x8 rw[WCH], rx[XCH];
+        auto gload = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+            for (int p = 0; p < WCH; ++p) rw[p] = *(const f16x8*)(wp[p] + k0);
 #pragma unroll
-        for (int j = 0; j < MT; ++j) acc[i][j] = f32x16{};
-
-    const int KT = K / BK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < KT) gload((kt + 1) * BK);
-        const f16* ws = sW[cur];
-        const f16* xs = sX[cur];
+            for (int p = 0; p < XCH; ++p) rx[p] = *(const f16x8*)(xp[p] + k0);
+        };
+        auto sstore = [&](f16* sw, f16* sx) {
 #pragma unroll
-        for (int kk = 0; kk < BK / 16; ++kk) {
-            const int kc = kk * 16 + 8 * (lane >> 5);
-            f16x8 af[2], bf[MT];
+            for (int p = 0; p < WCH; ++p) *(f16x8*)&sw[wo[p]] = rw[p];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                af[i] = *(const f16x8*)&ws[(wn * 64 + i * 32 + (lane & 31)) * LDK + kc];
+            for (int p = 0; p < XCH; ++p) *(f16x8*)&sx[xo[p]] = rx[p];
+        };
 #pragma unroll
-            for (int j = 0; j < MT; ++j)
-                bf[j] = *(const f16x8*)&xs[(wm * (BM / 2) + j * 32 + (lane & 31)) * LDK + kc];
+        for (int i = 0; i < TN; ++i)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < MT; ++j) acc[i][j] = mfma32(af[i], bf[j], acc[i][j]);
-        }
-        if (kt + 1 < KT) sstore(cur ^ 1);
+            for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
+        f16x8 fa[2][TN], fb[2][TM];
+        gload(kb * BK);
+        sstore(sm.w[0], sm.x[0]);
         __syncthreads();
-    }
-
-    // ---- epilogue: lane holds token m = .. + lane%32 and, per q4, the four
-    // consecutive features n = .. + 8*q4 + 4*(lane/32) + (0..3).
+        for (int kt = kb; kt < ke; ++kt) {
+            const bool odd = ((kt - kb) & 1) != 0;
+            const f16* ws = odd ? sm.w[1] : sm.w[0];
+            const f16* xs = odd ? sm.x[1] : sm.x[0];
+            if (kt + 1 < ke) gload((kt + 1) * BK);
 #pragma unroll
-    for (int j = 0; j < MT; ++j) {
-        const int m = m0 + wm * (BM / 2) + j * 32 + (lane & 31);
+            for (int i = 0; i < TN; ++i) fa[0][i] = *(const f16x8*)&ws[ao[i]];
+#pragma unroll
+            for (int j = 0; j < TM; ++j) fb[0][j] = *(const f16x8*)&xs[bo[j]];
+#pragma unroll
+            for (int kk = 0; kk < BK / 16; ++kk) {
+                const int cur = kk & 1, nxt = cur ^ 1;
+                if (kk + 1 < BK / 16) {
+#pragma unroll
+                    for (int i = 0; i < TN; ++i) fa[nxt][i] = *(const f16x8*)&ws[ao[i] + (kk + 1) * 16];
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) fb[nxt][j] = *(const f16x8*)&xs[bo[j] + (kk + 1) * 16];
+                }
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) acc.v[i][j] = mfma32(fa[cur][i], fb[cur][j], acc.v[i][j]);
+            }
+            if (kt + 1 < ke) {
+                if (odd) sstore(sm.w[0], sm.x[0]);
+                else sstore(sm.w[1], sm.x[1]);
+            }
+            __syncthreads();
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Tile policy 1c (GTile): LDS-staged like LdsTile with a WGN x WGM wave grid,
+// each wave TN x TM tiles of 32x32.  256x256 with 8 waves (2 per SIMD, each
+// 128x64) halves the vector-L1 bytes per FLOP of a 128x128 tile while keeping
+// each wave inside 128 accumulator + 128 architectural registers.
+template <int WGN, int WGM, int TN, int TM>
+struct GTile {
+    static constexpr int BN = 32 * TN * WGN, BM = 32 * TM * WGM, NT = 64 * WGN * WGM;
+    static constexpr int FTN = TN, FTM = TM;
+    static constexpr int WCH = BN * BK / 8 / NT, XCH = BM * BK / 8 / NT;
+    static_assert(WCH * NT * 8 == BN * BK && XCH * NT * 8 == BM * BK, "slab must split evenly");
+    using Acc = Frag<TN, TM>;
+    struct Smem {
+        f16 w[2][BN * LDK];
+        f16 x[2][BM * LDK];
+    };
+    __device__ static int nw(int n0) { return n0 + ((threadIdx.x >> 6) % WGN) * 32 * TN; }
+    __device__ static int mw(int m0) { return m0 + ((threadIdx.x >> 6) / WGN) * 32 * TM; }
+
+    __device__ static void run(const GemmArgs& a, int n0, int m0, int kb, int ke, Acc& acc, Smem& sm) {
+        const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+        const int wn = wv % WGN, wm = wv / WGN;
+        const int K = a.K;
+        const f16* wp[WCH];
+        const f16* xp[XCH];
+        int wo[WCH], xo[XCH];
+#pragma unroll
+        for (int p = 0; p < WCH; ++p) {
+            const int c = tid + NT * p, row = c >> 3, col = (c & 7) * 8;
+            wp[p] = a.W + (size_t)min(n0 + row, a.N - 1) * K + col;
+            wo[p] = row * LDK + col;
+        }
+#pragma unroll
+        for (int p = 0; p < XCH; ++p) {
+            const int c = tid + NT * p, row = c >> 3, col = (c & 7) * 8;
+            xp[p] = a.X + (size_t)min(m0 + row, a.M - 1) * K + col;
+            xo[p] = row * LDK + col;
+        }
+        int ao[TN], bo[TM];
+#pragma unroll
+        for (int i = 0; i < TN; ++i) ao[i] = (wn * 32 * TN + i * 32 + (lane & 31)) * LDK + 8 * (lane >> 5);
+#pragma unroll
+        for (int j = 0; j < TM; ++j) bo[j] = (wm * 32 * TM + j * 32 + (lane & 31)) * LDK + 8 * (lane >> 5);
+        f16x8 rw[WCH], rx[XCH];
+        auto gload = [&](int k0) {
+#pragma unroll
+            for (int p = 0; p < WCH; ++p) rw[p] = *(const f16x8*)(wp[p] + k0);
+#pragma unroll
+            for (int p = 0; p < XCH; ++p) rx[p] = *(const f16x8*)(xp[p] + k0);
+        };
+        auto sstore = [&](f16* sw, f16* sx) {
+#pragma unroll
+            for (int p = 0; p < WCH; ++p) *(f16x8*)&sw[wo[p]] = rw[p];
+#pragma unroll
+            for (int p = 0; p < XCH; ++p) *(f16x8*)&sx[xo[p]] = rx[p];
+        };
+        auto slab = [&](const f16* ws, const f16* xs) {
+            f16x8 fa[2][TN], fb[2][TM];
+#pragma unroll
+            for (int i = 0; i < TN; ++i) fa[0][i] = *(const f16x8*)&ws[ao[i]];
+#pragma unroll
+            for (int j = 0; j < TM; ++j) fb[0][j] = *(const f16x8*)&xs[bo[j]];
+#pragma unroll
+            for (int kk = 0; kk < BK / 16; ++kk) {
+                const int cur = kk & 1, nxt = cur ^ 1;
+                if (kk + 1 < BK / 16) {
+#pragma unroll
+                    for (int i = 0; i < TN; ++i) fa[nxt][i] = *(const f16x8*)&ws[ao[i] + (kk + 1) * 16];
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) fb[nxt][j] = *(const f16x8*)&xs[bo[j] + (kk + 1) * 16];
+                }
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) acc.v[i][j] = mfma32(fa[cur][i], fb[cur][j], acc.v[i][j]);
+            }
+        };
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
+        const int klast = (ke - 1) * BK;
+        gload(kb * BK);
+        sstore(sm.w[0], sm.x[0]);
+        __syncthreads();
+        int kt = kb;
+        for (; kt + 1 < ke; kt += 2) {
+            gload((kt + 1) * BK);
+            __builtin_amdgcn_sched_barrier(0);
+            slab(sm.w[0], sm.x[0]);
+            sstore(sm.w[1], sm.x[1]);
+            __syncthreads();
+            gload(min((kt + 2) * BK, klast));
+            __builtin_amdgcn_sched_barrier(0);
+            slab(sm.w[1], sm.x[1]);
+            sstore(sm.w[0], sm.x[0]);
+            __syncthreads();
+        }
+        if (kt < ke) {
+            slab(sm.w[0], sm.x[0]);
+            __syncthreads();
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Tile policy 1b (LdsTile2): LdsTile with the global loads issued two k-slabs
+// ahead (two register sets), so ~2x the bytes are in flight per block to
+// cover L2/MALL latency.  Slab s: global -> register set s%2 -> LDS buffer
+// s%2 -> MFMA.
+template <int TN, int TM>
+struct LdsTile2 : LdsTile<TN, TM> {
+    using B = LdsTile<TN, TM>;
+    using typename B::Acc;
+    using typename B::Smem;
+    static constexpr int BN = B::BN, BM = B::BM, NT = B::NT, FTN = TN, FTM = TM;
+    static constexpr int WCH = B::WCH, XCH = B::XCH;
+
+    __device__ static void run(const GemmArgs& a, int n0, int m0, int kb, int ke, Acc& acc, Smem& sm) {
+        const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+        const int wn = wv & 1, wm = wv >> 1;
+        const int K = a.K;
+        const f16* wp[WCH];
+        const f16* xp[XCH];
+        int wo[WCH], xo[XCH];
+#pragma unroll
+        for (int p = 0; p < WCH; ++p) {
+            const int c = tid + NT * p, row = c >> 3, col = (c & 7) * 8;
+            wp[p] = a.W + (size_t)min(n0 + row, a.N - 1) * K + col;
+            wo[p] = row * LDK + col;
+        }
+#pragma unroll
+        for (int p = 0; p < XCH; ++p) {
+            const int c = tid + NT * p, row = c >> 3, col = (c & 7) * 8;
+            xp[p] = a.X + (size_t)min(m0 + row, a.M - 1) * K + col;
+            xo[p] = row * LDK + col;
+        }
+        int ao[TN], bo[TM];
+#pragma unroll
+        for (int i = 0; i < TN; ++i) ao[i] = (wn * 32 * TN + i * 32 + (lane & 31)) * LDK + 8 * (lane >> 5);
+#pragma unroll
+        for (int j = 0; j < TM; ++j) bo[j] = (wm * 32 * TM + j * 32 + (lane & 31)) * LDK + 8 * (lane >> 5);
+        f16x8 rw0[WCH], rx0[XCH], rw1[WCH], rx1[XCH];
+        auto gload = [&](f16x8 (&rw)[WCH], f16x8 (&rx)[XCH], int k0) {
+#pragma unroll
+            for (int p = 0; p < WCH; ++p) rw[p] = *(const f16x8*)(wp[p] + k0);
+#pragma unroll
+            for (int p = 0; p < XCH; ++p) rx[p] = *(const f16x8*)(xp[p] + k0);
+        };
+        auto sstore = [&](const f16x8 (&rw)[WCH], const f16x8 (&rx)[XCH], f16* sw, f16* sx) {
+#pragma unroll
+            for (int p = 0; p < WCH; ++p) *(f16x8*)&sw[wo[p]] = rw[p];
+#pragma unroll
+            for (int p = 0; p < XCH; ++p) *(f16x8*)&sx[xo[p]] = rx[p];
+        };
+        auto slab = [&](const f16* ws, const f16* xs) {
+            f16x8 fa[2][TN], fb[2][TM];
+#pragma unroll
+            for (int i = 0; i < TN; ++i) fa[0][i] = *(const f16x8*)&ws[ao[i]];
+#pragma unroll
+            for (int j = 0; j < TM; ++j) fb[0][j] = *(const f16x8*)&xs[bo[j]];
+#pragma unroll
+            for (int kk = 0; kk < BK / 16; ++kk) {
+                const int cur = kk & 1, nxt = cur ^ 1;
+                if (kk + 1 < BK / 16) {
+#pragma unroll
+                    for (int i = 0; i < TN; ++i) fa[nxt][i] = *(const f16x8*)&ws[ao[i] + (kk + 1) * 16];
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) fb[nxt][j] = *(const f16x8*)&xs[bo[j] + (kk + 1) * 16];
+                }
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) acc.v[i][j] = mfma32(fa[cur][i], fb[cur][j], acc.v[i][j]);
+            }
+        };
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
+        // Prefetches are unconditional (k clamped to the last slab; a repeat
+        // load is simply never used) so the wait-count tracking stays exact.
+        const int klast = (ke - 1) * BK;
+        gload(rw0, rx0, kb * BK);
+        gload(rw1, rx1, min((kb + 1) * BK, klast));
+        sstore(rw0, rx0, sm.w[0], sm.x[0]);
+        __syncthreads();
+        int kt = kb;
+        for (; kt + 1 < ke; kt += 2) {
+            // slab kt (even) in LDS 0; set 0 free -> prefetch kt+2; then stage kt+1 (set 1) to LDS 1
+            gload(rw0, rx0, min((kt + 2) * BK, klast));
+            __builtin_amdgcn_sched_barrier(0);  // keep the prefetch issued before the MFMAs
+            slab(sm.w[0], sm.x[0]);
+            sstore(rw1, rx1, sm.w[1], sm.x[1]);
+            __syncthreads();
+            // slab kt+1 (odd) in LDS 1; set 1 free -> prefetch kt+3; then stage kt+2 (set 0) to LDS 0
+            gload(rw1, rx1, min((kt + 3) * BK, klast));
+            __builtin_amdgcn_sched_barrier(0);
+            slab(sm.w[1], sm.x[1]);
+            sstore(rw0, rx0, sm.w[0], sm.x[0]);
+            __syncthreads();
+        }
+        if (kt < ke) {
+            slab(sm.w[0], sm.x[0]);
+            __syncthreads();
+        }
+    }
+};
+
+// (nw, mw): the wave's first feature row and token.  Lane holds token
+// m = mw + j*32 + lane%32 and, per q4, the four consecutive features
+// n = nw + i*32 + 8*q4 + 4*(lane/32) + (0..3).
+template <int TN, int TM, int EPI>
+__device__ __forceinline__ void epilogue(const GemmArgs& a, int nw, int mw,
+                                         const Frag<TN, TM>& acc) {
+    const int lane = threadIdx.x & 63;
+    const int N = a.N, M = a.M;
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+        const int m = mw + j * 32 + (lane & 31);
         if (m >= M) continue;
         if constexpr (EPI == EPI_SWIGLU) {
-            // The wave's 64 weight rows are 32 W1 rows (tile 0) followed by the
-            // matching 32 W3 rows (tile 1) of feature block fb.
-            const int fb = (n0 + wn * 64) >> 6;
+            // Tiles (i, i+1), i even, are 32 W1 rows and the matching 32 W3
+            // rows of one 64-row block of the interleaved W1|W3 weight.
 #pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                const int f = 32 * fb + 8 * q4 + 4 * (lane >> 5);
-                f16x4 g;
+            for (int i = 0; i < TN; i += 2) {
+                const int fb = (nw + i * 32) >> 6;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float h1 = acc[0][j][4 * q4 + r], h3 = acc[1][j][4 * q4 + r];
-                    g[r] = (f16)(silu_f(h1) * h3);
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const int f = 32 * fb + 8 * q4 + 4 * (lane >> 5);
+                    if (f >= a.ldo) continue;
+                    f16x4 g;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float h1 = acc.v[i][j][4 * q4 + r], h3 = acc.v[i + 1][j][4 * q4 + r];
+                        g[r] = (f16)(silu_f(h1) * h3);
+                    }
+                    *(f16x4*)(a.out_f16 + (size_t)m * a.ldo + f) = g;
                 }
-                *(f16x4*)(a.out_f16 + (size_t)m * a.ldo + f) = g;
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TN; ++i)
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) {
-                    const int n = n0 + wn * 64 + i * 32 + 8 * q4 + 4 * (lane >> 5);
+                    const int n = nw + i * 32 + 8 * q4 + 4 * (lane >> 5);
                     if (n >= N) continue;
-                    float v0 = acc[i][j][4 * q4 + 0], v1 = acc[i][j][4 * q4 + 1];
-                    float v2 = acc[i][j][4 * q4 + 2], v3 = acc[i][j][4 * q4 + 3];
+                    float v0 = acc.v[i][j][4 * q4 + 0], v1 = acc.v[i][j][4 * q4 + 1];
+                    float v2 = acc.v[i][j][4 * q4 + 2], v3 = acc.v[i][j][4 * q4 + 3];
                     if constexpr (EPI == EPI_F32) {
                         if (a.softcap > 0.f) {
                             const float c = a.softcap, ic = 1.0f / c;
@@ -169,20 +422,136 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmArgs a) {
     }
 }
 
-template <int EPI>
-hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
-    const int nbN = (a.N + BN - 1) / BN;
-    const int tiles128 = nbN * ((a.M + 127) / 128);
-    if (tiles128 >= 512) {
-        hipLaunchKernelGGL((gemm_nt_kernel<128, EPI>), dim3(tiles128), dim3(256), 0, st, a);
+template <class Tl, int EPI, bool SK>
+__global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long long T) {
+    __shared__ __attribute__((aligned(16))) typename Tl::Smem sm;
+    const int nbN = (a.N + Tl::BN - 1) / Tl::BN, nbM = (a.M + Tl::BM - 1) / Tl::BM;
+    const int KT = a.K / BK;
+    typename Tl::Acc acc;
+    if constexpr (!SK) {
+        const int t = xcd_remap(blockIdx.x, nbN * nbM);
+        const int nb = t / nbM, mb = t - nb * nbM;
+        Tl::run(a, nb * Tl::BN, mb * Tl::BM, 0, KT, acc, sm);
+        epilogue<Tl::FTN, Tl::FTM, EPI>(a, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
     } else {
-        const int tiles64 = nbN * ((a.M + 63) / 64);
-        hipLaunchKernelGGL((gemm_nt_kernel<64, EPI>), dim3(tiles64), dim3(256), 0, st, a);
+        constexpr int TN = Tl::FTN, TM = Tl::FTM, NT = Tl::NT;
+        constexpr int NV = TN * TM * 4;  // f32x4 per thread per partial tile
+        const int tid = threadIdx.x;
+        const int lp = xcd_remap(blockIdx.x, P);
+        const long long it0 = (long long)lp * T / P, it1 = (long long)(lp + 1) * T / P;
+        long long it = it0;
+        while (it < it1) {
+            const int tile = (int)(it / KT);
+            const int kb = (int)(it - (long long)tile * KT);
+            const int ke = (int)((long long)KT < kb + (it1 - it) ? (long long)KT : kb + (it1 - it));
+            const int nb = tile / nbM, mb = tile - nb * nbM;
+            const int n0 = nb * Tl::BN, m0 = mb * Tl::BM;
+            Tl::run(a, n0, m0, kb, ke, acc, sm);
+            if (kb == 0 && ke == KT) {
+                epilogue<TN, TM, EPI>(a, Tl::nw(n0), Tl::mw(m0), acc);
+            } else {
+                // A block's first segment goes to slot 0, its last to slot 1;
+                // the fixup kernel merges them once this kernel has finished.
+                const int slot = (it == it0) ? 0 : 1;
+                f32x4* mine = (f32x4*)a.sk_part + ((size_t)(lp * 2 + slot) * NV) * NT + tid;
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            mine[(size_t)((i * TM + j) * 4 + q) * NT] =
+                                f32x4{acc.v[i][j][4 * q], acc.v[i][j][4 * q + 1], acc.v[i][j][4 * q + 2],
+                                      acc.v[i][j][4 * q + 3]};
+            }
+            it = (long long)tile * KT + ke;
+        }
+    }
+}
+
+// Stream-K fixup: one block per tile.  A tile covered by a single block was
+// finished by gemm_kernel; for a split tile, sum the partials of its
+// contributing blocks in block order (deterministic) and run the epilogue.
+template <class Tl, int EPI>
+__global__ __launch_bounds__(Tl::NT) void gemm_fixup_kernel(GemmArgs a, int P, long long T) {
+    constexpr int TN = Tl::FTN, TM = Tl::FTM, NT = Tl::NT;
+    constexpr int NV = TN * TM * 4;
+    const int nbM = (a.M + Tl::BM - 1) / Tl::BM;
+    const int KT = a.K / BK;
+    const int tile = blockIdx.x, tid = threadIdx.x;
+    const long long tb = (long long)tile * KT, te = tb + KT;
+    const int pf = (int)(((tb + 1) * P - 1) / T), pl = (int)((te * P - 1) / T);
+    if (pf == pl) return;
+    typename Tl::Acc acc;
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
+    for (int c = pf; c <= pl; ++c) {
+        const int cslot = ((long long)c * T / P >= tb) ? 0 : 1;
+        const f32x4* part = (const f32x4*)a.sk_part + ((size_t)(c * 2 + cslot) * NV) * NT + tid;
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4 o = part[(size_t)((i * TM + j) * 4 + q) * NT];
+                    acc.v[i][j][4 * q] += o[0];
+                    acc.v[i][j][4 * q + 1] += o[1];
+                    acc.v[i][j][4 * q + 2] += o[2];
+                    acc.v[i][j][4 * q + 3] += o[3];
+                }
+    }
+    const int nb = tile / nbM, mb = tile - nb * nbM;
+    epilogue<TN, TM, EPI>(a, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
+}
+
+template <class Tl, int EPI>
+hipError_t launch_tile(const GemmArgs& a, bool sk, hipStream_t st) {
+    const int nbN = (a.N + Tl::BN - 1) / Tl::BN, nbM = (a.M + Tl::BM - 1) / Tl::BM;
+    const int tiles = nbN * nbM;
+    const long long T = (long long)tiles * (a.K / BK);
+    if (sk) {
+        if (!a.sk_part || (size_t)SK_P * 2 * Tl::BN * Tl::BM > a.sk_part_floats) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((gemm_kernel<Tl, EPI, true>), dim3(SK_P), dim3(Tl::NT), 0, st, a, SK_P, T);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((gemm_fixup_kernel<Tl, EPI>), dim3(tiles), dim3(Tl::NT), 0, st, a, SK_P, T);
+    } else {
+        hipLaunchKernelGGL((gemm_kernel<Tl, EPI, false>), dim3(tiles), dim3(Tl::NT), 0, st, a, 1, T);
     }
     return hipGetLastError();
 }
 
+template <int EPI>
+hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
+    int cfg = a.force_cfg;
+    if (cfg == GCFG_AUTO) {
+        // Picked from measured sweeps over the forward's shapes (M = 512,
+        // 2048, 8192 rows; N = 3D, D, 2F, V; K = D or F) on MI355X.
+        const int t256 = ((a.N + 255) / 256) * ((a.M + 255) / 256);
+        const bool sk_ok = a.sk_part && (size_t)SK_P * 2 * 256 * 256 <= a.sk_part_floats;
+        if (t256 >= 600 && a.N >= 16384) cfg = GCFG_G8_256x256;
+        else if (t256 >= 300) cfg = sk_ok ? GCFG_G8_256x256_SK : GCFG_G8_256x256;
+        else if (a.K >= 8192 && sk_ok) cfg = t256 >= 100 ? GCFG_G8_256x256_SK : GCFG_P2_128x128_SK;
+        else if (a.N >= 16384 && t256 >= 200) cfg = GCFG_G8_256x256;
+        else if (t256 < 64 && sk_ok) cfg = GCFG_P2_128x128_SK;
+        else cfg = GCFG_P2_128x128;
+    }
+    switch (cfg) {
+        case GCFG_128x128: return launch_tile<LdsTile<2, 2>, EPI>(a, false, st);
+        case GCFG_P2_128x128: return launch_tile<LdsTile2<2, 2>, EPI>(a, false, st);
+        case GCFG_P2_128x128_SK: return launch_tile<LdsTile2<2, 2>, EPI>(a, true, st);
+        case GCFG_G8_256x256: return launch_tile<GTile<2, 4, 4, 2>, EPI>(a, false, st);
+        case GCFG_G8_256x256_SK: return launch_tile<GTile<2, 4, 4, 2>, EPI>(a, true, st);
+    }
+    return hipErrorInvalidValue;
+}
+
 }  // namespace
+
+size_t gemm_sk_part_floats() { return (size_t)SK_P * 2 * 256 * 256; }
 
 hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
     if (a.K % BK != 0 || a.N % 4 != 0 || a.M <= 0) return hipErrorInvalidValue;

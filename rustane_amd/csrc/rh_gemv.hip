@@ -2,9 +2,11 @@
 //
 // y[b][n] = sum_k W[n][k] * x[b][k] with W [N, K] fp16 streamed exactly once.
 // A block owns 16 weight rows (two 16-row tiles for the SwiGLU pair) and its
-// 4 waves split K in 128-wide chunks; each lane issues 64 contiguous bytes per
-// row tile per chunk, and the next chunk is loaded before the current one is
-// consumed.  The product is done on 16x16x32 MFMA with the tokens as the B
+// 4 waves split K in 128-wide chunks.  The MFMA's k order within a chunk is
+// k = 32u + 8g + e (u = MFMA step, g = lane group, e = element), so the four
+// lane groups of one row read 64 contiguous bytes per load instruction; the
+// next chunk is loaded before the current one is consumed. 
+// The product is done on 16x16x32 MFMA with the tokens as the B
 // operand (rows >= B are zero), which keeps the VALU free and handles B 1..16
 // with one kernel; MFMA throughput is far above what HBM can feed.  Epilogues
 // mirror the prefill GEMM's: RoPE + KV-cache append, residual, SwiGLU, logits.
@@ -34,10 +36,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
         wvalid[t] = rows[t] + r < N;
-        wp[t] = a.W + (size_t)(wvalid[t] ? rows[t] + r : 0) * K + 32 * g;
+        wp[t] = a.W + (size_t)(wvalid[t] ? rows[t] + r : 0) * K + 8 * g;
     }
     const bool xvalid = r < a.B;
-    const f16* xp = a.X + (size_t)(xvalid ? r : 0) * K + 32 * g;
+    const f16* xp = a.X + (size_t)(xvalid ? r : 0) * K + 8 * g;
 
     f32x4 acc[RT];
 #pragma unroll
@@ -51,9 +53,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         for (int t = 0; t < RT; ++t)
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                wr[t][u] = wvalid[t] ? *(const f16x8*)(wp[t] + off + 8 * u) : z;
+                wr[t][u] = wvalid[t] ? *(const f16x8*)(wp[t] + off + 32 * u) : z;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) xr[u] = xvalid ? *(const f16x8*)(xp + off + 8 * u) : z;
+        for (int u = 0; u < 4; ++u) xr[u] = xvalid ? *(const f16x8*)(xp + off + 32 * u) : z;
     };
     auto mac = [&](const f16x8 (&wr)[RT][4], const f16x8 (&xr)[4]) {
 #pragma unroll

@@ -26,7 +26,22 @@ struct GemmArgs {
     f16* vc;         // [B][H][ctx][hd]
     const float2* rope;  // [pos][hd/2] (cos, sin)
     int S, D, H, hd, ctx, pos0;
+    // Stream-K workspace (optional): fp32 partial tiles.
+    float* sk_part;
+    size_t sk_part_floats;
+    int force_cfg;  // 0 = heuristic; otherwise a GemmCfg value (tuning)
 };
+// Tile configurations of the prefill GEMM.
+enum GemmCfg {
+    GCFG_AUTO = 0,
+    GCFG_128x128 = 1,        // 4 waves 2x2, both operands via LDS, one slab ahead
+    GCFG_P2_128x128 = 2,     // same tile, two slabs of global prefetch
+    GCFG_P2_128x128_SK = 3,  // ... stream-K
+    GCFG_G8_256x256 = 4,     // 8 waves 2x4 (128x64 each), 256x256 tile
+    GCFG_G8_256x256_SK = 5,  // ... stream-K
+};
+// Floats of stream-K workspace any prefill GEMM needs.
+size_t gemm_sk_part_floats();
 hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st);
 
 // ---------------- attention ----------------
@@ -35,7 +50,7 @@ hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st);
 hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* out, int B, int H,
                                int S, int hd, int ctx, hipStream_t st);
 // Decode attention over positions 0..*pos (the current token is at *pos):
-// q [B][H*hd]; per (b, h, chunk) partial (m, l, o[hd]) then a combine.
+// q [B][H*hd]; per (b, h, chunk) partial (m, l, o[hd]), then a merge kernel.
 hipError_t launch_attn_decode(const f16* q, const f16* k, const f16* v, const int* pos,
                               float* part_m, float* part_l, float* part_o, f16* out, int B, int H,
                               int hd, int ctx, hipStream_t st);

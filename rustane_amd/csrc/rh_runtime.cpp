@@ -82,6 +82,10 @@ struct rh_ctx {
     float* staging = nullptr;
     size_t staging_elems = 0;
 
+    // stream-K workspace of the prefill GEMMs (fp32 partial tiles)
+    float* sk_part = nullptr;
+    size_t sk_part_floats = 0;
+
     Prof prof[RH_K_NCLASSES];
 };
 
@@ -167,6 +171,10 @@ int ensure_workspace(rh_ctx* ctx, int M) {
     RCK(dalloc(ctx, &ctx->mean, m));
     RCK(dalloc(ctx, &ctx->d_tok, m));
     RCK(dalloc(ctx, &ctx->d_tgt, m));
+    if (!ctx->sk_part) {
+        ctx->sk_part_floats = rh::gemm_sk_part_floats();
+        RCK(dalloc(ctx, &ctx->sk_part, ctx->sk_part_floats));
+    }
     ctx->ws_M = M;
     return RH_OK;
 }
@@ -208,6 +216,11 @@ int timed(rh_ctx* ctx, int cls, Fn&& fn) {
             return fail(ctx, RH_EDEVICE, std::string("launch ") + #expr + ": " + hipGetErrorString(e_)); \
     } while (0)
 
+void set_sk(const rh_ctx* ctx, rh::GemmArgs& g) {
+    g.sk_part = ctx->sk_part;
+    g.sk_part_floats = ctx->sk_part_floats;
+}
+
 // ---- the forward token loop -----------------------------------------------
 // kv_k/kv_v: per-layer K/V destination base and ctx stride.  For a plain
 // forward they are the scratch buffers (ctx = S); for a prefill they are the
@@ -228,6 +241,7 @@ int enqueue_body(rh_ctx* ctx, int B, int S, bool to_cache) {
         g.W = W.wqkv; g.X = ctx->xn; g.M = M; g.N = 3 * D; g.K = D;
         g.q = ctx->q; g.kc = kc; g.vc = vc; g.rope = ctx->rope;
         g.S = S; g.D = D; g.H = c.heads; g.hd = c.head_dim; g.ctx = kvctx; g.pos0 = 0;
+        set_sk(ctx, g);
         RCK(timed(ctx, RH_K_GEMM_QKV, [&] { return rh::launch_gemm(rh::EPI_QKV, g, st); }));
         RCK(timed(ctx, RH_K_ATTN, [&] {
             return rh::launch_attn_prefill(ctx->q, kc, vc, ctx->attn, B, c.heads, S, c.head_dim, kvctx, st);
@@ -235,15 +249,18 @@ int enqueue_body(rh_ctx* ctx, int B, int S, bool to_cache) {
         g = rh::GemmArgs{};
         g.W = W.wo; g.X = ctx->attn; g.M = M; g.N = D; g.K = D;
         g.out_f32 = ctx->x; g.ldo = D; g.alpha = alpha;
+        set_sk(ctx, g);
         RCK(timed(ctx, RH_K_GEMM_WO, [&] { return rh::launch_gemm(rh::EPI_RESID, g, st); }));
         LCK(rh::launch_rmsnorm(ctx->x, W.g2, ctx->xn, M, D, c.rms_eps, st));
         g = rh::GemmArgs{};
         g.W = W.w13; g.X = ctx->xn; g.M = M; g.N = 2 * F; g.K = D;
         g.out_f16 = ctx->gate; g.ldo = F;
+        set_sk(ctx, g);
         RCK(timed(ctx, RH_K_GEMM_W13, [&] { return rh::launch_gemm(rh::EPI_SWIGLU, g, st); }));
         g = rh::GemmArgs{};
         g.W = W.w2; g.X = ctx->gate; g.M = M; g.N = D; g.K = F;
         g.out_f32 = ctx->x; g.ldo = D; g.alpha = alpha;
+        set_sk(ctx, g);
         RCK(timed(ctx, RH_K_GEMM_W2, [&] { return rh::launch_gemm(rh::EPI_RESID, g, st); }));
     }
     return RH_OK;
@@ -257,6 +274,7 @@ int enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss) {
     rh::GemmArgs g{};
     g.W = ctx->embed; g.X = ctx->xn; g.M = M; g.N = c.vocab; g.K = D;
     g.out_f32 = ctx->logits; g.ldo = c.vocab; g.softcap = c.softcap;
+    set_sk(ctx, g);
     RCK(timed(ctx, RH_K_GEMM_LOGITS, [&] { return rh::launch_gemm(rh::EPI_F32, g, st); }));
     if (with_loss) {
         LCK(rh::launch_cross_entropy(ctx->logits, ctx->d_tgt, ctx->tok_loss, M, c.vocab, ctx->d_err, st));
