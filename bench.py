@@ -52,6 +52,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--extra-batches", default="", help="e.g. 4,16: also time these prefill batches")
     ap.add_argument("--decode-only", action="store_true", help="skip the prefill timing")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run three 256 MiB device-to-device copies (a known-size kernel "
+                         "for scaling hardware byte counters)")
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode with eager launches instead of graph replay (profilers that "
                          "cannot follow graph capture)")
@@ -110,6 +113,14 @@ def main():
         print(json.dumps({"decode": run_decode(ctx, cfg, args, hb, E, hip_rt, stream)}), flush=True)
         return
 
+    if args.copy_calibration:
+        nb = 256 << 20
+        src, dst = hip_rt.DeviceArray((nb,), np.uint8), hip_rt.DeviceArray((nb,), np.uint8)
+        for _ in range(3):
+            hip_rt.copy_d2d(dst, src, nb)
+        hip_rt.synchronize()
+        log(f"[bench] copy calibration: 3 x {nb} bytes device-to-device")
+
     B = args.batch
     ms, wall, k_ms, k_n, loss = run_prefill(B, args.steps, args.warmup)
     ms_step = ms / args.steps
@@ -158,9 +169,10 @@ def main():
                    "hidden": cfg.hidden, "nlayers": cfg.nlayers, "heads": cfg.heads,
                    "head_dim": cfg.hd, "vocab": cfg.vocab, "seq_len": cfg.seq, "batch": B,
                    "global_batch": B, "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "mfma", "kernel": "gemm_nt_kernel<128, EPI_SWIGLU> (W1|W3 + SwiGLU)",
+        "roofline": {"bound": "mfma", "kernel": "gemm_kernel<..., EPI_SWIGLU> (W1|W3 GEMM + SwiGLU)",
                      "achieved": round(w13_tflops, 1), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(w13_tflops / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                     "frac": round(w13_tflops / PEAK_FP16_TFLOPS, 4),
+                     "traffic": measured_traffic(args.config, B, cfg.seq),
                      "flops_per_launch": w13_launch_flops,
                      "mean_launch_us": round(w13_avg_s * 1e6, 2), "launches": k_n},
         "forward_mfma": {"achieved_tflops": round(fwd_tflops, 1),
@@ -176,6 +188,19 @@ def main():
     if cpu:
         line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
+
+
+def measured_traffic(config, batch, seq):
+    """HBM bytes per launch of the W1|W3 GEMM from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes recorded in profiles/ (null when that workload has not
+    been profiled)."""
+    path = os.path.join(ROOT, "profiles", "gemm_w13_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+        return rec.get(f"{config}_b{batch}_s{seq}")
+    except (OSError, ValueError):
+        return None
 
 
 def run_decode(ctx, cfg, args, hb, E, hip_rt, stream):

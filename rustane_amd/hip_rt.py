@@ -107,5 +107,9 @@ class Event:
             pass
 
 
+def copy_d2d(dst: "DeviceArray", src: "DeviceArray", nbytes: int):
+    _ck(rt().hipMemcpy(dst.ptr, src.ptr, nbytes, D2D), "hipMemcpy D2D")
+
+
 def synchronize():
     _ck(rt().hipDeviceSynchronize(), "hipDeviceSynchronize")
