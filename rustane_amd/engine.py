@@ -271,10 +271,12 @@ class ModelForwardWorkspace:
 
 def _check(cfg: ModelConfig, tokens, targets):
     tokens = np.asarray(tokens, np.uint32)
-    assert tokens.shape == (cfg.seq,), f"tokens must be [{cfg.seq}], got {tokens.shape}"
+    if tokens.shape != (cfg.seq,):
+        raise ValueError(f"tokens must be [{cfg.seq}], got {tokens.shape}")
     if targets is not None:
         targets = np.asarray(targets, np.uint32)
-        assert targets.shape == (cfg.seq,), f"targets must be [{cfg.seq}]"
+        if targets.shape != (cfg.seq,):
+            raise ValueError(f"targets must be [{cfg.seq}], got {targets.shape}")
     return tokens, targets
 
 

@@ -7,6 +7,7 @@ and the mean cross-entropy.  They are the only numeric golden values for the
 path that the reference holds.  Sources (read as data, nothing executed):
 
   results/forward_utilization/scale_ladder.json   "loss" per probe (6 d.p.)
+                                                  and "params_b" (model.rs:109-114 count)
   results/2026-03-18_1830_param-sweep.md          loss0 column (3 d.p.)
   README.md:58                                    600m-A "loss=9.0108"
 
@@ -30,7 +31,7 @@ def main():
                   and any(f'"name": "{e["name"]}"' in x for x in lines[max(0, i - 16):i]))
         out.append({"name": e["name"], "dim": e["dim"], "hidden": e["hidden"], "heads": e["heads"],
                     "nlayers": e["nlayers"], "seq": e["seq"], "vocab": 8192, "loss": e["loss"],
-                    "decimals": 6, "source": f"{p}:{ln}"})
+                    "decimals": 6, "params_b": e["params_b"], "source": f"{p}:{ln}"})
     p = "results/2026-03-18_1830_param-sweep.md"
     for i, l in enumerate(open(os.path.join(REF, p)).read().splitlines()):
         cells = [c.strip().strip("*") for c in l.split("|")]
