@@ -17,7 +17,8 @@
  * loops with the same contracts: vsma out = a*s + b, vsub out = b - a,
  * sgemm_at C += A * B^T (beta = 1), mtrans.
  *
- * Parity pins (what checks each function; see tests/test_oracle_*.py):
+ * Parity pins (what checks each function; tests/test_oracle_kats.py and
+ * tests/test_golden_losses.py):
  *   orc_random_vec            bit-exact vs an independent numpy LCG; golden losses
  *   orc_embedding_forward     reference KATs (cpu/embedding.rs:46-94)
  *   orc_rmsnorm_*             reference KATs + closed form (cpu/rmsnorm.rs:244-369)
@@ -32,6 +33,11 @@
  *   orc_forward (body)        layer = independent numpy float64 restatement on tiny shapes;
  *                             FFN/attention branch linearity in Wo and W2
  *   orc_decode_*              decode logits at position p == orc_forward logits at p
+ *
+ * Parity unpinned: the ANE's bit-level fp16 numerics (accumulation order, its
+ * softmax) that the reference executes inside the un-vendored `ane` crate; no
+ * vectors for them exist, only the reference's tolerances, so this
+ * restatement is fp32 and the GPU path is held to those tolerances.
  */
 #ifndef RUSTANE_ORACLE_H
 #define RUSTANE_ORACLE_H
