@@ -54,3 +54,13 @@ __device__ __forceinline__ int xcd_remap(int b, int total) {
 }
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+
+// Fragment order of a [N, K] fp16 weight (rows padded to a multiple of 16,
+// K a multiple of 128): 16-row x 128-k chunks, each stored as four 1 KB
+// fragments (k/32 % 4) of 64 lanes x 8 halves, lane = 16 * (k/8 % 4) + row % 16.
+// One 16-byte-per-lane load then reads 1 KB contiguous, and the lane/k
+// assignment is the 16x16x32 MFMA operand layout (k = 32u + 8g + e).
+__host__ __device__ __forceinline__ size_t frag_off(int row, int k, int K) {
+    const size_t chunk = (size_t)(row >> 4) * (size_t)(K >> 7) + (size_t)(k >> 7);
+    return ((chunk * 4 + ((k >> 5) & 3)) * 64 + 16 * ((k >> 3) & 3) + (row & 15)) * 8 + (k & 7);
+}

@@ -5,8 +5,10 @@
 // W1/W3/W2, full_model.rs:555-567 tied logits):
 //     Y[m][n] = sum_k X[m][k] * W[n][k]
 // X is the token-major fp16 activation [M, K]; W is the weight repacked at
-// upload to [N, K] ("out x in"), so both operands stream along k.  The MFMA
-// computes the transposed tile (A = weight rows, B = token rows): each lane's
+// upload to [N, K] ("out x in") in fragment order (frag_off: 1 KB pieces of
+// 16 rows x 32 k, the decode GEMV's operand layout), so both operands stream
+// along k.  The MFMA computes the transposed tile (A = weight rows, B = token
+// rows): each lane's
 // accumulator then holds 4 consecutive output features of one token, which
 // makes the RoPE pairs (2i, 2i+1) and 16-byte fp32 stores lane-local.
 //
@@ -35,6 +37,19 @@ namespace {
 
 constexpr int BK = 64, LDK = BK + 8;
 constexpr int SK_P = 256;  // stream-K blocks: one per CU
+
+// Weight load slot c of a BN x BK slab.  W is in fragment order (frag_off):
+// 64 consecutive slots read one 1 KB fragment (16 rows x 32 k), two
+// fragments cover the slab's 64 k of a 16-row block, and the slab at k0
+// starts k0 * 16 elements further on.  Row blocks past N are clamped (their
+// rows only feed accumulator rows the epilogue never stores).  lds_off is the
+// slot's place in the row-major [BN][LDK] LDS tile.
+__device__ __forceinline__ const f16* wslot(const GemmArgs& a, int n0, int c, int& lds_off) {
+    const int sb = c >> 6, l = c & 63, rbl = sb >> 1, uu = sb & 1;
+    const int rb = min((n0 >> 4) + rbl, ((a.N + 15) >> 4) - 1);
+    lds_off = (rbl * 16 + (l & 15)) * LDK + uu * 32 + (l >> 4) * 8;
+    return a.W + (size_t)rb * a.K * 16 + uu * 512 + l * 8;
+}
 
 template <int TN, int TM>
 struct Frag {
@@ -69,9 +84,7 @@ struct LdsTile {
         int wo[WCH], xo[XCH];
 #pragma unroll
         for (int p = 0; p < WCH; ++p) {
-            const int c = tid + NT * p, row = c >> 3, col = (c & 7) * 8;
-            wp[p] = a.W + (size_t)min(n0 + row, a.N - 1) * K + col;
-            wo[p] = row * LDK + col;
+            wp[p] = wslot(a, n0, tid + NT * p, wo[p]);
         }
 #pragma unroll
         for (int p = 0; p < XCH; ++p) {
@@ -87,7 +100,7 @@ struct LdsTile {
         f16x8 rw[WCH], rx[XCH];
         auto gload = [&](int k0) {
 #pragma unroll
-            for (int p = 0; p < WCH; ++p) rw[p] = *(const f16x8*)(wp[p] + k0);
+            for (int p = 0; p < WCH; ++p) rw[p] = *(const f16x8*)(wp[p] + (size_t)k0 * 16);
 #pragma unroll
             for (int p = 0; p < XCH; ++p) rx[p] = *(const f16x8*)(xp[p] + k0);
         };
@@ -165,9 +178,7 @@ struct GTile {
         int wo[WCH], xo[XCH];
 #pragma unroll
         for (int p = 0; p < WCH; ++p) {
-            const int c = tid + NT * p, row = c >> 3, col = (c & 7) * 8;
-            wp[p] = a.W + (size_t)min(n0 + row, a.N - 1) * K + col;
-            wo[p] = row * LDK + col;
+            wp[p] = wslot(a, n0, tid + NT * p, wo[p]);
         }
 #pragma unroll
         for (int p = 0; p < XCH; ++p) {
@@ -183,7 +194,7 @@ struct GTile {
         f16x8 rw[WCH], rx[XCH];
         auto gload = [&](int k0) {
 #pragma unroll
-            for (int p = 0; p < WCH; ++p) rw[p] = *(const f16x8*)(wp[p] + k0);
+            for (int p = 0; p < WCH; ++p) rw[p] = *(const f16x8*)(wp[p] + (size_t)k0 * 16);
 #pragma unroll
             for (int p = 0; p < XCH; ++p) rx[p] = *(const f16x8*)(xp[p] + k0);
         };
@@ -264,9 +275,7 @@ struct LdsTile2 : LdsTile<TN, TM> {
         int wo[WCH], xo[XCH];
 #pragma unroll
         for (int p = 0; p < WCH; ++p) {
-            const int c = tid + NT * p, row = c >> 3, col = (c & 7) * 8;
-            wp[p] = a.W + (size_t)min(n0 + row, a.N - 1) * K + col;
-            wo[p] = row * LDK + col;
+            wp[p] = wslot(a, n0, tid + NT * p, wo[p]);
         }
 #pragma unroll
         for (int p = 0; p < XCH; ++p) {
@@ -282,7 +291,7 @@ struct LdsTile2 : LdsTile<TN, TM> {
         f16x8 rw0[WCH], rx0[XCH], rw1[WCH], rx1[XCH];
         auto gload = [&](f16x8 (&rw)[WCH], f16x8 (&rx)[XCH], int k0) {
 #pragma unroll
-            for (int p = 0; p < WCH; ++p) rw[p] = *(const f16x8*)(wp[p] + k0);
+            for (int p = 0; p < WCH; ++p) rw[p] = *(const f16x8*)(wp[p] + (size_t)k0 * 16);
 #pragma unroll
             for (int p = 0; p < XCH; ++p) rx[p] = *(const f16x8*)(xp[p] + k0);
         };
@@ -488,6 +497,8 @@ __global__ __launch_bounds__(Tl::NT) void gemm_fixup_kernel(GemmArgs a, int P, l
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
     for (int c = pf; c <= pl; ++c) {
+        // with fewer iterations than blocks some blocks own none and wrote nothing
+        if ((long long)c * T / P == (long long)(c + 1) * T / P) continue;
         const int cslot = ((long long)c * T / P >= tb) ? 0 : 1;
         const f32x4* part = (const f32x4*)a.sk_part + ((size_t)(c * 2 + cslot) * NV) * NT + tid;
 #pragma unroll
@@ -530,13 +541,19 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
     if (cfg == GCFG_AUTO) {
         // Picked from measured sweeps over the forward's shapes (M = 512,
         // 2048, 8192 rows; N = 3D, D, 2F, V; K = D or F) on MI355X.
+        // Stream-K only pays when every block gets at least two K-iterations.
+        const long long KT = a.K / BK;
         const int t256 = ((a.N + 255) / 256) * ((a.M + 255) / 256);
+        const int t128 = ((a.N + 127) / 128) * ((a.M + 127) / 128);
         const bool sk_ok = a.sk_part && (size_t)SK_P * 2 * 256 * 256 <= a.sk_part_floats;
+        const bool sk256 = sk_ok && t256 * KT >= 2 * SK_P, sk128 = sk_ok && t128 * KT >= 2 * SK_P;
         if (t256 >= 600 && a.N >= 16384) cfg = GCFG_G8_256x256;
-        else if (t256 >= 300) cfg = sk_ok ? GCFG_G8_256x256_SK : GCFG_G8_256x256;
-        else if (a.K >= 8192 && sk_ok) cfg = t256 >= 100 ? GCFG_G8_256x256_SK : GCFG_P2_128x128_SK;
+        else if (t256 >= 300) cfg = sk256 ? GCFG_G8_256x256_SK : GCFG_G8_256x256;
+        else if (a.K >= 8192 && sk_ok)
+            cfg = t256 >= 100 ? (sk256 ? GCFG_G8_256x256_SK : GCFG_G8_256x256)
+                              : (sk128 ? GCFG_P2_128x128_SK : GCFG_P2_128x128);
         else if (a.N >= 16384 && t256 >= 200) cfg = GCFG_G8_256x256;
-        else if (t256 < 64 && sk_ok) cfg = GCFG_P2_128x128_SK;
+        else if (t256 < 64 && sk128) cfg = GCFG_P2_128x128_SK;
         else cfg = GCFG_P2_128x128;
     }
     switch (cfg) {

@@ -1,24 +1,32 @@
 // rh_gemv.hip -- decode projections for B <= 16 tokens (HBM-bound).
 //
-// y[b][n] = sum_k W[n][k] * x[b][k] with W [N, K] fp16 streamed exactly once.
+// y[b][n] = sum_k W[n][k] * x[b][k] with W [N, K] fp16 streamed exactly once,
+// stored in fragment order (frag_off in rh_device.h) so every load instruction
+// reads 1 KB contiguous (a row-major variant is kept for comparison).
 // A block owns 16 weight rows (two 16-row tiles for the SwiGLU pair) and its
-// 4 waves split K in 128-wide chunks.  The MFMA's k order within a chunk is
-// k = 32u + 8g + e (u = MFMA step, g = lane group, e = element), so the four
-// lane groups of one row read 64 contiguous bytes per load instruction; the
-// next chunk is loaded before the current one is consumed. 
-// The product is done on 16x16x32 MFMA with the tokens as the B
-// operand (rows >= B are zero), which keeps the VALU free and handles B 1..16
-// with one kernel; MFMA throughput is far above what HBM can feed.  Epilogues
-// mirror the prefill GEMM's: RoPE + KV-cache append, residual, SwiGLU, logits.
+// NW waves split K in 128-wide chunks, chunk c going to wave c % NW, so the
+// waves of a block read neighbouring 256-byte pieces of the same rows.  The
+// MFMA's k order within a chunk is k = 32u + 8g + e (u = MFMA step, g = lane
+// group, e = element), so the four lane groups of one row read 64 contiguous
+// bytes per load instruction.  Each wave keeps DEPTH chunks in flight: HBM
+// needs about bandwidth x latency bytes outstanding, and a decode GEMV has
+// only N/16 blocks to supply them.  Loads are unconditional (chunk indexes
+// past the wave's last chunk are clamped to a valid chunk and multiplied by
+// zero), which keeps the load/wait schedule branch-free.
+// The product runs on 16x16x32 MFMA with the tokens as the B operand (token
+// rows >= B read row 0 and are discarded), which keeps the VALU free and
+// handles B 1..16 with one kernel.  Epilogues mirror the prefill GEMM's:
+// RoPE + KV-cache append, residual, SwiGLU, logits (+ per-block argmax
+// partials for greedy decode).
 #include "rh_device.h"
 #include "rh_kernels.h"
 
 namespace rh {
 namespace {
 
-template <int EPI, int RT>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
-    __shared__ f32x4 sred[4][RT][64];
+template <int EPI, int RT, int NW, int DEPTH, bool SHUF>
+__global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
+    __shared__ f32x4 sred[NW][RT][64];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int K = a.K, N = a.N;
@@ -30,14 +38,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     } else {
         rows[0] = blockIdx.x * 16;
     }
-    const f16x8 z = {};
+    // Row-major W: lane (r, g) reads row r at k = 32u + 8g.  Fragment-order W
+    // ([N/16][K/128][4][64 lanes][8]): the same values, stored so each load
+    // instruction reads 1 KB contiguous.
     const f16* wp[RT];
-    bool wvalid[RT];
 #pragma unroll
-    for (int t = 0; t < RT; ++t) {
-        wvalid[t] = rows[t] + r < N;
-        wp[t] = a.W + (size_t)(wvalid[t] ? rows[t] + r : 0) * K + 8 * g;
-    }
+    for (int t = 0; t < RT; ++t)
+        wp[t] = SHUF ? a.W + (size_t)(rows[t] >> 4) * K * 16 + lane * 8
+                     : a.W + (size_t)(rows[t] + r < N ? rows[t] + r : 0) * K + 8 * g;
     const bool xvalid = r < a.B;
     const f16* xp = a.X + (size_t)(xvalid ? r : 0) * K + 8 * g;
 
@@ -46,55 +54,66 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     for (int t = 0; t < RT; ++t) acc[t] = f32x4{};
 
     const int nch = K / 128;
-    f16x8 wa[RT][4], xa[4], wb[RT][4], xb[4];
-    auto load = [&](int c, f16x8 (&wr)[RT][4], f16x8 (&xr)[4]) {
+    // chunks of this wave: w, w + NW, ... (< nch)
+    const int my = w < nch ? (nch - 1 - w) / NW + 1 : 0;
+    f16x8 wb[DEPTH][RT][4], xb[DEPTH][4];
+    auto load = [&](int i, f16x8 (&wr)[RT][4], f16x8 (&xr)[4]) {
+        const int c = min(w + i * NW, nch - 1);
         const size_t off = (size_t)c * 128;
 #pragma unroll
         for (int t = 0; t < RT; ++t)
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                wr[t][u] = wvalid[t] ? *(const f16x8*)(wp[t] + off + 32 * u) : z;
+                wr[t][u] = SHUF ? *(const f16x8*)(wp[t] + off * 16 + 512 * u)
+                                : *(const f16x8*)(wp[t] + off + 32 * u);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) xr[u] = xvalid ? *(const f16x8*)(xp + off + 32 * u) : z;
+        for (int u = 0; u < 4; ++u) xr[u] = *(const f16x8*)(xp + off + 32 * u);
     };
-    auto mac = [&](const f16x8 (&wr)[RT][4], const f16x8 (&xr)[4]) {
+    auto mac = [&](const f16x8 (&wr)[RT][4], const f16x8 (&xr)[4], bool live) {
+        const f16x8 z = {};
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < 4; ++u) {
+            const f16x8 xv = live ? xr[u] : z;
 #pragma unroll
-            for (int t = 0; t < RT; ++t) acc[t] = mfma16(wr[t][u], xr[u], acc[t]);
+            for (int t = 0; t < RT; ++t) acc[t] = mfma16(wr[t][u], xv, acc[t]);
+        }
     };
-    int c = w;
-    if (c < nch) load(c, wa, xa);
-    while (c < nch) {
-        const int c2 = c + 4;
-        if (c2 < nch) load(c2, wb, xb);
-        mac(wa, xa);
-        if (c2 >= nch) break;
-        const int c3 = c2 + 4;
-        if (c3 < nch) load(c3, wa, xa);
-        mac(wb, xb);
-        c = c3;
+#pragma unroll
+    for (int s = 0; s < DEPTH; ++s) load(s, wb[s], xb[s]);
+    int i = 0;
+    for (; i + DEPTH < my; i += DEPTH) {
+#pragma unroll
+        for (int s = 0; s < DEPTH; ++s) {
+            mac(wb[s], xb[s], true);
+            load(i + s + DEPTH, wb[s], xb[s]);
+        }
     }
+#pragma unroll
+    for (int s = 0; s < DEPTH; ++s) mac(wb[s], xb[s], i + s < my);
+
 #pragma unroll
     for (int t = 0; t < RT; ++t) sred[w][t][lane] = acc[t];
     __syncthreads();
     if (w != 0) return;
 #pragma unroll
-    for (int t = 0; t < RT; ++t)
-        acc[t] = (sred[0][t][lane] + sred[1][t][lane]) + (sred[2][t][lane] + sred[3][t][lane]);
-    if (!xvalid) return;
+    for (int t = 0; t < RT; ++t) {
+        f32x4 s = sred[0][t][lane];
+#pragma unroll
+        for (int v = 1; v < NW; ++v) s += sred[v][t][lane];
+        acc[t] = s;
+    }
     const int tok = r;
     // lane holds rows rows[t] + 4g + (0..3) for token `tok`
     if constexpr (EPI == GV_SWIGLU) {
+        if (!xvalid) return;
         const int jb = blockIdx.x >> 1, u = blockIdx.x & 1;
         const int f = 32 * jb + 16 * u + 4 * g;
         f16x4 gv;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) gv[i] = (f16)(silu_f(acc[0][i]) * acc[1][i]);
+        for (int e = 0; e < 4; ++e) gv[e] = (f16)(silu_f(acc[0][e]) * acc[1][e]);
         *(f16x4*)(a.out_f16 + (size_t)tok * a.ldo + f) = gv;
     } else {
         const int n = rows[0] + 4 * g;
-        if (n >= N) return;
         float v0 = acc[0][0], v1 = acc[0][1], v2 = acc[0][2], v3 = acc[0][3];
         if constexpr (EPI == GV_F32) {
             if (a.softcap > 0.f) {
@@ -102,14 +121,39 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
                 v0 = tanhf(v0 * ic) * cc; v1 = tanhf(v1 * ic) * cc;
                 v2 = tanhf(v2 * ic) * cc; v3 = tanhf(v3 * ic) * cc;
             }
-            *(f32x4*)(a.out_f32 + (size_t)tok * a.ldo + n) = f32x4{v0, v1, v2, v3};
+            if (xvalid && n < N)
+                *(f32x4*)(a.out_f32 + (size_t)tok * a.ldo + n) = f32x4{v0, v1, v2, v3};
+            if (a.am_val) {
+                // best of this lane's 4 rows (ties -> lowest row), then across the
+                // 4 lane groups of the token; rows >= N never win
+                float bv = -INFINITY;
+                int bi = 0x7fffffff;
+                if (n < N) {
+                    bv = v0; bi = n;
+                    if (v1 > bv) { bv = v1; bi = n + 1; }
+                    if (v2 > bv) { bv = v2; bi = n + 2; }
+                    if (v3 > bv) { bv = v3; bi = n + 3; }
+                }
+#pragma unroll
+                for (int o = 16; o < 64; o <<= 1) {
+                    const float ov = __shfl_xor(bv, o, RH_WAVE);
+                    const int oi = __shfl_xor(bi, o, RH_WAVE);
+                    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+                }
+                if (g == 0 && xvalid) {
+                    a.am_val[(size_t)blockIdx.x * 16 + tok] = bv;
+                    a.am_idx[(size_t)blockIdx.x * 16 + tok] = bi;
+                }
+            }
         } else if constexpr (EPI == GV_RESID) {
+            if (!xvalid || n >= N) return;
             f32x4* px = (f32x4*)(a.out_f32 + (size_t)tok * a.ldo + n);
             f32x4 x = *px;
             x[0] = v0 * a.alpha + x[0]; x[1] = v1 * a.alpha + x[1];
             x[2] = v2 * a.alpha + x[2]; x[3] = v3 * a.alpha + x[3];
             *px = x;
         } else {  // GV_QKV
+            if (!xvalid || n >= N) return;
             const int pos = *a.pos;
             const int sec = n / a.D, cc = n - sec * a.D;
             const int h = cc / a.hd, d = cc - h * a.hd;
@@ -130,21 +174,112 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
 }
 
+// One wave per token: reduce the per-block (value, index) partials of the
+// logits GEMV; ties -> lowest index.  Writes out[b], next_in[b] and
+// seq_out[state[1] * B + b]; then (advance) state[0] += 1, state[1] += 1.
+__global__ __launch_bounds__(1024) void argmax_final_kernel(const float* pv, const int* pi, int nblk,
+                                                            int B, uint32_t* out, uint32_t* next_in,
+                                                            uint32_t* seq_out, int* state, int advance) {
+    const int lane = threadIdx.x & 63, b = threadIdx.x >> 6;
+    if (b < B) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int p = lane; p < nblk; p += 64) {
+            const float v = pv[(size_t)p * 16 + b];
+            const int ix = pi[(size_t)p * 16 + b];
+            if (v > bv || (v == bv && ix < bi)) { bv = v; bi = ix; }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, RH_WAVE);
+            const int oi = __shfl_xor(bi, o, RH_WAVE);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (lane == 0) {
+            if (bi == 0x7fffffff) bi = 0;  // all logits NaN
+            out[b] = (uint32_t)bi;
+            if (next_in) next_in[b] = (uint32_t)bi;
+            if (seq_out) seq_out[(size_t)state[1] * B + b] = (uint32_t)bi;
+        }
+    }
+    if (!advance) return;
+    __syncthreads();  // every wave has read state[1]
+    if (threadIdx.x == 0) { state[0] += 1; state[1] += 1; }
+}
+
+// (NW, DEPTH) variants selectable through GemvArgs::cfg (1-based).
+struct Variant { int nw, depth; };
+constexpr Variant kVariants[] = {{4, 2}, {4, 3}, {4, 4}, {8, 2}, {8, 3}, {8, 4}, {16, 2}};
+constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
+
+template <int EPI, int RT, int NW, int DEPTH>
+hipError_t launch_one(const GemvArgs& a, int nblk, hipStream_t st) {
+    if (!a.w_rowmajor)
+        hipLaunchKernelGGL((gemv_kernel<EPI, RT, NW, DEPTH, true>), dim3(nblk), dim3(NW * 64), 0, st, a);
+    else
+        hipLaunchKernelGGL((gemv_kernel<EPI, RT, NW, DEPTH, false>), dim3(nblk), dim3(NW * 64), 0, st, a);
+    return hipSuccess;
+}
+
+template <int EPI, int RT>
+hipError_t launch_variant(int v, const GemvArgs& a, int nblk, hipStream_t st) {
+    switch (v) {
+        case 1: return launch_one<EPI, RT, 4, 2>(a, nblk, st);
+        case 2: return launch_one<EPI, RT, 4, 3>(a, nblk, st);
+        case 3: if constexpr (RT == 1) return launch_one<EPI, RT, 4, 4>(a, nblk, st); else break;
+        case 4: return launch_one<EPI, RT, 8, 2>(a, nblk, st);
+        case 5: return launch_one<EPI, RT, 8, 3>(a, nblk, st);
+        case 6: if constexpr (RT == 1) return launch_one<EPI, RT, 8, 4>(a, nblk, st); else break;
+        case 7: return launch_one<EPI, RT, 16, 2>(a, nblk, st);
+        default: break;
+    }
+    return hipErrorInvalidValue;
+}
+
+// Default variant per shape, from sweeps of the 7B decode shapes on MI355X
+// with fragment-ordered weights streamed from HBM (footprint > 2 GiB):
+// SwiGLU pair rows 8 waves x 2 deep; long rows (K 11008) 4 x 2; 16 tokens
+// 8 x 2; otherwise 4 waves, 4 deep for the tall matrices.
+int pick_variant(int epi, const GemvArgs& a) {
+    if (epi == GV_SWIGLU) return 4;
+    if (a.K > 4096) return 1;
+    if (a.B >= 8) return 4;
+    return a.N >= 8192 ? 3 : 1;
+}
+
 }  // namespace
+
+int gemv_num_variants() { return kNumVariants; }
 
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t st) {
     if (a.K % 128 != 0 || a.B < 1 || a.B > 16 || a.N % 4 != 0) return hipErrorInvalidValue;
+    if (a.am_val && (epi != GV_F32 || !a.am_idx)) return hipErrorInvalidValue;
+    const int v = a.cfg > 0 ? a.cfg : pick_variant(epi, a);
+    if (v > kNumVariants) return hipErrorInvalidValue;
     const int nblk = (a.N + 15) / 16;
+    hipError_t e;
     switch (epi) {
-        case GV_F32: hipLaunchKernelGGL((gemv_kernel<GV_F32, 1>), dim3(nblk), dim3(256), 0, st, a); break;
-        case GV_RESID: hipLaunchKernelGGL((gemv_kernel<GV_RESID, 1>), dim3(nblk), dim3(256), 0, st, a); break;
-        case GV_QKV: hipLaunchKernelGGL((gemv_kernel<GV_QKV, 1>), dim3(nblk), dim3(256), 0, st, a); break;
+        case GV_F32: e = launch_variant<GV_F32, 1>(v, a, nblk, st); break;
+        case GV_RESID: e = launch_variant<GV_RESID, 1>(v, a, nblk, st); break;
+        case GV_QKV: e = launch_variant<GV_QKV, 1>(v, a, nblk, st); break;
         case GV_SWIGLU:
             if (a.N % 64 != 0) return hipErrorInvalidValue;
-            hipLaunchKernelGGL((gemv_kernel<GV_SWIGLU, 2>), dim3(a.N / 32), dim3(256), 0, st, a);
+            e = launch_variant<GV_SWIGLU, 2>(v, a, a.N / 32, st);
             break;
         default: return hipErrorInvalidValue;
     }
+    if (e != hipSuccess) return e;
+    return hipGetLastError();
+}
+
+int gemv_argmax_blocks(int N) { return (N + 15) / 16; }
+
+hipError_t launch_argmax_final(const float* pv, const int* pi, int nblk, int B, uint32_t* out,
+                               uint32_t* next_in, uint32_t* seq_out, int* state, bool advance,
+                               hipStream_t st) {
+    if (B < 1 || B > 16 || nblk < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(1024), 0, st, pv, pi, nblk, B, out, next_in,
+                       seq_out, state, advance ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -70,8 +70,21 @@ struct GemvArgs {
     const float2* rope;
     const int* pos;    // device position
     int D, H, hd, ctx;
+    // GV_F32 only (optional): per-block argmax partials [gemv_argmax_blocks(N)][16]
+    float* am_val;
+    int* am_idx;
+    int cfg;           // 0 = default (waves, depth) variant; 1..gemv_num_variants() forces one
+    int w_rowmajor;    // 0: W in fragment order (frag_off, rows padded to 16); 1: row-major [N, K]
 };
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t st);
+int gemv_num_variants();
+int gemv_argmax_blocks(int N);
+// Greedy token from the logits GEMV's argmax partials (ties -> lowest id):
+// writes out[b], next_in[b] (nullable), seq_out[state[1]*B + b] (nullable),
+// then state[0] += 1, state[1] += 1 when advance is set.
+hipError_t launch_argmax_final(const float* pv, const int* pi, int nblk, int B, uint32_t* out,
+                               uint32_t* next_in, uint32_t* seq_out, int* state, bool advance,
+                               hipStream_t st);
 
 // ---------------- row ops ----------------
 hipError_t launch_embed(const uint32_t* tok, const f16* E, float* x, int rows, int D, int V,
@@ -84,23 +97,22 @@ hipError_t launch_rmsnorm_strided(const float* x, const float* gamma, f16* out, 
 hipError_t launch_cross_entropy(const float* logits, const uint32_t* targets, float* loss,
                                 int rows, int V, int* err, hipStream_t st);
 hipError_t launch_mean_rows(const float* loss, float* mean, int B, int S, hipStream_t st);
-// argmax over [B][V]; writes out[b], next_in[b] and seq_out[step*B + b]
-// (step from state[1]); ties -> lowest index.
-hipError_t launch_argmax(const float* logits, int B, int V, uint32_t* out, uint32_t* next_in,
-                         uint32_t* seq_out, const int* state, hipStream_t st);
-// state[0] += 1 (position), state[1] += 1 (step)
-hipError_t launch_advance(int* state, hipStream_t st);
 hipError_t launch_set_state(int* state, int pos, int step, hipStream_t st);
 hipError_t launch_fill_f32(float* p, float v, size_t n, hipStream_t st);
 
 // ---------------- weight packing ----------------
-// dst[(row_map(c))*ldd + r] = half(src[r*C + c]) for a [R][C] fp32 source.
-// map: 0 identity rows (dst row = row_off + c), 1 = W1/W3 interleave
-// (dst row = 64*(c/32) + c%32 + row_off).
+// Device weights are fp16 [N, K] in fragment order (frag_off in rh_device.h),
+// N padded to a multiple of 16.
+// Transposing pack: element (row_map(c), k = r) = half(src[r*C + c]) for a
+// [R][C] fp32 source, K = ldd.  map: 0 identity rows (dst row = row_off + c),
+// 1 = W1/W3 interleave (dst row = 64*(c/32) + c%32 + row_off).
 hipError_t launch_pack_transpose(const float* src, f16* dst, int R, int C, int ldd, int map,
                                  int row_off, hipStream_t st);
 hipError_t launch_unpack_transpose(const f16* src, float* dst, int R, int C, int lds, int map,
                                    int row_off, hipStream_t st);
+// Row pack: element (row, k) = half(src[row*K + k]) for a [R][K] source.
+hipError_t launch_pack_rows(const float* src, f16* dst, int R, int K, hipStream_t st);
+hipError_t launch_unpack_rows(const f16* src, float* dst, int R, int K, hipStream_t st);
 hipError_t launch_convert_f32_f16(const float* src, f16* dst, size_t n, hipStream_t st);
 hipError_t launch_convert_f16_f32(const f16* src, float* dst, size_t n, hipStream_t st);
 hipError_t launch_init_normal(float* dst, size_t n, uint64_t seed, uint32_t tensor_id, float std,

@@ -7,14 +7,16 @@
 //   ce         cross_entropy::forward_backward_batch (cpu/cross_entropy.rs:58-96),
 //              loss only: ln(sum exp(l - max)) - (l[t] - max), one block per row
 //   mean       total / S per sequence (full_model.rs:987)
-//   argmax     greedy token, ties -> lowest id
 //   pack/unpack  reference orientation (layer.rs:52-63) <-> device [out, in] fp16
+//              in fragment order (frag_off)
 #include "rh_device.h"
 #include "rh_kernels.h"
 
 namespace rh {
 namespace {
 
+// E is the fragment-ordered [V, D] table (frag_off); 8 consecutive k of a row
+// are 16 contiguous bytes.
 __global__ void embed_kernel(const uint32_t* tok, const f16* E, float* x, int D, int V, int* err) {
     const int row = blockIdx.x;
     uint32_t t = tok[row];
@@ -22,11 +24,11 @@ __global__ void embed_kernel(const uint32_t* tok, const f16* E, float* x, int D,
         if (threadIdx.x == 0) atomicAdd(err, 1);
         t = 0;
     }
-    const f16* src = E + (size_t)t * D;
     float* dst = x + (size_t)row * D;
-    for (int i = threadIdx.x * 4; i < D; i += blockDim.x * 4) {
-        const f16x4 v = *(const f16x4*)(src + i);
+    for (int i = threadIdx.x * 8; i < D; i += blockDim.x * 8) {
+        const f16x8 v = *(const f16x8*)(E + frag_off((int)t, i, D));
         *(f32x4*)(dst + i) = f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+        *(f32x4*)(dst + i + 4) = f32x4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
     }
 }
 
@@ -93,40 +95,6 @@ __global__ __launch_bounds__(256) void mean_kernel(const float* loss, float* mea
     if (threadIdx.x == 0) mean[b] = s / (float)S;
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(const float* logits, int V, uint32_t* out,
-                                                     uint32_t* next_in, uint32_t* seq_out,
-                                                     const int* state, int B) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
-    const int b = blockIdx.x, tid = threadIdx.x;
-    const float* l = logits + (size_t)b * V;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int i = tid; i < V; i += 256) {
-        const float v = l[i];
-        if (v > bv) { bv = v; bi = i; }  // strided scan: first hit is the lowest index
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, RH_WAVE);
-        const int oi = __shfl_xor(bi, o, RH_WAVE);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-    if ((tid & 63) == 0) { sv[tid >> 6] = bv; si[tid >> 6] = bi; }
-    __syncthreads();
-    if (tid == 0) {
-        for (int w = 1; w < 4; ++w)
-            if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
-        if (bi >= V) bi = 0;
-        out[b] = (uint32_t)bi;
-        if (next_in) next_in[b] = (uint32_t)bi;
-        if (seq_out) seq_out[(size_t)state[1] * B + b] = (uint32_t)bi;
-    }
-}
-
-__global__ void advance_kernel(int* state) {
-    if (threadIdx.x == 0) { state[0] += 1; state[1] += 1; }
-}
 __global__ void set_state_kernel(int* state, int pos, int step) {
     if (threadIdx.x == 0) { state[0] = pos; state[1] = step; }
 }
@@ -139,7 +107,8 @@ __device__ __forceinline__ int dst_row(int c, int map, int row_off) {
     return map == 1 ? 64 * (c >> 5) + (c & 31) + row_off : c + row_off;
 }
 
-// 32x32 tiles through LDS: reads rows of src, writes rows of dst.
+// 32x32 tiles through LDS: src [R][C] (in x out) -> dst row dst_row(c), k = r,
+// in fragment order with K = ldd.
 __global__ void pack_transpose_kernel(const float* src, f16* dst, int R, int C, int ldd, int map,
                                       int row_off) {
     __shared__ float tile[32][33];
@@ -152,7 +121,7 @@ __global__ void pack_transpose_kernel(const float* src, f16* dst, int R, int C, 
     __syncthreads();
     for (int y = ty; y < 32; y += 8) {
         const int c = c0 + y, r = r0 + tx;
-        if (c < C && r < R) dst[(size_t)dst_row(c, map, row_off) * ldd + r] = (f16)tile[tx][y];
+        if (c < C && r < R) dst[frag_off(dst_row(c, map, row_off), r, ldd)] = (f16)tile[tx][y];
     }
 }
 
@@ -163,13 +132,25 @@ __global__ void unpack_transpose_kernel(const f16* src, float* dst, int R, int C
     const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
     for (int y = ty; y < 32; y += 8) {
         const int c = c0 + y, r = r0 + tx;
-        tile[y][tx] = (c < C && r < R) ? (float)src[(size_t)dst_row(c, map, row_off) * lds + r] : 0.f;
+        tile[y][tx] = (c < C && r < R) ? (float)src[frag_off(dst_row(c, map, row_off), r, lds)] : 0.f;
     }
     __syncthreads();
     for (int y = ty; y < 32; y += 8) {
         const int r = r0 + y, c = c0 + tx;
         if (r < R && c < C) dst[(size_t)r * C + c] = tile[tx][y];
     }
+}
+
+// [R][K] fp32 rows (out x in) <-> fragment-ordered fp16.
+__global__ void pack_rows_kernel(const float* s, f16* d, int R, int K) {
+    const size_t n = (size_t)R * K;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        d[frag_off((int)(i / K), (int)(i % K), K)] = (f16)s[i];
+}
+__global__ void unpack_rows_kernel(const f16* s, float* d, int R, int K) {
+    const size_t n = (size_t)R * K;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        d[i] = (float)s[frag_off((int)(i / K), (int)(i % K), K)];
 }
 
 __global__ void convert_f32_f16_kernel(const float* s, f16* d, size_t n) {
@@ -246,16 +227,6 @@ hipError_t launch_mean_rows(const float* loss, float* mean, int B, int S, hipStr
     hipLaunchKernelGGL(mean_kernel, dim3(B), dim3(256), 0, st, loss, mean, S);
     return hipGetLastError();
 }
-hipError_t launch_argmax(const float* logits, int B, int V, uint32_t* out, uint32_t* next_in,
-                         uint32_t* seq_out, const int* state, hipStream_t st) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(B), dim3(256), 0, st, logits, V, out, next_in, seq_out,
-                       state, B);
-    return hipGetLastError();
-}
-hipError_t launch_advance(int* state, hipStream_t st) {
-    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, st, state);
-    return hipGetLastError();
-}
 hipError_t launch_set_state(int* state, int pos, int step, hipStream_t st) {
     hipLaunchKernelGGL(set_state_kernel, dim3(1), dim3(64), 0, st, state, pos, step);
     return hipGetLastError();
@@ -274,6 +245,14 @@ hipError_t launch_unpack_transpose(const f16* src, float* dst, int R, int C, int
                                    int row_off, hipStream_t st) {
     const dim3 grid((C + 31) / 32, (R + 31) / 32);
     hipLaunchKernelGGL(unpack_transpose_kernel, grid, dim3(256), 0, st, src, dst, R, C, lds, map, row_off);
+    return hipGetLastError();
+}
+hipError_t launch_pack_rows(const float* src, f16* dst, int R, int K, hipStream_t st) {
+    hipLaunchKernelGGL(pack_rows_kernel, dim3(grid_for((size_t)R * K, 256)), dim3(256), 0, st, src, dst, R, K);
+    return hipGetLastError();
+}
+hipError_t launch_unpack_rows(const f16* src, float* dst, int R, int K, hipStream_t st) {
+    hipLaunchKernelGGL(unpack_rows_kernel, dim3(grid_for((size_t)R * K, 256)), dim3(256), 0, st, src, dst, R, K);
     return hipGetLastError();
 }
 hipError_t launch_convert_f32_f16(const float* src, f16* dst, size_t n, hipStream_t st) {

@@ -72,6 +72,8 @@ struct rh_ctx {
     f16 *dxn = nullptr, *dq = nullptr, *dattn = nullptr, *dgate = nullptr;
     int* dstate = nullptr;
     uint32_t *dtok = nullptr, *dout = nullptr, *dseq = nullptr;
+    float* dam_v = nullptr;  // [argmax blocks][16] argmax partials of the logits GEMV
+    int* dam_i = nullptr;
     int dec_B = 0, host_pos = 0;
     bool have_prefill = false;
     bool use_graphs = true;
@@ -322,9 +324,10 @@ int enqueue_decode_step(rh_ctx* ctx, int B) {
     rh::GemvArgs g{};
     g.W = ctx->embed; g.X = ctx->dxn; g.B = B; g.N = c.vocab; g.K = D;
     g.out_f32 = ctx->dlogits; g.ldo = c.vocab; g.softcap = c.softcap;
+    g.am_val = ctx->dam_v; g.am_idx = ctx->dam_i;
     RCK(timed(ctx, RH_K_GEMV_LOGITS, [&] { return rh::launch_gemv(rh::GV_F32, g, st); }));
-    LCK(rh::launch_argmax(ctx->dlogits, B, c.vocab, ctx->dout, ctx->dtok, ctx->dseq, ctx->dstate, st));
-    LCK(rh::launch_advance(ctx->dstate, st));
+    LCK(rh::launch_argmax_final(ctx->dam_v, ctx->dam_i, rh::gemv_argmax_blocks(c.vocab), B, ctx->dout,
+                                ctx->dtok, ctx->dseq, ctx->dstate, true, st));
     return RH_OK;
 }
 
@@ -399,7 +402,7 @@ TensorMap layer_map(rh_ctx* ctx, int l, int j) {
 // staging (fp32, reference orientation) -> device fp16 layout
 int pack_from_staging(rh_ctx* ctx, const TensorMap& m) {
     if (m.map < 0) {
-        LCK(rh::launch_convert_f32_f16(ctx->staging, m.dst, (size_t)m.R * m.C, ctx->stream));
+        LCK(rh::launch_pack_rows(ctx->staging, m.dst, m.R, m.C, ctx->stream));
     } else {
         LCK(rh::launch_pack_transpose(ctx->staging, m.dst, m.R, m.C, m.ldd, m.map, m.row_off, ctx->stream));
     }
@@ -408,7 +411,7 @@ int pack_from_staging(rh_ctx* ctx, const TensorMap& m) {
 
 int unpack_to_staging(rh_ctx* ctx, const TensorMap& m) {
     if (m.map < 0) {
-        LCK(rh::launch_convert_f16_f32(m.dst, ctx->staging, (size_t)m.R * m.C, ctx->stream));
+        LCK(rh::launch_unpack_rows(m.dst, ctx->staging, m.R, m.C, ctx->stream));
     } else {
         LCK(rh::launch_unpack_transpose(m.dst, ctx->staging, m.R, m.C, m.ldd, m.map, m.row_off, ctx->stream));
     }
@@ -457,7 +460,10 @@ int rh_create(const rh_config* cfg, int device, int max_batch, int max_ctx, rh_c
 
     const size_t D = c.dim, F = c.hidden, V = c.vocab;
     int rc = RH_OK;
-    if ((rc = dalloc(ctx, &ctx->embed, V * D)) || (rc = dalloc(ctx, &ctx->gfinal, D))) return bail(rc);
+    // the embedding table doubles as the logits weight: fragment order, rows padded to 16
+    const size_t V16 = (V + 15) / 16 * 16;
+    if ((rc = dalloc(ctx, &ctx->embed, V16 * D)) || (rc = dalloc(ctx, &ctx->gfinal, D))) return bail(rc);
+    if (hipMemset(ctx->embed, 0, V16 * D * sizeof(f16)) != hipSuccess) return bail(RH_EDEVICE);
     ctx->L.resize(c.nlayers);
     for (auto& W : ctx->L) {
         if ((rc = dalloc(ctx, &W.wqkv, 3 * D * D)) || (rc = dalloc(ctx, &W.wo, D * D)) ||
@@ -481,7 +487,9 @@ int rh_create(const rh_config* cfg, int device, int max_batch, int max_ctx, rh_c
             (rc = dalloc(ctx, &ctx->pl, (size_t)Bd * c.heads * nch)) ||
             (rc = dalloc(ctx, &ctx->po, (size_t)Bd * c.heads * nch * c.head_dim)) ||
             (rc = dalloc(ctx, &ctx->dstate, 2)) || (rc = dalloc(ctx, &ctx->dtok, 16)) ||
-            (rc = dalloc(ctx, &ctx->dout, 16)) || (rc = dalloc(ctx, &ctx->dseq, (size_t)max_ctx * 16)))
+            (rc = dalloc(ctx, &ctx->dout, 16)) || (rc = dalloc(ctx, &ctx->dseq, (size_t)max_ctx * 16)) ||
+            (rc = dalloc(ctx, &ctx->dam_v, (size_t)rh::gemv_argmax_blocks(c.vocab) * 16)) ||
+            (rc = dalloc(ctx, &ctx->dam_i, (size_t)rh::gemv_argmax_blocks(c.vocab) * 16)))
             return bail(rc);
         // GEMV B operand rows >= B are never read, but keep them defined.
         if (hipMemset(ctx->dxn, 0, 16 * D * sizeof(f16)) != hipSuccess) return bail(RH_EDEVICE);
@@ -505,7 +513,7 @@ int rh_load_weights_f32(rh_ctx* ctx, const float* embed, const float* gamma_fina
     RCK(ensure_staging(ctx, std::max({V * D, D * F, D * D})));
     hipStream_t st = ctx->stream;
     HCK(hipMemcpyAsync(ctx->staging, embed, V * D * sizeof(float), hipMemcpyHostToDevice, st));
-    LCK(rh::launch_convert_f32_f16(ctx->staging, ctx->embed, V * D, st));
+    LCK(rh::launch_pack_rows(ctx->staging, ctx->embed, (int)V, (int)D, st));
     HCK(hipMemcpyAsync(ctx->gfinal, gamma_final, D * sizeof(float), hipMemcpyHostToDevice, st));
     for (int l = 0; l < c.nlayers; ++l) {
         const float* const* t = layer_tensors + 9 * l;
@@ -529,7 +537,7 @@ int rh_read_weights_f32(rh_ctx* ctx, float* embed, float* gamma_final, float* co
     RCK(ensure_staging(ctx, std::max({V * D, D * F, D * D})));
     hipStream_t st = ctx->stream;
     if (embed) {
-        LCK(rh::launch_convert_f16_f32(ctx->embed, ctx->staging, V * D, st));
+        LCK(rh::launch_unpack_rows(ctx->embed, ctx->staging, (int)V, (int)D, st));
         HCK(hipMemcpyAsync(embed, ctx->staging, V * D * sizeof(float), hipMemcpyDeviceToHost, st));
         HCK(hipStreamSynchronize(st));
     }
@@ -561,7 +569,7 @@ int rh_init_weights_normal(rh_ctx* ctx, uint64_t seed, float std_) {
     RCK(ensure_staging(ctx, std::max({V * D, D * F, D * D})));
     hipStream_t st = ctx->stream;
     LCK(rh::launch_init_normal(ctx->staging, V * D, seed, 0u, std_, st));
-    LCK(rh::launch_convert_f32_f16(ctx->staging, ctx->embed, V * D, st));
+    LCK(rh::launch_pack_rows(ctx->staging, ctx->embed, (int)V, (int)D, st));
     LCK(rh::launch_fill_f32(ctx->gfinal, 1.0f, D, st));
     for (int l = 0; l < c.nlayers; ++l) {
         for (int j = 0; j < 7; ++j) {
@@ -649,9 +657,11 @@ int rh_prefill(rh_ctx* ctx, const uint32_t* tokens, int batch, int len, uint32_t
     rh::GemvArgs g{};
     g.W = ctx->embed; g.X = ctx->dxn; g.B = batch; g.N = c.vocab; g.K = c.dim;
     g.out_f32 = ctx->dlogits; g.ldo = c.vocab; g.softcap = c.softcap;
+    g.am_val = ctx->dam_v; g.am_idx = ctx->dam_i;
     RCK(timed(ctx, RH_K_GEMV_LOGITS, [&] { return rh::launch_gemv(rh::GV_F32, g, st); }));
     LCK(rh::launch_set_state(ctx->dstate, len, 0, st));
-    LCK(rh::launch_argmax(ctx->dlogits, batch, c.vocab, ctx->dout, ctx->dtok, nullptr, ctx->dstate, st));
+    LCK(rh::launch_argmax_final(ctx->dam_v, ctx->dam_i, rh::gemv_argmax_blocks(c.vocab), batch, ctx->dout,
+                                ctx->dtok, nullptr, ctx->dstate, false, st));
     if (next_tok_out) HCK(hipMemcpyAsync(next_tok_out, ctx->dout, batch * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
     if (last_logits_out)
         HCK(hipMemcpyAsync(last_logits_out, ctx->dlogits, (size_t)batch * c.vocab * sizeof(float),

@@ -61,6 +61,16 @@ def test_forward_batch_ragged_seq(orc):
     _compare(orc, cfg, w, tok, tgt)
 
 
+def test_forward_stream_k_shapes(orc):
+    """Shapes whose QKV (N 3072, K 1024) and W2 (K 8192) GEMMs take the
+    stream-K path (partial tiles + fix-up kernel) with the RoPE/cache and
+    residual epilogues; M = 256 rows over two sequences."""
+    cfg = ModelConfig(1024, 8192, 8, 8, 128, 128, 1, 2048)
+    w = ModelWeights.normal(cfg, seed=17)
+    tok, tgt = tokens_uniform(18, cfg.vocab, 2, cfg.seq)
+    _compare(orc, cfg, w, tok, tgt)
+
+
 def test_forward_softcap(orc):
     cfg = small_cfg()
     w = ModelWeights.normal(cfg, seed=7)
