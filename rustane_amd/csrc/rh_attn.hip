@@ -162,12 +162,15 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
     }
 }
 
-constexpr int DCH = 128;  // decode positions per chunk block
-
-// One block per (chunk, head, sequence).  hd/8 lanes share a position (16-byte
-// K/V loads); every K and V load of a thread is issued before any of its
-// arithmetic so each block pays the memory latency about once.
-template <int HD>
+// Decode attention: one block per (chunk of DCH positions, head, sequence),
+// 4 waves.  Lane = LPP * slot + j: j owns dims 8j..8j+7 of one position
+// (16-byte K/V loads), so a wave covers 64 / LPP positions per pass.  Each
+// wave takes DCH/4 consecutive positions, issues every K and V load of them
+// first, and keeps an online-softmax state (m, l, o) per slot; slots merge
+// with shuffles and the 4 waves through LDS once at the end, so the block
+// pays the memory latency once and synchronises once.  Positions past the
+// current one read a clamped (valid) row and are masked.
+template <int HD, int DCH>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict__ Q,
                                                           const f16* __restrict__ Kc,
                                                           const f16* __restrict__ Vc,
@@ -175,96 +178,104 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict_
                                                           float* part_m, float* part_l,
                                                           float* part_o, int H, int ctx,
                                                           float scale) {
-    constexpr int LPP = HD / 8;       // lanes per position
-    constexpr int NSLOT = 256 / LPP;  // positions per pass of the block
-    constexpr int PER = DCH / NSLOT;  // positions per thread
-    __shared__ float sS[DCH];
-    __shared__ float sO[NSLOT][HD + 4];
-    __shared__ float red[4];
-    const int tid = threadIdx.x, j = tid % LPP, slot = tid / LPP;
+    constexpr int LPP = HD / 8, SL = 64 / LPP, PW = DCH / 4, NP = PW / SL;
+    static_assert(NP * SL * 4 == DCH, "chunk must split over 4 waves x slots");
+    __shared__ float sm_[4], sl_[4];
+    __shared__ float so_[4][HD];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int j = lane % LPP, slot = lane / LPP;
     const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int nch = gridDim.x;
     const int nctx = *pos + 1;
     const int t0 = chunk * DCH, t1 = min(nctx, t0 + DCH);
     const size_t bh = (size_t)b * H + h;
     const size_t pidx = bh * nch + chunk;
-    if (t0 < t1) {
-        const f16x8 qv = *(const f16x8*)(Q + bh * HD + 8 * j);
-        const f16* Kb = Kc + bh * ctx * HD + 8 * j;
-        const f16* Vb = Vc + bh * ctx * HD + 8 * j;
-        const f16x8 z = {};
-        f16x8 kv[PER], vv[PER];
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int t = t0 + slot + i * NSLOT;
-            kv[i] = t < t1 ? *(const f16x8*)(Kb + (size_t)t * HD) : z;
-        }
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int t = t0 + slot + i * NSLOT;
-            vv[i] = t < t1 ? *(const f16x8*)(Vb + (size_t)t * HD) : z;
-        }
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            float d = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) d += (float)qv[e] * (float)kv[i][e];
-#pragma unroll
-            for (int o = LPP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, RH_WAVE);
-            const int t = t0 + slot + i * NSLOT;
-            if (j == 0 && t < t1) sS[t - t0] = d * scale;
-        }
-        __syncthreads();
-        const int n = t1 - t0;
-        float mx = tid < n ? sS[tid] : -INFINITY;  // n <= DCH < 256
-        mx = wave_max(mx);
-        if ((tid & 63) == 0) red[tid >> 6] = mx;
-        __syncthreads();
-        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        __syncthreads();
-        float p = 0.f;
-        if (tid < n) {
-            p = __expf(sS[tid] - mx);
-            sS[tid] = p;
-        }
-        const float ls = block_sum_256(p, red);  // its barrier also publishes sS
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int t = t0 + slot + i * NSLOT;
-            const float pt = t < t1 ? sS[t - t0] : 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] += pt * (float)vv[i][e];
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sO[slot][8 * j + e] = acc[e];
-        __syncthreads();
-        if (tid < HD) {
-            float o = 0.f;
-            for (int k = 0; k < NSLOT; ++k) o += sO[k][tid];
-            part_o[pidx * HD + tid] = o;
-        }
-        if (tid == 0) { part_m[pidx] = mx; part_l[pidx] = ls; }
-    } else {
+    if (t0 >= t1) {
         if (tid == 0) { part_m[pidx] = -INFINITY; part_l[pidx] = 0.f; }
         if (tid < HD) part_o[pidx * HD + tid] = 0.f;
+        return;
+    }
+    const f16x8 qv = *(const f16x8*)(Q + bh * HD + 8 * j);
+    const f16* Kb = Kc + bh * ctx * HD + 8 * j;
+    const f16* Vb = Vc + bh * ctx * HD + 8 * j;
+    const int tw = t0 + w * PW + slot;  // this lane's first position; then + SL per pass
+    f16x8 kv[NP], vv[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) kv[i] = *(const f16x8*)(Kb + (size_t)min(tw + i * SL, t1 - 1) * HD);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) vv[i] = *(const f16x8*)(Vb + (size_t)min(tw + i * SL, t1 - 1) * HD);
+    float sc[NP];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d += (float)qv[e] * (float)kv[i][e];
+#pragma unroll
+        for (int o = LPP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, RH_WAVE);
+        sc[i] = tw + i * SL < t1 ? d * scale : -INFINITY;
+        m = fmaxf(m, sc[i]);
+    }
+    float l = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const float p = sc[i] == -INFINITY ? 0.f : __expf(sc[i] - m);
+        l += p;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] += p * (float)vv[i][e];
+    }
+    // merge the SL slots of the wave (lanes with equal j)
+#pragma unroll
+    for (int off = LPP; off < 64; off <<= 1) {
+        const float om = __shfl_xor(m, off, RH_WAVE), ol = __shfl_xor(l, off, RH_WAVE);
+        const float nm = fmaxf(m, om);
+        const float ca = m == -INFINITY ? 0.f : __expf(m - nm);
+        const float cb = om == -INFINITY ? 0.f : __expf(om - nm);
+        l = l * ca + ol * cb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = o[e] * ca + __shfl_xor(o[e], off, RH_WAVE) * cb;
+        m = nm;
+    }
+    if (slot == 0) {
+        if (j == 0) { sm_[w] = m; sl_[w] = l; }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) so_[w][8 * j + e] = o[e];
+    }
+    __syncthreads();
+    if (tid < HD) {
+        const float M = fmaxf(fmaxf(sm_[0], sm_[1]), fmaxf(sm_[2], sm_[3]));
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float c = sm_[v] == -INFINITY ? 0.f : __expf(sm_[v] - M);
+            L += sl_[v] * c;
+            O += so_[v][tid] * c;
+        }
+        part_o[pidx * HD + tid] = O;
+        if (tid == 0) { part_m[pidx] = M; part_l[pidx] = L; }
     }
 }
 
-// Merges the chunk partials of one (head, sequence).
+// Merges the chunk partials of one (head, sequence).  The loads of 8 chunks
+// are issued together (the partials come from other XCDs' L2s, so each load
+// is a long round trip); empty chunks carry m = -inf, l = 0, o = 0.
 __global__ void attn_merge_kernel(const float* part_m, const float* part_l, const float* part_o,
                                   f16* out, int H, int HD, int nch) {
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const size_t bh = (size_t)b * H + h;
+    const float* pm = part_m + bh * nch;
+    const float* pl = part_l + bh * nch;
+    const float* po = part_o + bh * nch * HD + d;
     float M = -INFINITY;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, part_m[bh * nch + c]);
+#pragma unroll 8
+    for (int c = 0; c < nch; ++c) M = fmaxf(M, pm[c]);
     float l = 0.f, o = 0.f;
+#pragma unroll 8
     for (int c = 0; c < nch; ++c) {
-        const float mc = part_m[bh * nch + c];
-        if (mc == -INFINITY) continue;
-        const float wgt = __expf(mc - M);
-        l += part_l[bh * nch + c] * wgt;
-        o += part_o[(bh * nch + c) * HD + d] * wgt;
+        const float mc = pm[c];
+        const float wgt = mc == -INFINITY ? 0.f : __expf(mc - M);
+        l += pl[c] * wgt;
+        o += po[(size_t)c * HD] * wgt;
     }
     out[bh * HD + d] = (f16)(o / l);
 }
@@ -284,22 +295,28 @@ hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* ou
     return hipGetLastError();
 }
 
-int attn_decode_chunks(int ctx) { return (ctx + DCH - 1) / DCH; }
+// positions per decode chunk block
+constexpr int DCH_DEFAULT = 128;
+
+int attn_decode_chunks(int ctx) { return (ctx + DCH_DEFAULT - 1) / DCH_DEFAULT; }
 
 hipError_t launch_attn_decode(const f16* q, const f16* k, const f16* v, const int* pos,
                               float* part_m, float* part_l, float* part_o, f16* out, int B, int H,
-                              int hd, int ctx, hipStream_t st) {
-    const int nch = attn_decode_chunks(ctx);
+                              int hd, int ctx, hipStream_t st, int dch) {
+    if (dch == 0) dch = DCH_DEFAULT;
+    const int nch = (ctx + dch - 1) / dch;
     const dim3 grid(nch, H, B);
     const float scale = 1.0f / sqrtf((float)hd);
-    if (hd == 128)
-        hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, st, q, k, v, pos, part_m,
-                           part_l, part_o, H, ctx, scale);
-    else if (hd == 64)
-        hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(256), 0, st, q, k, v, pos, part_m,
-                           part_l, part_o, H, ctx, scale);
-    else
-        return hipErrorInvalidValue;
+#define RH_ATTN_DEC(HD_, DCH_)                                                                     \
+    hipLaunchKernelGGL((attn_decode_kernel<HD_, DCH_>), grid, dim3(256), 0, st, q, k, v, pos, part_m, \
+                       part_l, part_o, H, ctx, scale)
+    if (hd == 128 && dch == 64) RH_ATTN_DEC(128, 64);
+    else if (hd == 128 && dch == 128) RH_ATTN_DEC(128, 128);
+    else if (hd == 128 && dch == 256) RH_ATTN_DEC(128, 256);
+    else if (hd == 64 && dch == 64) RH_ATTN_DEC(64, 64);
+    else if (hd == 64 && dch == 128) RH_ATTN_DEC(64, 128);
+    else return hipErrorInvalidValue;
+#undef RH_ATTN_DEC
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(H, B), dim3(hd), 0, st, part_m, part_l, part_o, out,

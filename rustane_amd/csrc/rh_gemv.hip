@@ -1,16 +1,14 @@
 // rh_gemv.hip -- decode projections for B <= 16 tokens (HBM-bound).
 //
 // y[b][n] = sum_k W[n][k] * x[b][k] with W [N, K] fp16 streamed exactly once,
-// stored in fragment order (frag_off in rh_device.h) so every load instruction
-// reads 1 KB contiguous (a row-major variant is kept for comparison).
-// A block owns 16 weight rows (two 16-row tiles for the SwiGLU pair) and its
-// NW waves split K in 128-wide chunks, chunk c going to wave c % NW, so the
-// waves of a block read neighbouring 256-byte pieces of the same rows.  The
-// MFMA's k order within a chunk is k = 32u + 8g + e (u = MFMA step, g = lane
-// group, e = element), so the four lane groups of one row read 64 contiguous
-// bytes per load instruction.  Each wave keeps DEPTH chunks in flight: HBM
-// needs about bandwidth x latency bytes outstanding, and a decode GEMV has
-// only N/16 blocks to supply them.  Loads are unconditional (chunk indexes
+// stored in fragment order (frag_off in rh_device.h) so every load
+// instruction reads 1 KB contiguous.  A block owns 16 weight rows (two
+// 16-row tiles for the SwiGLU pair) and its NW waves split K in 128-wide
+// chunks, chunk c going to wave c % NW.  The MFMA's k order within a chunk is
+// k = 32u + 8g + e (u = MFMA step, g = lane group, e = element), which is the
+// order the fragments are stored in.  Each wave keeps DEPTH chunks in flight:
+// HBM needs about bandwidth x latency bytes outstanding, and a decode GEMV
+// has only N/16 blocks to supply them.  Loads are unconditional (chunk indexes
 // past the wave's last chunk are clamped to a valid chunk and multiplied by
 // zero), which keeps the load/wait schedule branch-free.
 // The product runs on 16x16x32 MFMA with the tokens as the B operand (token
@@ -18,15 +16,22 @@
 // handles B 1..16 with one kernel.  Epilogues mirror the prefill GEMM's:
 // RoPE + KV-cache append, residual, SwiGLU, logits (+ per-block argmax
 // partials for greedy decode).
+//
+// NORM: the input is the fp32 residual stream and the block applies the
+// RMSNorm itself (rmsnorm::forward_channel_first, cpu/rmsnorm.rs:149-183)
+// into LDS while its first weight chunks are in flight, in the same
+// summation order as the standalone row kernel, so the normalised fp16 rows
+// are bit-identical and one launch per norm disappears.
 #include "rh_device.h"
 #include "rh_kernels.h"
 
 namespace rh {
 namespace {
 
-template <int EPI, int RT, int NW, int DEPTH, bool SHUF>
+template <int EPI, int RT, int NW, int DEPTH, bool NORM>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
     __shared__ f32x4 sred[NW][RT][64];
+    extern __shared__ __attribute__((aligned(16))) f16 sx[];  // NORM: normalised rows [B][K]
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int K = a.K, N = a.N;
@@ -38,16 +43,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
     } else {
         rows[0] = blockIdx.x * 16;
     }
-    // Row-major W: lane (r, g) reads row r at k = 32u + 8g.  Fragment-order W
-    // ([N/16][K/128][4][64 lanes][8]): the same values, stored so each load
-    // instruction reads 1 KB contiguous.
     const f16* wp[RT];
 #pragma unroll
-    for (int t = 0; t < RT; ++t)
-        wp[t] = SHUF ? a.W + (size_t)(rows[t] >> 4) * K * 16 + lane * 8
-                     : a.W + (size_t)(rows[t] + r < N ? rows[t] + r : 0) * K + 8 * g;
+    for (int t = 0; t < RT; ++t) wp[t] = a.W + (size_t)(rows[t] >> 4) * K * 16 + lane * 8;
     const bool xvalid = r < a.B;
-    const f16* xp = a.X + (size_t)(xvalid ? r : 0) * K + 8 * g;
+    const int xrow = xvalid ? r : 0;
+    const f16* xp = a.X + (size_t)xrow * K + 8 * g;
 
     f32x4 acc[RT];
 #pragma unroll
@@ -56,18 +57,24 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
     const int nch = K / 128;
     // chunks of this wave: w, w + NW, ... (< nch)
     const int my = w < nch ? (nch - 1 - w) / NW + 1 : 0;
-    f16x8 wb[DEPTH][RT][4], xb[DEPTH][4];
-    auto load = [&](int i, f16x8 (&wr)[RT][4], f16x8 (&xr)[4]) {
-        const int c = min(w + i * NW, nch - 1);
-        const size_t off = (size_t)c * 128;
+    constexpr int XD = NORM ? 1 : DEPTH;  // X from LDS is read at use, not prefetched
+    f16x8 wb[DEPTH][RT][4], xb[XD][4];
+    auto wload = [&](int i, f16x8 (&wr)[RT][4]) {
+        const size_t c = (size_t)min(w + i * NW, nch - 1);
 #pragma unroll
         for (int t = 0; t < RT; ++t)
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                wr[t][u] = SHUF ? *(const f16x8*)(wp[t] + off * 16 + 512 * u)
-                                : *(const f16x8*)(wp[t] + off + 32 * u);
+            for (int u = 0; u < 4; ++u) wr[t][u] = *(const f16x8*)(wp[t] + c * 2048 + 512 * u);
+    };
+    auto xload = [&](int i, f16x8 (&xr)[4]) {
+        const int off = min(w + i * NW, nch - 1) * 128;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) xr[u] = *(const f16x8*)(xp + off + 32 * u);
+        for (int u = 0; u < 4; ++u) {
+            if constexpr (NORM)
+                xr[u] = *(const f16x8*)&sx[xrow * K + off + 32 * u + 8 * g];
+            else
+                xr[u] = *(const f16x8*)(xp + off + 32 * u);
+        }
     };
     auto mac = [&](const f16x8 (&wr)[RT][4], const f16x8 (&xr)[4], bool live) {
         const f16x8 z = {};
@@ -79,17 +86,59 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
         }
     };
 #pragma unroll
-    for (int s = 0; s < DEPTH; ++s) load(s, wb[s], xb[s]);
+    for (int s = 0; s < DEPTH; ++s) {
+        wload(s, wb[s]);
+        if constexpr (!NORM) xload(s, xb[s]);
+    }
+    if constexpr (NORM) {
+        // r = 1/sqrt(sum(x^2) * (1/K) + eps), out = (x * r) * gamma: threads
+        // 0..255 sum in the row kernel's order, the whole block writes
+        __shared__ float red[NW];
+        for (int t = 0; t < a.B; ++t) {
+            const float* xr = a.xres + (size_t)t * K;
+            float ss = 0.f;
+            if (tid < 256)
+                for (int i = tid * 4; i < K; i += 1024) {
+                    const f32x4 v = *(const f32x4*)(xr + i);
+                    ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+                }
+            ss = wave_sum(ss);
+            __syncthreads();
+            if (lane == 0) red[w] = ss;
+            __syncthreads();
+            const float rs = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) * (1.0f / (float)K) + a.eps);
+            for (int i = tid * 4; i < K; i += NW * 256) {
+                const f32x4 v = *(const f32x4*)(xr + i);
+                const f32x4 gm = *(const f32x4*)(a.gamma + i);
+                *(f16x4*)&sx[t * K + i] = f16x4{(f16)(v[0] * rs * gm[0]), (f16)(v[1] * rs * gm[1]),
+                                                (f16)(v[2] * rs * gm[2]), (f16)(v[3] * rs * gm[3])};
+            }
+        }
+        __syncthreads();
+    }
     int i = 0;
     for (; i + DEPTH < my; i += DEPTH) {
 #pragma unroll
         for (int s = 0; s < DEPTH; ++s) {
-            mac(wb[s], xb[s], true);
-            load(i + s + DEPTH, wb[s], xb[s]);
+            if constexpr (NORM) {
+                xload(i + s, xb[0]);
+                mac(wb[s], xb[0], true);
+            } else {
+                mac(wb[s], xb[s], true);
+                xload(i + s + DEPTH, xb[s]);
+            }
+            wload(i + s + DEPTH, wb[s]);
         }
     }
 #pragma unroll
-    for (int s = 0; s < DEPTH; ++s) mac(wb[s], xb[s], i + s < my);
+    for (int s = 0; s < DEPTH; ++s) {
+        if constexpr (NORM) {
+            xload(i + s, xb[0]);
+            mac(wb[s], xb[0], i + s < my);
+        } else {
+            mac(wb[s], xb[s], i + s < my);
+        }
+    }
 
 #pragma unroll
     for (int t = 0; t < RT; ++t) sred[w][t][lane] = acc[t];
@@ -174,36 +223,53 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
     }
 }
 
-// One wave per token: reduce the per-block (value, index) partials of the
-// logits GEMV; ties -> lowest index.  Writes out[b], next_in[b] and
-// seq_out[state[1] * B + b]; then (advance) state[0] += 1, state[1] += 1.
+// Reduce the per-block (value, index) partials of the logits GEMV; ties ->
+// lowest index.  16 waves: 16/B per token (B <= 16), each strided over the
+// partials with 4 loads in flight, then the token's waves merge through LDS.
+// Writes out[b], next_in[b] and seq_out[state[1] * B + b]; then (advance)
+// state[0] += 1, state[1] += 1.
 __global__ __launch_bounds__(1024) void argmax_final_kernel(const float* pv, const int* pi, int nblk,
                                                             int B, uint32_t* out, uint32_t* next_in,
                                                             uint32_t* seq_out, int* state, int advance) {
-    const int lane = threadIdx.x & 63, b = threadIdx.x >> 6;
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int wpt = 16 / B;  // waves per token
+    const int b = w / wpt, sub = w - b * wpt;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    auto take = [&](float v, int ix) {
+        if (v > bv || (v == bv && ix < bi)) { bv = v; bi = ix; }
+    };
     if (b < B) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int p = lane; p < nblk; p += 64) {
-            const float v = pv[(size_t)p * 16 + b];
-            const int ix = pi[(size_t)p * 16 + b];
-            if (v > bv || (v == bv && ix < bi)) { bv = v; bi = ix; }
-        }
+        const int step = wpt * 64;
+        int p = sub * 64 + lane;
+        for (; p + 3 * step < nblk; p += 4 * step) {
+            float v[4];
+            int ix[4];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, RH_WAVE);
-            const int oi = __shfl_xor(bi, o, RH_WAVE);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+            for (int q = 0; q < 4; ++q) {
+                v[q] = pv[(size_t)(p + q * step) * 16 + b];
+                ix[q] = pi[(size_t)(p + q * step) * 16 + b];
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) take(v[q], ix[q]);
         }
-        if (lane == 0) {
-            if (bi == 0x7fffffff) bi = 0;  // all logits NaN
-            out[b] = (uint32_t)bi;
-            if (next_in) next_in[b] = (uint32_t)bi;
-            if (seq_out) seq_out[(size_t)state[1] * B + b] = (uint32_t)bi;
-        }
+        for (; p < nblk; p += step) take(pv[(size_t)p * 16 + b], pi[(size_t)p * 16 + b]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) take(__shfl_xor(bv, o, RH_WAVE), __shfl_xor(bi, o, RH_WAVE));
+        if (lane == 0) { sv[w] = bv; si[w] = bi; }
+    }
+    __syncthreads();
+    if (b < B && sub == 0 && lane == 0) {
+        for (int v = 1; v < wpt; ++v) take(sv[w + v], si[w + v]);
+        if (bi == 0x7fffffff) bi = 0;  // all logits NaN
+        out[b] = (uint32_t)bi;
+        if (next_in) next_in[b] = (uint32_t)bi;
+        if (seq_out) seq_out[(size_t)state[1] * B + b] = (uint32_t)bi;
     }
     if (!advance) return;
-    __syncthreads();  // every wave has read state[1]
+    __syncthreads();  // every token's writer has read state[1]
     if (threadIdx.x == 0) { state[0] += 1; state[1] += 1; }
 }
 
@@ -214,10 +280,14 @@ constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 
 template <int EPI, int RT, int NW, int DEPTH>
 hipError_t launch_one(const GemvArgs& a, int nblk, hipStream_t st) {
-    if (!a.w_rowmajor)
-        hipLaunchKernelGGL((gemv_kernel<EPI, RT, NW, DEPTH, true>), dim3(nblk), dim3(NW * 64), 0, st, a);
-    else
-        hipLaunchKernelGGL((gemv_kernel<EPI, RT, NW, DEPTH, false>), dim3(nblk), dim3(NW * 64), 0, st, a);
+    if constexpr (EPI != GV_RESID) {
+        if (a.xres) {
+            const size_t lds = (size_t)a.B * a.K * sizeof(f16);
+            hipLaunchKernelGGL((gemv_kernel<EPI, RT, NW, DEPTH, true>), dim3(nblk), dim3(NW * 64), lds, st, a);
+            return hipSuccess;
+        }
+    }
+    hipLaunchKernelGGL((gemv_kernel<EPI, RT, NW, DEPTH, false>), dim3(nblk), dim3(NW * 64), 0, st, a);
     return hipSuccess;
 }
 
@@ -251,9 +321,12 @@ int pick_variant(int epi, const GemvArgs& a) {
 
 int gemv_num_variants() { return kNumVariants; }
 
+bool gemv_norm_fits(int B, int K) { return (size_t)B * K * sizeof(f16) <= GEMV_NORM_LDS; }
+
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t st) {
     if (a.K % 128 != 0 || a.B < 1 || a.B > 16 || a.N % 4 != 0) return hipErrorInvalidValue;
     if (a.am_val && (epi != GV_F32 || !a.am_idx)) return hipErrorInvalidValue;
+    if (a.xres && (epi == GV_RESID || !a.gamma || !gemv_norm_fits(a.B, a.K))) return hipErrorInvalidValue;
     const int v = a.cfg > 0 ? a.cfg : pick_variant(epi, a);
     if (v > kNumVariants) return hipErrorInvalidValue;
     const int nblk = (a.N + 15) / 16;

@@ -51,9 +51,11 @@ hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* ou
                                int S, int hd, int ctx, hipStream_t st);
 // Decode attention over positions 0..*pos (the current token is at *pos):
 // q [B][H*hd]; per (b, h, chunk) partial (m, l, o[hd]), then a merge kernel.
+// Partial buffers hold B*H*attn_decode_chunks(ctx) entries; dch (positions per
+// chunk, 0 = default) is for tuning and must not exceed those buffers.
 hipError_t launch_attn_decode(const f16* q, const f16* k, const f16* v, const int* pos,
                               float* part_m, float* part_l, float* part_o, f16* out, int B, int H,
-                              int hd, int ctx, hipStream_t st);
+                              int hd, int ctx, hipStream_t st, int dch = 0);
 int attn_decode_chunks(int ctx);
 
 // ---------------- decode GEMV (B <= 16 tokens) ----------------
@@ -74,10 +76,17 @@ struct GemvArgs {
     float* am_val;
     int* am_idx;
     int cfg;           // 0 = default (waves, depth) variant; 1..gemv_num_variants() forces one
-    int w_rowmajor;    // 0: W in fragment order (frag_off, rows padded to 16); 1: row-major [N, K]
+    // Optional in-kernel RMSNorm (not GV_RESID): X is ignored and the input is
+    // rmsnorm(xres [B, K] fp32) * gamma, eps; needs gemv_norm_fits(B, K).
+    const float* xres;
+    const float* gamma;
+    float eps;
 };
+// W is fp16 [N, K] in fragment order (frag_off), rows padded to a multiple of 16.
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t st);
 int gemv_num_variants();
+constexpr size_t GEMV_NORM_LDS = 32768;  // bytes of normalised rows a block may stage
+bool gemv_norm_fits(int B, int K);
 int gemv_argmax_blocks(int N);
 // Greedy token from the logits GEMV's argmax partials (ties -> lowest id):
 // writes out[b], next_in[b] (nullable), seq_out[state[1]*B + b] (nullable),

@@ -285,20 +285,33 @@ int enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss) {
     return RH_OK;
 }
 
-// One decode step for B tokens at position dstate[0].
+// One decode step for B tokens at position dstate[0].  For small B the
+// RMSNorms run inside the QKV / W1|W3 / logits GEMVs (one launch fewer per
+// norm); otherwise a row kernel writes the normalised rows first.
 int enqueue_decode_step(rh_ctx* ctx, int B) {
     const rh_config& c = ctx->cfg;
     const int D = c.dim, F = c.hidden;
     const float alpha = 1.0f / std::sqrt(2.0f * (float)c.nlayers);
+    const bool fuse_norm = rh::gemv_norm_fits(B, D);
     hipStream_t st = ctx->stream;
+    // input of a normed GEMV: fused (xres + gamma) or via the row kernel (X)
+    auto normed = [&](rh::GemvArgs& g, const float* gamma) -> int {
+        if (fuse_norm) {
+            g.xres = ctx->dx; g.gamma = gamma; g.eps = c.rms_eps;
+        } else {
+            LCK(rh::launch_rmsnorm(ctx->dx, gamma, ctx->dxn, B, D, c.rms_eps, st));
+            g.X = ctx->dxn;
+        }
+        return RH_OK;
+    };
     LCK(rh::launch_embed(ctx->dtok, ctx->embed, ctx->dx, B, D, c.vocab, ctx->d_err, st));
     for (int l = 0; l < c.nlayers; ++l) {
         const Layer& W = ctx->L[l];
         f16* kc = ctx->kcache + (size_t)l * ctx->kv_layer;
         f16* vc = ctx->vcache + (size_t)l * ctx->kv_layer;
-        LCK(rh::launch_rmsnorm(ctx->dx, W.g1, ctx->dxn, B, D, c.rms_eps, st));
         rh::GemvArgs g{};
-        g.W = W.wqkv; g.X = ctx->dxn; g.B = B; g.N = 3 * D; g.K = D;
+        RCK(normed(g, W.g1));
+        g.W = W.wqkv; g.B = B; g.N = 3 * D; g.K = D;
         g.out_f16 = ctx->dq; g.kc = kc; g.vc = vc; g.rope = ctx->rope; g.pos = ctx->dstate;
         g.D = D; g.H = c.heads; g.hd = c.head_dim; g.ctx = ctx->max_ctx;
         RCK(timed(ctx, RH_K_GEMV_QKV, [&] { return rh::launch_gemv(rh::GV_QKV, g, st); }));
@@ -310,9 +323,9 @@ int enqueue_decode_step(rh_ctx* ctx, int B) {
         g.W = W.wo; g.X = ctx->dattn; g.B = B; g.N = D; g.K = D;
         g.out_f32 = ctx->dx; g.ldo = D; g.alpha = alpha;
         RCK(timed(ctx, RH_K_GEMV_WO, [&] { return rh::launch_gemv(rh::GV_RESID, g, st); }));
-        LCK(rh::launch_rmsnorm(ctx->dx, W.g2, ctx->dxn, B, D, c.rms_eps, st));
         g = rh::GemvArgs{};
-        g.W = W.w13; g.X = ctx->dxn; g.B = B; g.N = 2 * F; g.K = D;
+        RCK(normed(g, W.g2));
+        g.W = W.w13; g.B = B; g.N = 2 * F; g.K = D;
         g.out_f16 = ctx->dgate; g.ldo = F;
         RCK(timed(ctx, RH_K_GEMV_W13, [&] { return rh::launch_gemv(rh::GV_SWIGLU, g, st); }));
         g = rh::GemvArgs{};
@@ -320,9 +333,9 @@ int enqueue_decode_step(rh_ctx* ctx, int B) {
         g.out_f32 = ctx->dx; g.ldo = D; g.alpha = alpha;
         RCK(timed(ctx, RH_K_GEMV_W2, [&] { return rh::launch_gemv(rh::GV_RESID, g, st); }));
     }
-    LCK(rh::launch_rmsnorm(ctx->dx, ctx->gfinal, ctx->dxn, B, D, c.rms_eps, st));
     rh::GemvArgs g{};
-    g.W = ctx->embed; g.X = ctx->dxn; g.B = B; g.N = c.vocab; g.K = D;
+    RCK(normed(g, ctx->gfinal));
+    g.W = ctx->embed; g.B = B; g.N = c.vocab; g.K = D;
     g.out_f32 = ctx->dlogits; g.ldo = c.vocab; g.softcap = c.softcap;
     g.am_val = ctx->dam_v; g.am_idx = ctx->dam_i;
     RCK(timed(ctx, RH_K_GEMV_LOGITS, [&] { return rh::launch_gemv(rh::GV_F32, g, st); }));
