@@ -63,33 +63,49 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
 
     const int kend = min(S, q0 + 64);
     const int nkb = (kend + KB - 1) / KB;
+    // K/V of the next key block are loaded into registers while the current
+    // one is computed, then stored to LDS at the top of the next iteration.
+    constexpr int KL = KB * HD / 8 / 256;           // 16-byte K loads per thread
+    constexpr int VL = (KB / 2) * (HD / 8) / 256;   // key pairs per thread
+    f16x8 rk[KL], rva[VL], rvb[VL];
+    auto gload = [&](int k0) {
+        const f16x8 z = {};
+#pragma unroll
+        for (int p = 0; p < KL; ++p) {
+            const int c = tid + 256 * p, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+            const int key = k0 + row;
+            rk[p] = key < S ? *(const f16x8*)(Kb + (size_t)key * HD + col) : z;
+        }
+#pragma unroll
+        for (int p = 0; p < VL; ++p) {
+            const int u = tid + 256 * p, kp = u & 31, col = (u >> 5) * 8;
+            const int key0 = k0 + 2 * kp;
+            rva[p] = key0 < S ? *(const f16x8*)(Vb + (size_t)key0 * HD + col) : z;
+            rvb[p] = key0 + 1 < S ? *(const f16x8*)(Vb + (size_t)(key0 + 1) * HD + col) : z;
+        }
+    };
+    gload(0);
     for (int kb = 0; kb < nkb; ++kb) {
         const int k0 = kb * KB;
         __syncthreads();
         // K block -> sK[key][hd]
 #pragma unroll
-        for (int p = 0; p < KB * HD / 8 / 256; ++p) {
+        for (int p = 0; p < KL; ++p) {
             const int c = tid + 256 * p, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
-            const int key = k0 + row;
-            f16x8 v = {};
-            if (key < S) v = *(const f16x8*)(Kb + (size_t)key * HD + col);
-            *(f16x8*)&sK[row * LDK + col] = v;
+            *(f16x8*)&sK[row * LDK + col] = rk[p];
         }
         // V block -> sVt[hd][key], two keys per 32-bit LDS store
 #pragma unroll
-        for (int p = 0; p < (KB / 2) * (HD / 8) / 256; ++p) {
+        for (int p = 0; p < VL; ++p) {
             const int u = tid + 256 * p, kp = u & 31, col = (u >> 5) * 8;
-            const int key0 = k0 + 2 * kp;
-            f16x8 va = {}, vb = {};
-            if (key0 < S) va = *(const f16x8*)(Vb + (size_t)key0 * HD + col);
-            if (key0 + 1 < S) vb = *(const f16x8*)(Vb + (size_t)(key0 + 1) * HD + col);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 typedef f16 f16x2 __attribute__((ext_vector_type(2)));
-                *(f16x2*)&sVt[(col + e) * LDV + 2 * kp] = f16x2{va[e], vb[e]};
+                *(f16x2*)&sVt[(col + e) * LDV + 2 * kp] = f16x2{rva[p][e], rvb[p][e]};
             }
         }
         __syncthreads();
+        if (kb + 1 < nkb) gload(k0 + KB);
 
         // S^T tiles: chunk c (32 keys) x half u; tile row r -> key
         // 32c + 8(r/4) + 4u + r%4, so lane group g holds keys 32c + 8g + (0..7).

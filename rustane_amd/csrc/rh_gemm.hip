@@ -65,7 +65,7 @@ struct Frag {
 // LDS reads of k-step kk+1 are in flight under the MFMAs of step kk.
 template <int TN, int TM>
 struct LdsTile {
-    static constexpr int BN = 64 * TN, BM = 64 * TM, NT = 256, FTN = TN, FTM = TM;
+    static constexpr int BN = 64 * TN, BM = 64 * TM, NT = 256, FTN = TN, FTM = TM, KI = BK;
     static constexpr int WCH = BN * BK / 8 / NT, XCH = BM * BK / 8 / NT;
     using Acc = Frag<TN, TM>;
     struct Smem {
@@ -158,7 +158,7 @@ struct LdsTile {
 template <int WGN, int WGM, int TN, int TM>
 struct GTile {
     static constexpr int BN = 32 * TN * WGN, BM = 32 * TM * WGM, NT = 64 * WGN * WGM;
-    static constexpr int FTN = TN, FTM = TM;
+    static constexpr int FTN = TN, FTM = TM, KI = BK;
     static constexpr int WCH = BN * BK / 8 / NT, XCH = BM * BK / 8 / NT;
     static_assert(WCH * NT * 8 == BN * BK && XCH * NT * 8 == BM * BK, "slab must split evenly");
     using Acc = Frag<TN, TM>;
@@ -263,7 +263,7 @@ struct LdsTile2 : LdsTile<TN, TM> {
     using B = LdsTile<TN, TM>;
     using typename B::Acc;
     using typename B::Smem;
-    static constexpr int BN = B::BN, BM = B::BM, NT = B::NT, FTN = TN, FTM = TM;
+    static constexpr int BN = B::BN, BM = B::BM, NT = B::NT, FTN = TN, FTM = TM, KI = BK;
     static constexpr int WCH = B::WCH, XCH = B::XCH;
 
     __device__ static void run(const GemmArgs& a, int n0, int m0, int kb, int ke, Acc& acc, Smem& sm) {
@@ -355,6 +355,129 @@ struct LdsTile2 : LdsTile<TN, TM> {
     }
 };
 
+// ---------------------------------------------------------------------------
+// Tile policy 2 (DTile): operands go global -> LDS by DMA
+// (global_load_lds_dwordx4: 16 bytes per lane land at LDS base + 16 * lane),
+// so no registers stage them and NS = 4 stages of 32 k are in flight.  A
+// stage holds BN/16 weight fragments and BM/16 activation fragments of 1 KB
+// each, both in fragment order: the weight is stored that way (each DMA reads
+// 1 KB contiguous) and the row-major activation is gathered into it (lane
+// 16g + r reads row r at k + 8g).  The 32x32x16 MFMA operand of lane 32h + r
+// at k16-step s is then lane 16(2s + h) + r%16 of fragment r/16: 16 lanes read
+// 256 contiguous bytes, conflict-free without padding.  One barrier per stage:
+// each wave waits for its own DMA of the stage (an explicit vmcnt, since the
+// stages behind it stay in flight), then the barrier publishes every wave's.
+// The stages are separate LDS arrays so the compiler's own wait-count
+// tracking can tell them apart and adds no drain of its own.
+template <int WGN, int WGM, int TN, int TM>
+struct DTile {
+    static constexpr int BN = 32 * TN * WGN, BM = 32 * TM * WGM, NT = 64 * WGN * WGM;
+    static constexpr int FTN = TN, FTM = TM, KI = 32, NS = 4;
+    static constexpr int NWF = BN / 16, NXF = BM / 16, NWAVE = WGN * WGM;
+    static constexpr int LPS = (NWF + NXF) / NWAVE;  // DMA instructions per wave per stage
+    static_assert(LPS * NWAVE == NWF + NXF, "fragments must split evenly over the waves");
+    static constexpr int SH = (NWF + NXF) * 512;     // halves per stage
+    using Acc = Frag<TN, TM>;
+    struct Smem {};
+    __device__ static int nw(int n0) { return n0 + ((threadIdx.x >> 6) % WGN) * 32 * TN; }
+    __device__ static int mw(int m0) { return m0 + ((threadIdx.x >> 6) / WGN) * 32 * TM; }
+    // s_waitcnt with vmcnt <= n (expcnt, lgkmcnt left at their maximum)
+    static constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+    // s_waitcnt with vmcnt <= n and lgkmcnt == 0: this wave's LDS reads are done
+    static constexpr int vm_lgkm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
+
+    __device__ static void run(const GemmArgs& a, int n0, int m0, int kb, int ke, Acc& acc, Smem&) {
+        __shared__ __attribute__((aligned(1024))) f16 st0[SH], st1[SH], st2[SH], st3[SH];
+        const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+        const int wn = wv % WGN, wm = wv / WGN;
+        const int K = a.K;
+        // this wave's DMA fragments: f = wv * LPS + q over [weight frags | activation frags]
+        const f16* gp[LPS];
+        int gstep[LPS], loff[LPS];
+#pragma unroll
+        for (int q = 0; q < LPS; ++q) {
+            const int f = wv * LPS + q;
+            loff[q] = f * 512;
+            if (f < NWF) {
+                const int rb = min((n0 >> 4) + f, ((a.N + 15) >> 4) - 1);
+                gp[q] = a.W + (size_t)rb * K * 16 + lane * 8;
+                gstep[q] = 512;  // one 32-k fragment column of the 16-row block
+            } else {
+                const int row = min(m0 + 16 * (f - NWF) + (lane & 15), a.M - 1);
+                gp[q] = a.X + (size_t)row * K + 8 * (lane >> 4);
+                gstep[q] = 32;
+            }
+        }
+        const int r = lane & 31, h = lane >> 5;
+        int ao[TN], bo[TM];
+#pragma unroll
+        for (int i = 0; i < TN; ++i) ao[i] = (((wn * 32 * TN + 32 * i) >> 4) + (r >> 4)) * 512 + 128 * h + 8 * (r & 15);
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+            bo[j] = (NWF + ((wm * 32 * TM + 32 * j) >> 4) + (r >> 4)) * 512 + 128 * h + 8 * (r & 15);
+        auto buf = [&](int s) -> f16* { return s == 0 ? st0 : s == 1 ? st1 : s == 2 ? st2 : st3; };
+        auto issue = [&](int kt, f16* st) {
+#pragma unroll
+            for (int q = 0; q < LPS; ++q)
+                __builtin_amdgcn_global_load_lds((const void*)(gp[q] + (size_t)kt * gstep[q]),
+                                                 (__attribute__((address_space(3))) void*)(st + loff[q]), 16, 0, 0);
+        };
+        // fragments of one stage: [k16 step][tile]
+        struct Frags { f16x8 a[2][TN], b[2][TM]; };
+        auto readf = [&](const f16* st, Frags& f) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                for (int i = 0; i < TN; ++i) f.a[ks][i] = *(const f16x8*)&st[ao[i] + 256 * ks];
+#pragma unroll
+                for (int j = 0; j < TM; ++j) f.b[ks][j] = *(const f16x8*)&st[bo[j] + 256 * ks];
+            }
+        };
+        auto mfmas = [&](const Frags& f) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) acc.v[i][j] = mfma32(f.a[ks][i], f.b[ks][j], acc.v[i][j]);
+        };
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
+        // no wave may still read the stages from a previous call
+        __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(63));
+        __builtin_amdgcn_s_barrier();
+        const int n = ke - kb;
+#pragma unroll
+        for (int p = 0; p < NS - 1; ++p) issue(kb + min(p, n - 1), buf(p));
+        // Stage t sits in buffer t % NS.  Step t: publish stage t+1, refill the
+        // buffer stage t came from (its fragments are already in registers),
+        // read stage t+1's fragments, then run stage t's MFMAs under those reads.
+        Frags f0, f1;
+        __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((NS - 2) * LPS));
+        __builtin_amdgcn_s_barrier();
+        issue(kb + min(NS - 1, n - 1), buf(NS - 1));
+        readf(buf(0), f0);
+        auto step = [&](int t, Frags& cur, Frags& nxt, f16* refill, const f16* next) {
+            __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((NS - 2) * LPS));
+            __builtin_amdgcn_s_barrier();
+            issue(kb + min(t + NS, n - 1), refill);
+            readf(next, nxt);  // past the last stage: a harmless read of a stale buffer
+            if (t < n) mfmas(cur);
+        };
+        // single exit: every pass runs NS steps (the vmcnt bookkeeping stays uniform)
+        for (int t = 0; t < n; t += NS) {
+            step(t, f0, f1, buf(0), buf(1));
+            step(t + 1, f1, f0, buf(1), buf(2));
+            step(t + 2, f0, f1, buf(2), buf(3));
+            step(t + 3, f1, f0, buf(3), buf(0));
+        }
+        // the trailing (unused) stage loads must land before the LDS is reused
+        __builtin_amdgcn_s_waitcnt(vm_wait(0));
+    }
+};
+
 // (nw, mw): the wave's first feature row and token.  Lane holds token
 // m = mw + j*32 + lane%32 and, per q4, the four consecutive features
 // n = nw + i*32 + 8*q4 + 4*(lane/32) + (0..3).
@@ -435,7 +558,7 @@ template <class Tl, int EPI, bool SK>
 __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long long T) {
     __shared__ __attribute__((aligned(16))) typename Tl::Smem sm;
     const int nbN = (a.N + Tl::BN - 1) / Tl::BN, nbM = (a.M + Tl::BM - 1) / Tl::BM;
-    const int KT = a.K / BK;
+    const int KT = a.K / Tl::KI;
     typename Tl::Acc acc;
     if constexpr (!SK) {
         const int t = xcd_remap(blockIdx.x, nbN * nbM);
@@ -486,7 +609,7 @@ __global__ __launch_bounds__(Tl::NT) void gemm_fixup_kernel(GemmArgs a, int P, l
     constexpr int TN = Tl::FTN, TM = Tl::FTM, NT = Tl::NT;
     constexpr int NV = TN * TM * 4;
     const int nbM = (a.M + Tl::BM - 1) / Tl::BM;
-    const int KT = a.K / BK;
+    const int KT = a.K / Tl::KI;
     const int tile = blockIdx.x, tid = threadIdx.x;
     const long long tb = (long long)tile * KT, te = tb + KT;
     const int pf = (int)(((tb + 1) * P - 1) / T), pl = (int)((te * P - 1) / T);
@@ -522,7 +645,7 @@ template <class Tl, int EPI>
 hipError_t launch_tile(const GemmArgs& a, bool sk, hipStream_t st) {
     const int nbN = (a.N + Tl::BN - 1) / Tl::BN, nbM = (a.M + Tl::BM - 1) / Tl::BM;
     const int tiles = nbN * nbM;
-    const long long T = (long long)tiles * (a.K / BK);
+    const long long T = (long long)tiles * (a.K / Tl::KI);
     if (sk) {
         if (!a.sk_part || (size_t)SK_P * 2 * Tl::BN * Tl::BM > a.sk_part_floats) return hipErrorInvalidValue;
         hipLaunchKernelGGL((gemm_kernel<Tl, EPI, true>), dim3(SK_P), dim3(Tl::NT), 0, st, a, SK_P, T);
@@ -539,22 +662,22 @@ template <int EPI>
 hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
     int cfg = a.force_cfg;
     if (cfg == GCFG_AUTO) {
-        // Picked from measured sweeps over the forward's shapes (M = 512,
-        // 2048, 8192 rows; N = 3D, D, 2F, V; K = D or F) on MI355X.
-        // Stream-K only pays when every block gets at least two K-iterations.
-        const long long KT = a.K / BK;
+        // Picked from measured sweeps over the forward's shapes on MI355X (M =
+        // 512, 2048, 8192 rows; N = 3D, D, 2F, V; K = D or F; random fp16
+        // operands).  256x256 when there are enough tiles to fill the chip,
+        // 256x128 for mid counts, stream-K 256x128 / 128x128 for the
+        // narrow Wo and W2 shapes; stream-K only when every block gets at
+        // least two 32-wide k-iterations.
+        const long long KT = a.K / 32;
         const int t256 = ((a.N + 255) / 256) * ((a.M + 255) / 256);
+        const int t256x128 = ((a.N + 255) / 256) * ((a.M + 127) / 128);
         const int t128 = ((a.N + 127) / 128) * ((a.M + 127) / 128);
         const bool sk_ok = a.sk_part && (size_t)SK_P * 2 * 256 * 256 <= a.sk_part_floats;
-        const bool sk256 = sk_ok && t256 * KT >= 2 * SK_P, sk128 = sk_ok && t128 * KT >= 2 * SK_P;
-        if (t256 >= 600 && a.N >= 16384) cfg = GCFG_G8_256x256;
-        else if (t256 >= 300) cfg = sk256 ? GCFG_G8_256x256_SK : GCFG_G8_256x256;
-        else if (a.K >= 8192 && sk_ok)
-            cfg = t256 >= 100 ? (sk256 ? GCFG_G8_256x256_SK : GCFG_G8_256x256)
-                              : (sk128 ? GCFG_P2_128x128_SK : GCFG_P2_128x128);
-        else if (a.N >= 16384 && t256 >= 200) cfg = GCFG_G8_256x256;
-        else if (t256 < 64 && sk128) cfg = GCFG_P2_128x128_SK;
-        else cfg = GCFG_P2_128x128;
+        if (t256 >= 160) cfg = GCFG_D8_256x256;
+        else if (a.K >= 8192)
+            cfg = sk_ok && t256x128 * KT >= 2 * SK_P ? GCFG_D4_256x128_SK : GCFG_D8_256x128;
+        else if (t256x128 >= 128) cfg = GCFG_D8_256x128;
+        else cfg = sk_ok && t128 * KT >= 2 * SK_P ? GCFG_D4_128x128_SK : GCFG_D4_128x128;
     }
     switch (cfg) {
         case GCFG_128x128: return launch_tile<LdsTile<2, 2>, EPI>(a, false, st);
@@ -562,6 +685,16 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         case GCFG_P2_128x128_SK: return launch_tile<LdsTile2<2, 2>, EPI>(a, true, st);
         case GCFG_G8_256x256: return launch_tile<GTile<2, 4, 4, 2>, EPI>(a, false, st);
         case GCFG_G8_256x256_SK: return launch_tile<GTile<2, 4, 4, 2>, EPI>(a, true, st);
+        case GCFG_D8_256x256: return launch_tile<DTile<2, 4, 4, 2>, EPI>(a, false, st);
+        case GCFG_D8_256x256_SK: return launch_tile<DTile<2, 4, 4, 2>, EPI>(a, true, st);
+        case GCFG_D4_128x128: return launch_tile<DTile<2, 2, 2, 2>, EPI>(a, false, st);
+        case GCFG_D4_128x128_SK: return launch_tile<DTile<2, 2, 2, 2>, EPI>(a, true, st);
+        case GCFG_D8_256x128: return launch_tile<DTile<4, 2, 2, 2>, EPI>(a, false, st);
+        case GCFG_D8_256x128_SK: return launch_tile<DTile<4, 2, 2, 2>, EPI>(a, true, st);
+        case GCFG_D4_256x256: return launch_tile<DTile<2, 2, 4, 4>, EPI>(a, false, st);
+        case GCFG_D4_256x256_SK: return launch_tile<DTile<2, 2, 4, 4>, EPI>(a, true, st);
+        case GCFG_D4_256x128: return launch_tile<DTile<2, 2, 4, 2>, EPI>(a, false, st);
+        case GCFG_D4_256x128_SK: return launch_tile<DTile<2, 2, 4, 2>, EPI>(a, true, st);
     }
     return hipErrorInvalidValue;
 }
@@ -571,7 +704,7 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
 size_t gemm_sk_part_floats() { return (size_t)SK_P * 2 * 256 * 256; }
 
 hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
-    if (a.K % BK != 0 || a.N % 4 != 0 || a.M <= 0) return hipErrorInvalidValue;
+    if (a.K % 128 != 0 || a.N % 4 != 0 || a.M <= 0) return hipErrorInvalidValue;
     switch (epi) {
         case EPI_F32: return launch_epi<EPI_F32>(a, st);
         case EPI_RESID: return launch_epi<EPI_RESID>(a, st);

@@ -39,6 +39,16 @@ enum GemmCfg {
     GCFG_P2_128x128_SK = 3,  // ... stream-K
     GCFG_G8_256x256 = 4,     // 8 waves 2x4 (128x64 each), 256x256 tile
     GCFG_G8_256x256_SK = 5,  // ... stream-K
+    GCFG_D8_256x256 = 6,     // DMA-to-LDS 4-stage pipeline, 8 waves (128x64 each)
+    GCFG_D8_256x256_SK = 7,
+    GCFG_D4_128x128 = 8,     // DMA-to-LDS, 4 waves (64x64 each)
+    GCFG_D4_128x128_SK = 9,
+    GCFG_D8_256x128 = 10,    // DMA-to-LDS, 8 waves (64x64 each)
+    GCFG_D8_256x128_SK = 11,
+    GCFG_D4_256x256 = 12,    // DMA-to-LDS, 4 waves (128x128 each, accumulators in AGPRs)
+    GCFG_D4_256x256_SK = 13,
+    GCFG_D4_256x128 = 14,    // DMA-to-LDS, 4 waves (128x64 each)
+    GCFG_D4_256x128_SK = 15,
 };
 // Floats of stream-K workspace any prefill GEMM needs.
 size_t gemm_sk_part_floats();
