@@ -601,22 +601,25 @@ __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long lo
     }
 }
 
-// Stream-K fixup: one block per tile.  A tile covered by a single block was
-// finished by gemm_kernel; for a split tile, sum the partials of its
-// contributing blocks in block order (deterministic) and run the epilogue.
+// Stream-K fixup: one block per (tile, slice of SL 32-row tiles of every
+// wave; SL = 2 for SwiGLU, whose epilogue pairs W1/W3 tiles).  A tile covered
+// by a single block was finished by gemm_kernel; for a split tile, sum the
+// partials of its contributing blocks in block order (deterministic) and run
+// the epilogue on the slice.
 template <class Tl, int EPI>
 __global__ __launch_bounds__(Tl::NT) void gemm_fixup_kernel(GemmArgs a, int P, long long T) {
     constexpr int TN = Tl::FTN, TM = Tl::FTM, NT = Tl::NT;
     constexpr int NV = TN * TM * 4;
+    constexpr int SL = EPI == EPI_SWIGLU ? 2 : 1;
     const int nbM = (a.M + Tl::BM - 1) / Tl::BM;
     const int KT = a.K / Tl::KI;
-    const int tile = blockIdx.x, tid = threadIdx.x;
+    const int tile = blockIdx.x, i0 = blockIdx.y * SL, tid = threadIdx.x;
     const long long tb = (long long)tile * KT, te = tb + KT;
     const int pf = (int)(((tb + 1) * P - 1) / T), pl = (int)((te * P - 1) / T);
     if (pf == pl) return;
-    typename Tl::Acc acc;
+    Frag<SL, TM> acc;
 #pragma unroll
-    for (int i = 0; i < TN; ++i)
+    for (int i = 0; i < SL; ++i)
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
     for (int c = pf; c <= pl; ++c) {
@@ -625,12 +628,12 @@ __global__ __launch_bounds__(Tl::NT) void gemm_fixup_kernel(GemmArgs a, int P, l
         const int cslot = ((long long)c * T / P >= tb) ? 0 : 1;
         const f32x4* part = (const f32x4*)a.sk_part + ((size_t)(c * 2 + cslot) * NV) * NT + tid;
 #pragma unroll
-        for (int i = 0; i < TN; ++i)
+        for (int i = 0; i < SL; ++i)
 #pragma unroll
             for (int j = 0; j < TM; ++j)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const f32x4 o = part[(size_t)((i * TM + j) * 4 + q) * NT];
+                    const f32x4 o = part[(size_t)(((i0 + i) * TM + j) * 4 + q) * NT];
                     acc.v[i][j][4 * q] += o[0];
                     acc.v[i][j][4 * q + 1] += o[1];
                     acc.v[i][j][4 * q + 2] += o[2];
@@ -638,7 +641,7 @@ __global__ __launch_bounds__(Tl::NT) void gemm_fixup_kernel(GemmArgs a, int P, l
                 }
     }
     const int nb = tile / nbM, mb = tile - nb * nbM;
-    epilogue<TN, TM, EPI>(a, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
+    epilogue<SL, TM, EPI>(a, Tl::nw(nb * Tl::BN) + 32 * i0, Tl::mw(mb * Tl::BM), acc);
 }
 
 template <class Tl, int EPI>
@@ -651,7 +654,9 @@ hipError_t launch_tile(const GemmArgs& a, bool sk, hipStream_t st) {
         hipLaunchKernelGGL((gemm_kernel<Tl, EPI, true>), dim3(SK_P), dim3(Tl::NT), 0, st, a, SK_P, T);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((gemm_fixup_kernel<Tl, EPI>), dim3(tiles), dim3(Tl::NT), 0, st, a, SK_P, T);
+        constexpr int SL = EPI == EPI_SWIGLU ? 2 : 1;
+        hipLaunchKernelGGL((gemm_fixup_kernel<Tl, EPI>), dim3(tiles, Tl::FTN / SL), dim3(Tl::NT), 0, st, a,
+                           SK_P, T);
     } else {
         hipLaunchKernelGGL((gemm_kernel<Tl, EPI, false>), dim3(tiles), dim3(Tl::NT), 0, st, a, 1, T);
     }
