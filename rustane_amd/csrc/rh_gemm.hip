@@ -374,8 +374,10 @@ struct DTile {
     static constexpr int BN = 32 * TN * WGN, BM = 32 * TM * WGM, NT = 64 * WGN * WGM;
     static constexpr int FTN = TN, FTM = TM, KI = 32, NS = 4;
     static constexpr int NWF = BN / 16, NXF = BM / 16, NWAVE = WGN * WGM;
-    static constexpr int LPS = (NWF + NXF) / NWAVE;  // DMA instructions per wave per stage
-    static_assert(LPS * NWAVE == NWF + NXF, "fragments must split evenly over the waves");
+    // DMA instructions per wave per stage; when the fragments do not split
+    // evenly, surplus slots repeat the last fragment (identical bytes to the
+    // same LDS place), so every wave issues the same count and vmcnt stays exact.
+    static constexpr int LPS = (NWF + NXF + NWAVE - 1) / NWAVE;
     static constexpr int SH = (NWF + NXF) * 512;     // halves per stage
     using Acc = Frag<TN, TM>;
     struct Smem {};
@@ -396,7 +398,7 @@ struct DTile {
         int gstep[LPS], loff[LPS];
 #pragma unroll
         for (int q = 0; q < LPS; ++q) {
-            const int f = wv * LPS + q;
+            const int f = min(wv * LPS + q, NWF + NXF - 1);
             loff[q] = f * 512;
             if (f < NWF) {
                 const int rb = min((n0 >> 4) + f, ((a.N + 15) >> 4) - 1);
@@ -491,19 +493,20 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, int nw, int mw,
         const int m = mw + j * 32 + (lane & 31);
         if (m >= M) continue;
         if constexpr (EPI == EPI_SWIGLU) {
-            // Tiles (i, i+1), i even, are 32 W1 rows and the matching 32 W3
-            // rows of one 64-row block of the interleaved W1|W3 weight.
+            // W1|W3 is interleaved in 16-row groups: rows 0..15 of 32-row tile T
+            // are W1 rows of features 16T.., rows 16..31 the matching W3 rows,
+            // and row r + 16 sits in the same lane as row r (accumulator + 8).
 #pragma unroll
-            for (int i = 0; i < TN; i += 2) {
-                const int fb = (nw + i * 32) >> 6;
+            for (int i = 0; i < TN; ++i) {
+                const int T = (nw + i * 32) >> 5;
 #pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    const int f = 32 * fb + 8 * q4 + 4 * (lane >> 5);
+                for (int q4 = 0; q4 < 2; ++q4) {
+                    const int f = 16 * T + 8 * q4 + 4 * (lane >> 5);
                     if (f >= a.ldo) continue;
                     f16x4 g;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float h1 = acc.v[i][j][4 * q4 + r], h3 = acc.v[i + 1][j][4 * q4 + r];
+                        const float h1 = acc.v[i][j][4 * q4 + r], h3 = acc.v[i][j][4 * q4 + 8 + r];
                         g[r] = (f16)(silu_f(h1) * h3);
                     }
                     *(f16x4*)(a.out_f16 + (size_t)m * a.ldo + f) = g;
@@ -601,8 +604,7 @@ __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long lo
     }
 }
 
-// Stream-K fixup: one block per (tile, slice of SL 32-row tiles of every
-// wave; SL = 2 for SwiGLU, whose epilogue pairs W1/W3 tiles).  A tile covered
+// Stream-K fixup: one block per (tile, 32-row tile of every wave).  A tile covered
 // by a single block was finished by gemm_kernel; for a split tile, sum the
 // partials of its contributing blocks in block order (deterministic) and run
 // the epilogue on the slice.
@@ -610,7 +612,7 @@ template <class Tl, int EPI>
 __global__ __launch_bounds__(Tl::NT) void gemm_fixup_kernel(GemmArgs a, int P, long long T) {
     constexpr int TN = Tl::FTN, TM = Tl::FTM, NT = Tl::NT;
     constexpr int NV = TN * TM * 4;
-    constexpr int SL = EPI == EPI_SWIGLU ? 2 : 1;
+    constexpr int SL = 1;
     const int nbM = (a.M + Tl::BM - 1) / Tl::BM;
     const int KT = a.K / Tl::KI;
     const int tile = blockIdx.x, i0 = blockIdx.y * SL, tid = threadIdx.x;
@@ -654,9 +656,7 @@ hipError_t launch_tile(const GemmArgs& a, bool sk, hipStream_t st) {
         hipLaunchKernelGGL((gemm_kernel<Tl, EPI, true>), dim3(SK_P), dim3(Tl::NT), 0, st, a, SK_P, T);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        constexpr int SL = EPI == EPI_SWIGLU ? 2 : 1;
-        hipLaunchKernelGGL((gemm_fixup_kernel<Tl, EPI>), dim3(tiles, Tl::FTN / SL), dim3(Tl::NT), 0, st, a,
-                           SK_P, T);
+        hipLaunchKernelGGL((gemm_fixup_kernel<Tl, EPI>), dim3(tiles, Tl::FTN), dim3(Tl::NT), 0, st, a, SK_P, T);
     } else {
         hipLaunchKernelGGL((gemm_kernel<Tl, EPI, false>), dim3(tiles), dim3(Tl::NT), 0, st, a, 1, T);
     }
@@ -667,22 +667,33 @@ template <int EPI>
 hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
     int cfg = a.force_cfg;
     if (cfg == GCFG_AUTO) {
-        // Picked from measured sweeps over the forward's shapes on MI355X (M =
-        // 512, 2048, 8192 rows; N = 3D, D, 2F, V; K = D or F; random fp16
-        // operands).  256x256 when there are enough tiles to fill the chip,
-        // 256x128 for mid counts, stream-K 256x128 / 128x128 for the
-        // narrow Wo and W2 shapes; stream-K only when every block gets at
-        // least two 32-wide k-iterations.
+        // Data-parallel tiles: estimated time = rounds of one block per CU x
+        // tile FLOPs / that tile's sustained per-CU rate.  The rates are
+        // measured on MI355X with random fp16 operands (TFLOP/s per CU at full
+        // occupancy); the estimate trades wave quantization (e.g. 172 vs 230
+        // tiles at M = 512) against per-tile efficiency.  Narrow outputs (Wo)
+        // and long K (W2) use stream-K instead, when every block gets at least
+        // two 32-wide k-iterations.
+        struct Cand { int cfg, bn, bm; float rate; };
+        constexpr Cand dp[] = {{GCFG_D8_256x256, 256, 256, 4.2f}, {GCFG_D8_192x256, 192, 256, 3.5f},
+                               {GCFG_D8_256x128, 256, 128, 4.0f}, {GCFG_D4_192x128, 192, 128, 3.3f},
+                               {GCFG_D4_128x128, 128, 128, 2.7f}};
         const long long KT = a.K / 32;
-        const int t256 = ((a.N + 255) / 256) * ((a.M + 255) / 256);
         const int t256x128 = ((a.N + 255) / 256) * ((a.M + 127) / 128);
         const int t128 = ((a.N + 127) / 128) * ((a.M + 127) / 128);
         const bool sk_ok = a.sk_part && (size_t)SK_P * 2 * 256 * 256 <= a.sk_part_floats;
-        if (t256 >= 160) cfg = GCFG_D8_256x256;
-        else if (a.K >= 8192)
-            cfg = sk_ok && t256x128 * KT >= 2 * SK_P ? GCFG_D4_256x128_SK : GCFG_D8_256x128;
-        else if (t256x128 >= 128) cfg = GCFG_D8_256x128;
-        else cfg = sk_ok && t128 * KT >= 2 * SK_P ? GCFG_D4_128x128_SK : GCFG_D4_128x128;
+        if (sk_ok && a.K >= 8192 && t256x128 < 160 && t256x128 * KT >= 2 * SK_P) {
+            cfg = GCFG_D4_256x128_SK;
+        } else if (sk_ok && t128 < 160 && t128 * KT >= 2 * SK_P) {
+            cfg = GCFG_D4_128x128_SK;
+        } else {
+            float best = 3.0e38f;
+            for (const Cand& c : dp) {
+                const long long tiles = (long long)((a.N + c.bn - 1) / c.bn) * ((a.M + c.bm - 1) / c.bm);
+                const float t = (float)((tiles + SK_P - 1) / SK_P) * (float)c.bn * (float)c.bm / c.rate;
+                if (t < best) { best = t; cfg = c.cfg; }
+            }
+        }
     }
     switch (cfg) {
         case GCFG_128x128: return launch_tile<LdsTile<2, 2>, EPI>(a, false, st);
@@ -700,6 +711,10 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         case GCFG_D4_256x256_SK: return launch_tile<DTile<2, 2, 4, 4>, EPI>(a, true, st);
         case GCFG_D4_256x128: return launch_tile<DTile<2, 2, 4, 2>, EPI>(a, false, st);
         case GCFG_D4_256x128_SK: return launch_tile<DTile<2, 2, 4, 2>, EPI>(a, true, st);
+        case GCFG_D4_192x128: return launch_tile<DTile<2, 2, 3, 2>, EPI>(a, false, st);
+        case GCFG_D4_192x128_SK: return launch_tile<DTile<2, 2, 3, 2>, EPI>(a, true, st);
+        case GCFG_D8_192x256: return launch_tile<DTile<2, 4, 3, 2>, EPI>(a, false, st);
+        case GCFG_D8_192x256_SK: return launch_tile<DTile<2, 4, 3, 2>, EPI>(a, true, st);
     }
     return hipErrorInvalidValue;
 }
@@ -714,7 +729,7 @@ hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
         case EPI_F32: return launch_epi<EPI_F32>(a, st);
         case EPI_RESID: return launch_epi<EPI_RESID>(a, st);
         case EPI_SWIGLU:
-            if (a.N % 64 != 0) return hipErrorInvalidValue;
+            if (a.N % 32 != 0) return hipErrorInvalidValue;
             return launch_epi<EPI_SWIGLU>(a, st);
         case EPI_QKV: return launch_epi<EPI_QKV>(a, st);
     }

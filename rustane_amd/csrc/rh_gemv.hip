@@ -37,9 +37,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
     const int K = a.K, N = a.N;
     int rows[RT];
     if constexpr (EPI == GV_SWIGLU) {
-        const int jb = blockIdx.x >> 1, u = blockIdx.x & 1;
-        rows[0] = 64 * jb + 16 * u;
-        rows[1] = 64 * jb + 32 + 16 * u;
+        // W1|W3 interleaved in 16-row groups: block b owns features 16b..16b+15
+        rows[0] = 32 * blockIdx.x;
+        rows[1] = 32 * blockIdx.x + 16;
     } else {
         rows[0] = blockIdx.x * 16;
     }
@@ -155,8 +155,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
     // lane holds rows rows[t] + 4g + (0..3) for token `tok`
     if constexpr (EPI == GV_SWIGLU) {
         if (!xvalid) return;
-        const int jb = blockIdx.x >> 1, u = blockIdx.x & 1;
-        const int f = 32 * jb + 16 * u + 4 * g;
+        const int f = 16 * blockIdx.x + 4 * g;
         f16x4 gv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) gv[e] = (f16)(silu_f(acc[0][e]) * acc[1][e]);
@@ -336,7 +335,7 @@ hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t st) {
         case GV_RESID: e = launch_variant<GV_RESID, 1>(v, a, nblk, st); break;
         case GV_QKV: e = launch_variant<GV_QKV, 1>(v, a, nblk, st); break;
         case GV_SWIGLU:
-            if (a.N % 64 != 0) return hipErrorInvalidValue;
+            if (a.N % 32 != 0) return hipErrorInvalidValue;
             e = launch_variant<GV_SWIGLU, 2>(v, a, a.N / 32, st);
             break;
         default: return hipErrorInvalidValue;

@@ -49,6 +49,10 @@ enum GemmCfg {
     GCFG_D4_256x256_SK = 13,
     GCFG_D4_256x128 = 14,    // DMA-to-LDS, 4 waves (128x64 each)
     GCFG_D4_256x128_SK = 15,
+    GCFG_D4_192x128 = 16,    // DMA-to-LDS, 4 waves (96x64 each)
+    GCFG_D4_192x128_SK = 17,
+    GCFG_D8_192x256 = 18,    // DMA-to-LDS, 8 waves (96x64 each)
+    GCFG_D8_192x256_SK = 19,
 };
 // Floats of stream-K workspace any prefill GEMM needs.
 size_t gemm_sk_part_floats();
@@ -124,7 +128,8 @@ hipError_t launch_fill_f32(float* p, float v, size_t n, hipStream_t st);
 // N padded to a multiple of 16.
 // Transposing pack: element (row_map(c), k = r) = half(src[r*C + c]) for a
 // [R][C] fp32 source, K = ldd.  map: 0 identity rows (dst row = row_off + c),
-// 1 = W1/W3 interleave (dst row = 64*(c/32) + c%32 + row_off).
+// 1 = W1/W3 interleave in 16-row groups (dst row = 32*(c/16) + c%16 + row_off,
+// row_off 0 for W1 and 16 for W3).
 hipError_t launch_pack_transpose(const float* src, f16* dst, int R, int C, int ldd, int map,
                                  int row_off, hipStream_t st);
 hipError_t launch_unpack_transpose(const f16* src, float* dst, int R, int C, int lds, int map,

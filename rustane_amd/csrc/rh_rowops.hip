@@ -104,7 +104,7 @@ __global__ void fill_kernel(float* p, float v, size_t n) {
 }
 
 __device__ __forceinline__ int dst_row(int c, int map, int row_off) {
-    return map == 1 ? 64 * (c >> 5) + (c & 31) + row_off : c + row_off;
+    return map == 1 ? 32 * (c >> 4) + (c & 15) + row_off : c + row_off;
 }
 
 // 32x32 tiles through LDS: src [R][C] (in x out) -> dst row dst_row(c), k = r,

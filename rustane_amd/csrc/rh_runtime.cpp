@@ -406,7 +406,7 @@ TensorMap layer_map(rh_ctx* ctx, int l, int j) {
         case 2: return {D, D, 0, 2 * D, W.wqkv, D};
         case 3: return {D, D, 0, 0, W.wo, D};
         case 4: return {D, F, 1, 0, W.w13, D};
-        case 5: return {D, F, 1, 32, W.w13, D};
+        case 5: return {D, F, 1, 16, W.w13, D};
         case 6: return {D, F, -1, 0, W.w2, F};
     }
     return {0, 0, -1, 0, nullptr, 0};
