@@ -169,12 +169,13 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
     float lt = l_run + __shfl_xor(l_run, 16, RH_WAVE);
     lt += __shfl_xor(lt, 32, RH_WAVE);
     if (qi < S) {
+        // token-major [B*S][H*HD] in fragment order (the Wo GEMM's operand layout)
         const float inv = 1.0f / lt;
-        f16* op = out + ((size_t)b * S + qi) * ((size_t)H * HD) + (size_t)h * HD + 4 * g;
+        const int row = b * S + qi;
 #pragma unroll
         for (int j = 0; j < NHT; ++j)
-            *(f16x4*)(op + 16 * j) = f16x4{(f16)(o[j][0] * inv), (f16)(o[j][1] * inv),
-                                           (f16)(o[j][2] * inv), (f16)(o[j][3] * inv)};
+            *(f16x4*)(out + frag_off(row, h * HD + 16 * j + 4 * g, H * HD)) =
+                f16x4{(f16)(o[j][0] * inv), (f16)(o[j][1] * inv), (f16)(o[j][2] * inv), (f16)(o[j][3] * inv)};
     }
 }
 

@@ -4,26 +4,23 @@
 // (kernels/sdpa_fwd.rs:115-117 QKV, dyn_matmul.rs:15-75 Wo, ffn_fused.rs:80-160
 // W1/W3/W2, full_model.rs:555-567 tied logits):
 //     Y[m][n] = sum_k X[m][k] * W[n][k]
-// X is the token-major fp16 activation [M, K]; W is the weight repacked at
-// upload to [N, K] ("out x in") in fragment order (frag_off: 1 KB pieces of
-// 16 rows x 32 k, the decode GEMV's operand layout), so both operands stream
-// along k.  The MFMA computes the transposed tile (A = weight rows, B = token
-// rows): each lane's
-// accumulator then holds 4 consecutive output features of one token, which
-// makes the RoPE pairs (2i, 2i+1) and 16-byte fp32 stores lane-local.
+// X is the token-major fp16 activation [M, K] and W the weight repacked at
+// upload to [N, K] ("out x in"); both are stored in fragment order (frag_off:
+// 1 KB pieces of 16 rows x 32 k), so both stream along k in 1 KB pieces.  The
+// MFMA computes the transposed tile (A = weight rows, B = token rows): each
+// lane's accumulator then holds 4 consecutive output features of one token,
+// which makes the RoPE pairs (2i, 2i+1) and 16-byte fp32 stores lane-local.
 //
-// Tile policies (all: 32x32x16 MFMA, 64-wide k-slabs, both operands staged
-// through LDS with rows padded by 16 bytes so the 16-byte fragment reads are
-// bank-conflict free, fragments double-buffered in registers):
-//   LdsTile<2,2>   128x128, 4 waves (2x2, 64x64 each), one slab of prefetch
-//   LdsTile2<2,2>  same tile, global loads issued two slabs ahead
-//   GTile<2,4,4,2> 256x256, 8 waves (2x4, 128x64 each, 2 per SIMD); half the
-//                  vector-L1 bytes per FLOP of the 128x128 tile
+// Tile policy: DTile (below) -- both operands in fragment order in HBM, moved
+// global -> LDS by DMA through a 4-stage pipeline of 32-wide k slices,
+// 32x32x16 MFMA on fragments double-buffered in registers.  Instantiated as
+// 256x256 (8 waves of 128x64, or 4 waves of 128x128 with AGPR accumulators),
+// 256x128, 192x256, 192x128 and 128x128; a cost model picks one per shape.
 // Out-of-range rows are clamped, not predicated (they only feed accumulator
 // entries the epilogue never stores), so the loads are branch-free.  Tiles are
 // remapped so blocks sharing a weight panel run on the same XCD (one L2).
 //
-// Stream-K: P blocks split the tiles x k-slabs iteration space evenly.  A
+// Stream-K: P blocks split the tiles x k-iterations space evenly.  A
 // block whose range covers only part of a tile stores its fp32 partial; a
 // second kernel sums each split tile's partials in block order
 // (deterministic) and runs the epilogue.  Blocks never communicate inside a
@@ -35,21 +32,7 @@
 namespace rh {
 namespace {
 
-constexpr int BK = 64, LDK = BK + 8;
 constexpr int SK_P = 256;  // stream-K blocks: one per CU
-
-// Weight load slot c of a BN x BK slab.  W is in fragment order (frag_off):
-// 64 consecutive slots read one 1 KB fragment (16 rows x 32 k), two
-// fragments cover the slab's 64 k of a 16-row block, and the slab at k0
-// starts k0 * 16 elements further on.  Row blocks past N are clamped (their
-// rows only feed accumulator rows the epilogue never stores).  lds_off is the
-// slot's place in the row-major [BN][LDK] LDS tile.
-__device__ __forceinline__ const f16* wslot(const GemmArgs& a, int n0, int c, int& lds_off) {
-    const int sb = c >> 6, l = c & 63, rbl = sb >> 1, uu = sb & 1;
-    const int rb = min((n0 >> 4) + rbl, ((a.N + 15) >> 4) - 1);
-    lds_off = (rbl * 16 + (l & 15)) * LDK + uu * 32 + (l >> 4) * 8;
-    return a.W + (size_t)rb * a.K * 16 + uu * 512 + l * 8;
-}
 
 template <int TN, int TM>
 struct Frag {
@@ -57,312 +40,13 @@ struct Frag {
 };
 
 // ---------------------------------------------------------------------------
-// Tile policy 1 (LdsTile): both operands staged through LDS; 2 x 2 waves, each
-// TN x TM tiles of 32x32.  Block = (64 TN) features x (64 TM) tokens.
-// Rows past N or M are clamped to the last valid row instead of predicated:
-// they only feed accumulator rows/columns the epilogue never stores, and the
-// loads stay branch-free.  Fragments are double-buffered in registers so the
-// LDS reads of k-step kk+1 are in flight under the MFMAs of step kk.
-template <int TN, int TM>
-struct LdsTile {
-    static constexpr int BN = 64 * TN, BM = 64 * TM, NT = 256, FTN = TN, FTM = TM, KI = BK;
-    static constexpr int WCH = BN * BK / 8 / NT, XCH = BM * BK / 8 / NT;
-    using Acc = Frag<TN, TM>;
-    struct Smem {
-        f16 w[2][BN * LDK];
-        f16 x[2][BM * LDK];
-    };
-    __device__ static int nw(int n0) { return n0 + ((threadIdx.x >> 6) & 1) * 32 * TN; }
-    __device__ static int mw(int m0) { return m0 + (threadIdx.x >> 7) * 32 * TM; }
-
-    __device__ static void run(const GemmArgs& a, int n0, int m0, int kb, int ke, Acc& acc, Smem& sm) {
-        const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-        const int wn = wv & 1, wm = wv >> 1;
-        const int K = a.K;
-        const f16* wp[WCH];
-        const f16* xp[XCH];
-        int wo[WCH], xo[XCH];
-#pragma unroll
-        for (int p = 0; p < WCH; ++p) {
-            wp[p] = wslot(a, n0, tid + NT * p, wo[p]);
-        }
-#pragma unroll
-        for (int p = 0; p < XCH; ++p) {
-            const int c = tid + NT * p, row = c >> 3, col = (c & 7) * 8;
-            xp[p] = a.X + (size_t)min(m0 + row, a.M - 1) * K + col;
-            xo[p] = row * LDK + col;
-        }
-        int ao[TN], bo[TM];
-#pragma unroll
-        for (int i = 0; i < TN; ++i) ao[i] = (wn * 32 * TN + i * 32 + (lane & 31)) * LDK + 8 * (lane >> 5);
-#pragma unroll
-        for (int j = 0; j < TM; ++j) bo[j] = (wm * 32 * TM + j * 32 + (lane & 31)) * LDK + 8 * (lane >> 5);
-        f16x8 rw[WCH], rx[XCH];
-        auto gload = [&](int k0) {
-#pragma unroll
-            for (int p = 0; p < WCH; ++p) rw[p] = *(const f16x8*)(wp[p] + (size_t)k0 * 16);
-#pragma unroll
-            for (int p = 0; p < XCH; ++p) rx[p] = *(const f16x8*)(xp[p] + k0);
-        };
-        auto sstore = [&](f16* sw, f16* sx) {
-#pragma unroll
-            for (int p = 0; p < WCH; ++p) *(f16x8*)&sw[wo[p]] = rw[p];
-#pragma unroll
-            for (int p = 0; p < XCH; ++p) *(f16x8*)&sx[xo[p]] = rx[p];
-        };
-#pragma unroll
-        for (int i = 0; i < TN; ++i)
-#pragma unroll
-            for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
-        f16x8 fa[2][TN], fb[2][TM];
-        gload(kb * BK);
-        sstore(sm.w[0], sm.x[0]);
-        __syncthreads();
-        for (int kt = kb; kt < ke; ++kt) {
-            const bool odd = ((kt - kb) & 1) != 0;
-            const f16* ws = odd ? sm.w[1] : sm.w[0];
-            const f16* xs = odd ? sm.x[1] : sm.x[0];
-            if (kt + 1 < ke) gload((kt + 1) * BK);
-#pragma unroll
-            for (int i = 0; i < TN; ++i) fa[0][i] = *(const f16x8*)&ws[ao[i]];
-#pragma unroll
-            for (int j = 0; j < TM; ++j) fb[0][j] = *(const f16x8*)&xs[bo[j]];
-#pragma unroll
-            for (int kk = 0; kk < BK / 16; ++kk) {
-                const int cur = kk & 1, nxt = cur ^ 1;
-                if (kk + 1 < BK / 16) {
-#pragma unroll
-                    for (int i = 0; i < TN; ++i) fa[nxt][i] = *(const f16x8*)&ws[ao[i] + (kk + 1) * 16];
-#pragma unroll
-                    for (int j = 0; j < TM; ++j) fb[nxt][j] = *(const f16x8*)&xs[bo[j] + (kk + 1) * 16];
-                }
-#pragma unroll
-                for (int i = 0; i < TN; ++i)
-#pragma unroll
-                    for (int j = 0; j < TM; ++j) acc.v[i][j] = mfma32(fa[cur][i], fb[cur][j], acc.v[i][j]);
-            }
-            if (kt + 1 < ke) {
-                if (odd) sstore(sm.w[0], sm.x[0]);
-                else sstore(sm.w[1], sm.x[1]);
-            }
-            __syncthreads();
-        }
-    }
-};
-
-// ---------------------------------------------------------------------------
-// Tile policy 1c (GTile): LDS-staged like LdsTile with a WGN x WGM wave grid,
-// each wave TN x TM tiles of 32x32.  256x256 with 8 waves (2 per SIMD, each
-// 128x64) halves the vector-L1 bytes per FLOP of a 128x128 tile while keeping
-// each wave inside 128 accumulator + 128 architectural registers.
-template <int WGN, int WGM, int TN, int TM>
-struct GTile {
-    static constexpr int BN = 32 * TN * WGN, BM = 32 * TM * WGM, NT = 64 * WGN * WGM;
-    static constexpr int FTN = TN, FTM = TM, KI = BK;
-    static constexpr int WCH = BN * BK / 8 / NT, XCH = BM * BK / 8 / NT;
-    static_assert(WCH * NT * 8 == BN * BK && XCH * NT * 8 == BM * BK, "slab must split evenly");
-    using Acc = Frag<TN, TM>;
-    struct Smem {
-        f16 w[2][BN * LDK];
-        f16 x[2][BM * LDK];
-    };
-    __device__ static int nw(int n0) { return n0 + ((threadIdx.x >> 6) % WGN) * 32 * TN; }
-    __device__ static int mw(int m0) { return m0 + ((threadIdx.x >> 6) / WGN) * 32 * TM; }
-
-    __device__ static void run(const GemmArgs& a, int n0, int m0, int kb, int ke, Acc& acc, Smem& sm) {
-        const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-        const int wn = wv % WGN, wm = wv / WGN;
-        const int K = a.K;
-        const f16* wp[WCH];
-        const f16* xp[XCH];
-        int wo[WCH], xo[XCH];
-#pragma unroll
-        for (int p = 0; p < WCH; ++p) {
-            wp[p] = wslot(a, n0, tid + NT * p, wo[p]);
-        }
-#pragma unroll
-        for (int p = 0; p < XCH; ++p) {
-            const int c = tid + NT * p, row = c >> 3, col = (c & 7) * 8;
-            xp[p] = a.X + (size_t)min(m0 + row, a.M - 1) * K + col;
-            xo[p] = row * LDK + col;
-        }
-        int ao[TN], bo[TM];
-#pragma unroll
-        for (int i = 0; i < TN; ++i) ao[i] = (wn * 32 * TN + i * 32 + (lane & 31)) * LDK + 8 * (lane >> 5);
-#pragma unroll
-        for (int j = 0; j < TM; ++j) bo[j] = (wm * 32 * TM + j * 32 + (lane & 31)) * LDK + 8 * (lane >> 5);
-        f16x8 rw[WCH], rx[XCH];
-        auto gload = [&](int k0) {
-#pragma unroll
-            for (int p = 0; p < WCH; ++p) rw[p] = *(const f16x8*)(wp[p] + (size_t)k0 * 16);
-#pragma unroll
-            for (int p = 0; p < XCH; ++p) rx[p] = *(const f16x8*)(xp[p] + k0);
-        };
-        auto sstore = [&](f16* sw, f16* sx) {
-#pragma unroll
-            for (int p = 0; p < WCH; ++p) *(f16x8*)&sw[wo[p]] = rw[p];
-#pragma unroll
-            for (int p = 0; p < XCH; ++p) *(f16x8*)&sx[xo[p]] = rx[p];
-        };
-        auto slab = [&](const f16* ws, const f16* xs) {
-            f16x8 fa[2][TN], fb[2][TM];
-#pragma unroll
-            for (int i = 0; i < TN; ++i) fa[0][i] = *(const f16x8*)&ws[ao[i]];
-#pragma unroll
-            for (int j = 0; j < TM; ++j) fb[0][j] = *(const f16x8*)&xs[bo[j]];
-#pragma unroll
-            for (int kk = 0; kk < BK / 16; ++kk) {
-                const int cur = kk & 1, nxt = cur ^ 1;
-                if (kk + 1 < BK / 16) {
-#pragma unroll
-                    for (int i = 0; i < TN; ++i) fa[nxt][i] = *(const f16x8*)&ws[ao[i] + (kk + 1) * 16];
-#pragma unroll
-                    for (int j = 0; j < TM; ++j) fb[nxt][j] = *(const f16x8*)&xs[bo[j] + (kk + 1) * 16];
-                }
-#pragma unroll
-                for (int i = 0; i < TN; ++i)
-#pragma unroll
-                    for (int j = 0; j < TM; ++j) acc.v[i][j] = mfma32(fa[cur][i], fb[cur][j], acc.v[i][j]);
-            }
-        };
-#pragma unroll
-        for (int i = 0; i < TN; ++i)
-#pragma unroll
-            for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
-        const int klast = (ke - 1) * BK;
-        gload(kb * BK);
-        sstore(sm.w[0], sm.x[0]);
-        __syncthreads();
-        int kt = kb;
-        for (; kt + 1 < ke; kt += 2) {
-            gload((kt + 1) * BK);
-            __builtin_amdgcn_sched_barrier(0);
-            slab(sm.w[0], sm.x[0]);
-            sstore(sm.w[1], sm.x[1]);
-            __syncthreads();
-            gload(min((kt + 2) * BK, klast));
-            __builtin_amdgcn_sched_barrier(0);
-            slab(sm.w[1], sm.x[1]);
-            sstore(sm.w[0], sm.x[0]);
-            __syncthreads();
-        }
-        if (kt < ke) {
-            slab(sm.w[0], sm.x[0]);
-            __syncthreads();
-        }
-    }
-};
-
-// ---------------------------------------------------------------------------
-// Tile policy 1b (LdsTile2): LdsTile with the global loads issued two k-slabs
-// ahead (two register sets), so ~2x the bytes are in flight per block to
-// cover L2/MALL latency.  Slab s: global -> register set s%2 -> LDS buffer
-// s%2 -> MFMA.
-template <int TN, int TM>
-struct LdsTile2 : LdsTile<TN, TM> {
-    using B = LdsTile<TN, TM>;
-    using typename B::Acc;
-    using typename B::Smem;
-    static constexpr int BN = B::BN, BM = B::BM, NT = B::NT, FTN = TN, FTM = TM, KI = BK;
-    static constexpr int WCH = B::WCH, XCH = B::XCH;
-
-    __device__ static void run(const GemmArgs& a, int n0, int m0, int kb, int ke, Acc& acc, Smem& sm) {
-        const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-        const int wn = wv & 1, wm = wv >> 1;
-        const int K = a.K;
-        const f16* wp[WCH];
-        const f16* xp[XCH];
-        int wo[WCH], xo[XCH];
-#pragma unroll
-        for (int p = 0; p < WCH; ++p) {
-            wp[p] = wslot(a, n0, tid + NT * p, wo[p]);
-        }
-#pragma unroll
-        for (int p = 0; p < XCH; ++p) {
-            const int c = tid + NT * p, row = c >> 3, col = (c & 7) * 8;
-            xp[p] = a.X + (size_t)min(m0 + row, a.M - 1) * K + col;
-            xo[p] = row * LDK + col;
-        }
-        int ao[TN], bo[TM];
-#pragma unroll
-        for (int i = 0; i < TN; ++i) ao[i] = (wn * 32 * TN + i * 32 + (lane & 31)) * LDK + 8 * (lane >> 5);
-#pragma unroll
-        for (int j = 0; j < TM; ++j) bo[j] = (wm * 32 * TM + j * 32 + (lane & 31)) * LDK + 8 * (lane >> 5);
-        f16x8 rw0[WCH], rx0[XCH], rw1[WCH], rx1[XCH];
-        auto gload = [&](f16x8 (&rw)[WCH], f16x8 (&rx)[XCH], int k0) {
-#pragma unroll
-            for (int p = 0; p < WCH; ++p) rw[p] = *(const f16x8*)(wp[p] + (size_t)k0 * 16);
-#pragma unroll
-            for (int p = 0; p < XCH; ++p) rx[p] = *(const f16x8*)(xp[p] + k0);
-        };
-        auto sstore = [&](const f16x8 (&rw)[WCH], const f16x8 (&rx)[XCH], f16* sw, f16* sx) {
-#pragma unroll
-            for (int p = 0; p < WCH; ++p) *(f16x8*)&sw[wo[p]] = rw[p];
-#pragma unroll
-            for (int p = 0; p < XCH; ++p) *(f16x8*)&sx[xo[p]] = rx[p];
-        };
-        auto slab = [&](const f16* ws, const f16* xs) {
-            f16x8 fa[2][TN], fb[2][TM];
-#pragma unroll
-            for (int i = 0; i < TN; ++i) fa[0][i] = *(const f16x8*)&ws[ao[i]];
-#pragma unroll
-            for (int j = 0; j < TM; ++j) fb[0][j] = *(const f16x8*)&xs[bo[j]];
-#pragma unroll
-            for (int kk = 0; kk < BK / 16; ++kk) {
-                const int cur = kk & 1, nxt = cur ^ 1;
-                if (kk + 1 < BK / 16) {
-#pragma unroll
-                    for (int i = 0; i < TN; ++i) fa[nxt][i] = *(const f16x8*)&ws[ao[i] + (kk + 1) * 16];
-#pragma unroll
-                    for (int j = 0; j < TM; ++j) fb[nxt][j] = *(const f16x8*)&xs[bo[j] + (kk + 1) * 16];
-                }
-#pragma unroll
-                for (int i = 0; i < TN; ++i)
-#pragma unroll
-                    for (int j = 0; j < TM; ++j) acc.v[i][j] = mfma32(fa[cur][i], fb[cur][j], acc.v[i][j]);
-            }
-        };
-#pragma unroll
-        for (int i = 0; i < TN; ++i)
-#pragma unroll
-            for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
-        // Prefetches are unconditional (k clamped to the last slab; a repeat
-        // load is simply never used) so the wait-count tracking stays exact.
-        const int klast = (ke - 1) * BK;
-        gload(rw0, rx0, kb * BK);
-        gload(rw1, rx1, min((kb + 1) * BK, klast));
-        sstore(rw0, rx0, sm.w[0], sm.x[0]);
-        __syncthreads();
-        int kt = kb;
-        for (; kt + 1 < ke; kt += 2) {
-            // slab kt (even) in LDS 0; set 0 free -> prefetch kt+2; then stage kt+1 (set 1) to LDS 1
-            gload(rw0, rx0, min((kt + 2) * BK, klast));
-            __builtin_amdgcn_sched_barrier(0);  // keep the prefetch issued before the MFMAs
-            slab(sm.w[0], sm.x[0]);
-            sstore(rw1, rx1, sm.w[1], sm.x[1]);
-            __syncthreads();
-            // slab kt+1 (odd) in LDS 1; set 1 free -> prefetch kt+3; then stage kt+2 (set 0) to LDS 0
-            gload(rw1, rx1, min((kt + 3) * BK, klast));
-            __builtin_amdgcn_sched_barrier(0);
-            slab(sm.w[1], sm.x[1]);
-            sstore(rw0, rx0, sm.w[0], sm.x[0]);
-            __syncthreads();
-        }
-        if (kt < ke) {
-            slab(sm.w[0], sm.x[0]);
-            __syncthreads();
-        }
-    }
-};
-
-// ---------------------------------------------------------------------------
-// Tile policy 2 (DTile): operands go global -> LDS by DMA
+// Tile policy (DTile): operands go global -> LDS by DMA
 // (global_load_lds_dwordx4: 16 bytes per lane land at LDS base + 16 * lane),
 // so no registers stage them and NS = 4 stages of 32 k are in flight.  A
 // stage holds BN/16 weight fragments and BM/16 activation fragments of 1 KB
-// each, both in fragment order: the weight is stored that way (each DMA reads
-// 1 KB contiguous) and the row-major activation is gathered into it (lane
-// 16g + r reads row r at k + 8g).  The 32x32x16 MFMA operand of lane 32h + r
+// each; both operands are stored in fragment order in HBM (the activations by
+// the kernels that produce them), so every DMA instruction reads 1 KB
+// contiguous.  The 32x32x16 MFMA operand of lane 32h + r
 // at k16-step s is then lane 16(2s + h) + r%16 of fragment r/16: 16 lanes read
 // 256 contiguous bytes, conflict-free without padding.  One barrier per stage:
 // each wave waits for its own DMA of the stage (an explicit vmcnt, since the
@@ -405,9 +89,9 @@ struct DTile {
                 gp[q] = a.W + (size_t)rb * K * 16 + lane * 8;
                 gstep[q] = 512;  // one 32-k fragment column of the 16-row block
             } else {
-                const int row = min(m0 + 16 * (f - NWF) + (lane & 15), a.M - 1);
-                gp[q] = a.X + (size_t)row * K + 8 * (lane >> 4);
-                gstep[q] = 32;
+                const int rb = min((m0 >> 4) + f - NWF, ((a.M + 15) >> 4) - 1);
+                gp[q] = a.X + (size_t)rb * K * 16 + lane * 8;
+                gstep[q] = 512;
             }
         }
         const int r = lane & 31, h = lane >> 5;
@@ -509,7 +193,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, int nw, int mw,
                         const float h1 = acc.v[i][j][4 * q4 + r], h3 = acc.v[i][j][4 * q4 + 8 + r];
                         g[r] = (f16)(silu_f(h1) * h3);
                     }
-                    *(f16x4*)(a.out_f16 + (size_t)m * a.ldo + f) = g;
+                    *(f16x4*)(a.out_f16 + frag_off(m, f, a.ldo)) = g;
                 }
             }
         } else {
@@ -675,9 +359,9 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         // and long K (W2) use stream-K instead, when every block gets at least
         // two 32-wide k-iterations.
         struct Cand { int cfg, bn, bm; float rate; };
-        constexpr Cand dp[] = {{GCFG_D8_256x256, 256, 256, 4.2f}, {GCFG_D8_192x256, 192, 256, 3.5f},
-                               {GCFG_D8_256x128, 256, 128, 4.0f}, {GCFG_D4_192x128, 192, 128, 3.3f},
-                               {GCFG_D4_128x128, 128, 128, 2.7f}};
+        constexpr Cand dp[] = {{GCFG_D8_256x256, 256, 256, 4.4f}, {GCFG_D8_192x256, 192, 256, 3.9f},
+                               {GCFG_D8_256x128, 256, 128, 4.0f}, {GCFG_D4_192x128, 192, 128, 3.95f},
+                               {GCFG_D4_128x128, 128, 128, 3.7f}};
         const long long KT = a.K / 32;
         const int t256x128 = ((a.N + 255) / 256) * ((a.M + 127) / 128);
         const int t128 = ((a.N + 127) / 128) * ((a.M + 127) / 128);
@@ -696,11 +380,6 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         }
     }
     switch (cfg) {
-        case GCFG_128x128: return launch_tile<LdsTile<2, 2>, EPI>(a, false, st);
-        case GCFG_P2_128x128: return launch_tile<LdsTile2<2, 2>, EPI>(a, false, st);
-        case GCFG_P2_128x128_SK: return launch_tile<LdsTile2<2, 2>, EPI>(a, true, st);
-        case GCFG_G8_256x256: return launch_tile<GTile<2, 4, 4, 2>, EPI>(a, false, st);
-        case GCFG_G8_256x256_SK: return launch_tile<GTile<2, 4, 4, 2>, EPI>(a, true, st);
         case GCFG_D8_256x256: return launch_tile<DTile<2, 4, 4, 2>, EPI>(a, false, st);
         case GCFG_D8_256x256_SK: return launch_tile<DTile<2, 4, 4, 2>, EPI>(a, true, st);
         case GCFG_D4_128x128: return launch_tile<DTile<2, 2, 2, 2>, EPI>(a, false, st);

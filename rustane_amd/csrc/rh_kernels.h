@@ -12,11 +12,11 @@ namespace rh {
 enum GemmEpi { EPI_F32 = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
 
 struct GemmArgs {
-    const f16* W;  // [N, K] row-major (weights, "out x in")
-    const f16* X;  // [M, K] row-major (activations, token-major)
+    const f16* W;  // [N, K] weights ("out x in"), fragment order (frag_off), rows padded to 16
+    const f16* X;  // [M, K] activations (token-major), fragment order, rows padded to 16
     int M, N, K;
     float* out_f32;  // EPI_F32: [M, ldo]; EPI_RESID: residual x [M, ldo], updated in place
-    f16* out_f16;    // EPI_SWIGLU: gate [M, ldo]
+    f16* out_f16;    // EPI_SWIGLU: gate [M, ldo] in fragment order
     int ldo;
     float alpha;     // EPI_RESID: x += alpha * acc
     float softcap;   // EPI_F32: c * tanh(acc / c) when c > 0
@@ -31,27 +31,23 @@ struct GemmArgs {
     size_t sk_part_floats;
     int force_cfg;  // 0 = heuristic; otherwise a GemmCfg value (tuning)
 };
-// Tile configurations of the prefill GEMM.
+// Tile configurations of the prefill GEMM (all: direct-to-LDS 4-stage
+// pipeline; waves x per-wave tile).
 enum GemmCfg {
     GCFG_AUTO = 0,
-    GCFG_128x128 = 1,        // 4 waves 2x2, both operands via LDS, one slab ahead
-    GCFG_P2_128x128 = 2,     // same tile, two slabs of global prefetch
-    GCFG_P2_128x128_SK = 3,  // ... stream-K
-    GCFG_G8_256x256 = 4,     // 8 waves 2x4 (128x64 each), 256x256 tile
-    GCFG_G8_256x256_SK = 5,  // ... stream-K
-    GCFG_D8_256x256 = 6,     // DMA-to-LDS 4-stage pipeline, 8 waves (128x64 each)
-    GCFG_D8_256x256_SK = 7,
-    GCFG_D4_128x128 = 8,     // DMA-to-LDS, 4 waves (64x64 each)
+    GCFG_D8_256x256 = 6,     // 8 waves (128x64 each)
+    GCFG_D8_256x256_SK = 7,  // ... stream-K
+    GCFG_D4_128x128 = 8,     // 4 waves (64x64 each)
     GCFG_D4_128x128_SK = 9,
-    GCFG_D8_256x128 = 10,    // DMA-to-LDS, 8 waves (64x64 each)
+    GCFG_D8_256x128 = 10,    // 8 waves (64x64 each)
     GCFG_D8_256x128_SK = 11,
-    GCFG_D4_256x256 = 12,    // DMA-to-LDS, 4 waves (128x128 each, accumulators in AGPRs)
+    GCFG_D4_256x256 = 12,    // 4 waves (128x128 each, accumulators in AGPRs)
     GCFG_D4_256x256_SK = 13,
-    GCFG_D4_256x128 = 14,    // DMA-to-LDS, 4 waves (128x64 each)
+    GCFG_D4_256x128 = 14,    // 4 waves (128x64 each)
     GCFG_D4_256x128_SK = 15,
-    GCFG_D4_192x128 = 16,    // DMA-to-LDS, 4 waves (96x64 each)
+    GCFG_D4_192x128 = 16,    // 4 waves (96x64 each)
     GCFG_D4_192x128_SK = 17,
-    GCFG_D8_192x256 = 18,    // DMA-to-LDS, 8 waves (96x64 each)
+    GCFG_D8_192x256 = 18,    // 8 waves (96x64 each)
     GCFG_D8_192x256_SK = 19,
 };
 // Floats of stream-K workspace any prefill GEMM needs.
@@ -60,7 +56,7 @@ hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st);
 
 // ---------------- attention ----------------
 // Causal prefill attention: q [B][H][S][hd], k/v [B][H][ctx][hd] (positions
-// 0..S-1), out token-major [B*S][H*hd].
+// 0..S-1), out token-major [B*S][H*hd] in fragment order (rows padded to 16).
 hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* out, int B, int H,
                                int S, int hd, int ctx, hipStream_t st);
 // Decode attention over positions 0..*pos (the current token is at *pos):
@@ -112,8 +108,10 @@ hipError_t launch_argmax_final(const float* pv, const int* pi, int nblk, int B, 
 // ---------------- row ops ----------------
 hipError_t launch_embed(const uint32_t* tok, const f16* E, float* x, int rows, int D, int V,
                         int* err, hipStream_t st);
+// out [rows, D] row-major, or in fragment order (frag_off, rows padded to 16)
+// when frag is set (the layout of every prefill GEMM operand).
 hipError_t launch_rmsnorm(const float* x, const float* gamma, f16* out, int rows, int D,
-                          float eps, hipStream_t st);
+                          float eps, hipStream_t st, bool frag = false);
 // rmsnorm of rows x[(r*stride + offset)] -> out[r]  (last-position gather)
 hipError_t launch_rmsnorm_strided(const float* x, const float* gamma, f16* out, int rows, int D,
                                   float eps, int stride_rows, int offset_rows, hipStream_t st);

@@ -34,7 +34,7 @@ __global__ void embed_kernel(const uint32_t* tok, const f16* E, float* x, int D,
 
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const float* gamma, f16* out,
                                                       int D, float eps, int stride_rows,
-                                                      int offset_rows) {
+                                                      int offset_rows, int frag) {
     __shared__ float red[4];
     const int row = blockIdx.x;
     const float* xr = x + ((size_t)row * stride_rows + offset_rows) * D;
@@ -49,8 +49,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const floa
     for (int i = threadIdx.x * 4; i < D; i += 1024) {
         const f32x4 v = *(const f32x4*)(xr + i);
         const f32x4 gm = *(const f32x4*)(gamma + i);
-        *(f16x4*)(o + i) = f16x4{(f16)(v[0] * r * gm[0]), (f16)(v[1] * r * gm[1]),
-                                 (f16)(v[2] * r * gm[2]), (f16)(v[3] * r * gm[3])};
+        f16* dst = frag ? out + frag_off(row, i, D) : o + i;
+        *(f16x4*)dst = f16x4{(f16)(v[0] * r * gm[0]), (f16)(v[1] * r * gm[1]),
+                             (f16)(v[2] * r * gm[2]), (f16)(v[3] * r * gm[3])};
     }
 }
 
@@ -208,14 +209,14 @@ hipError_t launch_embed(const uint32_t* tok, const f16* E, float* x, int rows, i
     return hipGetLastError();
 }
 hipError_t launch_rmsnorm(const float* x, const float* gamma, f16* out, int rows, int D, float eps,
-                          hipStream_t st) {
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps, 1, 0);
+                          hipStream_t st, bool frag) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps, 1, 0, frag ? 1 : 0);
     return hipGetLastError();
 }
 hipError_t launch_rmsnorm_strided(const float* x, const float* gamma, f16* out, int rows, int D,
                                   float eps, int stride_rows, int offset_rows, hipStream_t st) {
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps,
-                       stride_rows, offset_rows);
+                       stride_rows, offset_rows, 0);
     return hipGetLastError();
 }
 hipError_t launch_cross_entropy(const float* logits, const uint32_t* targets, float* loss, int rows,

@@ -161,13 +161,15 @@ int ensure_workspace(rh_ctx* ctx, int M) {
                     ctx->logits, ctx->tok_loss, ctx->mean, ctx->d_tok, ctx->d_tgt};
     for (void* p : olds) dfree(ctx, p);
     const size_t D = D_(ctx), F = F_(ctx), V = V_(ctx), m = (size_t)M;
+    // GEMM operands (xn, attn, gate) are in fragment order: rows padded to 16
+    const size_t m16 = (m + 15) / 16 * 16;
     RCK(dalloc(ctx, &ctx->x, m * D));
-    RCK(dalloc(ctx, &ctx->xn, m * D));
+    RCK(dalloc(ctx, &ctx->xn, m16 * D));
     RCK(dalloc(ctx, &ctx->q, m * D));
     RCK(dalloc(ctx, &ctx->kbuf, m * D));
     RCK(dalloc(ctx, &ctx->vbuf, m * D));
-    RCK(dalloc(ctx, &ctx->attn, m * D));
-    RCK(dalloc(ctx, &ctx->gate, m * F));
+    RCK(dalloc(ctx, &ctx->attn, m16 * D));
+    RCK(dalloc(ctx, &ctx->gate, m16 * F));
     RCK(dalloc(ctx, &ctx->logits, m * V));
     RCK(dalloc(ctx, &ctx->tok_loss, m));
     RCK(dalloc(ctx, &ctx->mean, m));
@@ -238,7 +240,7 @@ int enqueue_body(rh_ctx* ctx, int B, int S, bool to_cache) {
         f16* kc = to_cache ? ctx->kcache + (size_t)l * ctx->kv_layer : ctx->kbuf;
         f16* vc = to_cache ? ctx->vcache + (size_t)l * ctx->kv_layer : ctx->vbuf;
         const int kvctx = to_cache ? ctx->max_ctx : S;
-        LCK(rh::launch_rmsnorm(ctx->x, W.g1, ctx->xn, M, D, c.rms_eps, st));
+        LCK(rh::launch_rmsnorm(ctx->x, W.g1, ctx->xn, M, D, c.rms_eps, st, true));
         rh::GemmArgs g{};
         g.W = W.wqkv; g.X = ctx->xn; g.M = M; g.N = 3 * D; g.K = D;
         g.q = ctx->q; g.kc = kc; g.vc = vc; g.rope = ctx->rope;
@@ -253,7 +255,7 @@ int enqueue_body(rh_ctx* ctx, int B, int S, bool to_cache) {
         g.out_f32 = ctx->x; g.ldo = D; g.alpha = alpha;
         set_sk(ctx, g);
         RCK(timed(ctx, RH_K_GEMM_WO, [&] { return rh::launch_gemm(rh::EPI_RESID, g, st); }));
-        LCK(rh::launch_rmsnorm(ctx->x, W.g2, ctx->xn, M, D, c.rms_eps, st));
+        LCK(rh::launch_rmsnorm(ctx->x, W.g2, ctx->xn, M, D, c.rms_eps, st, true));
         g = rh::GemmArgs{};
         g.W = W.w13; g.X = ctx->xn; g.M = M; g.N = 2 * F; g.K = D;
         g.out_f16 = ctx->gate; g.ldo = F;
@@ -272,7 +274,7 @@ int enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss) {
     const rh_config& c = ctx->cfg;
     const int M = B * S, D = c.dim;
     hipStream_t st = ctx->stream;
-    LCK(rh::launch_rmsnorm(ctx->x, ctx->gfinal, ctx->xn, M, D, c.rms_eps, st));
+    LCK(rh::launch_rmsnorm(ctx->x, ctx->gfinal, ctx->xn, M, D, c.rms_eps, st, true));
     rh::GemmArgs g{};
     g.W = ctx->embed; g.X = ctx->xn; g.M = M; g.N = c.vocab; g.K = D;
     g.out_f32 = ctx->logits; g.ldo = c.vocab; g.softcap = c.softcap;
