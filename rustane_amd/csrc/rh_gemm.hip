@@ -359,7 +359,7 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         // and long K (W2) use stream-K instead, when every block gets at least
         // two 32-wide k-iterations.
         struct Cand { int cfg, bn, bm; float rate; };
-        constexpr Cand dp[] = {{GCFG_D8_256x256, 256, 256, 4.4f}, {GCFG_D8_192x256, 192, 256, 3.9f},
+        constexpr Cand dp[] = {{GCFG_D8_256x256, 256, 256, 4.4f}, {GCFG_D4_192x256, 192, 256, 4.18f},
                                {GCFG_D8_256x128, 256, 128, 4.0f}, {GCFG_D4_192x128, 192, 128, 3.95f},
                                {GCFG_D4_128x128, 128, 128, 3.7f}};
         const long long KT = a.K / 32;
@@ -394,6 +394,8 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         case GCFG_D4_192x128_SK: return launch_tile<DTile<2, 2, 3, 2>, EPI>(a, true, st);
         case GCFG_D8_192x256: return launch_tile<DTile<2, 4, 3, 2>, EPI>(a, false, st);
         case GCFG_D8_192x256_SK: return launch_tile<DTile<2, 4, 3, 2>, EPI>(a, true, st);
+        case GCFG_D4_192x256: return launch_tile<DTile<2, 2, 3, 4>, EPI>(a, false, st);
+        case GCFG_D4_192x256_SK: return launch_tile<DTile<2, 2, 3, 4>, EPI>(a, true, st);
     }
     return hipErrorInvalidValue;
 }

@@ -49,6 +49,8 @@ enum GemmCfg {
     GCFG_D4_192x128_SK = 17,
     GCFG_D8_192x256 = 18,    // 8 waves (96x64 each)
     GCFG_D8_192x256_SK = 19,
+    GCFG_D4_192x256 = 20,    // 4 waves (96x128 each, accumulators in AGPRs)
+    GCFG_D4_192x256_SK = 21,
 };
 // Floats of stream-K workspace any prefill GEMM needs.
 size_t gemm_sk_part_floats();

@@ -34,7 +34,7 @@ __global__ void embed_kernel(const uint32_t* tok, const f16* E, float* x, int D,
 
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const float* gamma, f16* out,
                                                       int D, float eps, int stride_rows,
-                                                      int offset_rows, int frag) {
+                                                      int offset_rows) {
     __shared__ float red[4];
     const int row = blockIdx.x;
     const float* xr = x + ((size_t)row * stride_rows + offset_rows) * D;
@@ -49,9 +49,34 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const floa
     for (int i = threadIdx.x * 4; i < D; i += 1024) {
         const f32x4 v = *(const f32x4*)(xr + i);
         const f32x4 gm = *(const f32x4*)(gamma + i);
-        f16* dst = frag ? out + frag_off(row, i, D) : o + i;
-        *(f16x4*)dst = f16x4{(f16)(v[0] * r * gm[0]), (f16)(v[1] * r * gm[1]),
-                             (f16)(v[2] * r * gm[2]), (f16)(v[3] * r * gm[3])};
+        *(f16x4*)(o + i) = f16x4{(f16)(v[0] * r * gm[0]), (f16)(v[1] * r * gm[1]),
+                                 (f16)(v[2] * r * gm[2]), (f16)(v[3] * r * gm[3])};
+    }
+}
+
+// RMSNorm into fragment order: one block per row, the row kernel's sum, then
+// each thread writes 8 consecutive k (one 16-byte lane slot of a fragment).
+__global__ __launch_bounds__(256) void rmsnorm_frag_kernel(const float* x, const float* gamma, f16* out,
+                                                           int D, float eps) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    const float* xr = x + (size_t)row * D;
+    float ss = 0.f;
+    for (int i = threadIdx.x * 4; i < D; i += 1024) {
+        const f32x4 v = *(const f32x4*)(xr + i);
+        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    }
+    ss = block_sum_256(ss, red);
+    const float r = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
+    for (int i = threadIdx.x * 8; i < D; i += 2048) {
+        const f32x4 v0 = *(const f32x4*)(xr + i), v1 = *(const f32x4*)(xr + i + 4);
+        const f32x4 g0 = *(const f32x4*)(gamma + i), g1 = *(const f32x4*)(gamma + i + 4);
+        f16x8 o;
+        o[0] = (f16)(v0[0] * r * g0[0]); o[1] = (f16)(v0[1] * r * g0[1]);
+        o[2] = (f16)(v0[2] * r * g0[2]); o[3] = (f16)(v0[3] * r * g0[3]);
+        o[4] = (f16)(v1[0] * r * g1[0]); o[5] = (f16)(v1[1] * r * g1[1]);
+        o[6] = (f16)(v1[2] * r * g1[2]); o[7] = (f16)(v1[3] * r * g1[3]);
+        *(f16x8*)(out + frag_off(row, i, D)) = o;
     }
 }
 
@@ -210,13 +235,16 @@ hipError_t launch_embed(const uint32_t* tok, const f16* E, float* x, int rows, i
 }
 hipError_t launch_rmsnorm(const float* x, const float* gamma, f16* out, int rows, int D, float eps,
                           hipStream_t st, bool frag) {
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps, 1, 0, frag ? 1 : 0);
+    if (frag)
+        hipLaunchKernelGGL(rmsnorm_frag_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps);
+    else
+        hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps, 1, 0);
     return hipGetLastError();
 }
 hipError_t launch_rmsnorm_strided(const float* x, const float* gamma, f16* out, int rows, int D,
                                   float eps, int stride_rows, int offset_rows, hipStream_t st) {
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps,
-                       stride_rows, offset_rows, 0);
+                       stride_rows, offset_rows);
     return hipGetLastError();
 }
 hipError_t launch_cross_entropy(const float* logits, const uint32_t* targets, float* loss, int rows,
