@@ -38,6 +38,19 @@ def small_cfg(dim=256, hidden=512, heads=4, hd=64, nlayers=2, vocab=1024, seq=64
     return ModelConfig(dim, hidden, heads, heads, hd, seq, nlayers, vocab)
 
 
+def random_gammas(w: ModelWeights, seed: int):
+    """Replaces every RMSNorm gamma (both per layer and the final one) with a
+    distinct U(0.5, 1.5) vector, so a kernel that drops a gamma or applies the
+    wrong one fails parity."""
+    rng = np.random.default_rng(seed)
+    D = w.gamma_final.shape[0]
+    for lw in w.layers:
+        lw.gamma1 = rng.uniform(0.5, 1.5, D).astype(np.float32)
+        lw.gamma2 = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    w.gamma_final = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    return w
+
+
 def cosine(a, b):
     a = a.ravel().astype(np.float64)
     b = b.ravel().astype(np.float64)

@@ -13,7 +13,7 @@ import pytest
 from rustane_amd import hip_bridge as hb
 from rustane_amd.engine import ModelConfig, ModelWeights
 
-from helpers import LOGIT_ATOL, oracle_cfg, oracle_weights, small_cfg, tokens_uniform
+from helpers import LOGIT_ATOL, oracle_cfg, oracle_weights, random_gammas, small_cfg, tokens_uniform
 
 pytestmark = pytest.mark.gpu
 
@@ -116,6 +116,24 @@ def test_decode_batch16_long_context_hd128(orc):
         _, last = c.prefill(tok[:, :300], want_logits=True)
         assert np.abs(last - lg[:, 299]).max() <= LOGIT_ATOL
         for p in range(300, 306):
+            _, dl = c.decode_step(tok[:, p], want_logits=True)
+            err = float(np.abs(dl - lg[:, p]).max())
+            assert err <= LOGIT_ATOL, (p, err)
+
+
+@pytest.mark.parametrize("dim,batch", [(256, 2), (2048, 16)])
+def test_decode_nonunit_gammas(orc, dim, batch):
+    """Random gammas through the decode norms: at dim 256 the RMSNorm is fused
+    into the GEMV (the normalised rows fit in LDS), at dim 2048 x 16 rows it
+    runs as its own kernel."""
+    cfg = small_cfg(dim=dim, hidden=1024, heads=dim // 128, hd=128, nlayers=2, vocab=1024, seq=40)
+    w = random_gammas(ModelWeights.normal(cfg, seed=53), seed=54)
+    tok, tgt = tokens_uniform(55, cfg.vocab, batch, cfg.seq)
+    lg, _, _ = orc.forward(oracle_cfg(orc, cfg), oracle_weights(orc, w), tok, tgt)
+    with _ctx(cfg, w, batch, 64) as c:
+        _, last = c.prefill(tok[:, :32], want_logits=True)
+        assert np.abs(last - lg[:, 31]).max() <= LOGIT_ATOL
+        for p in range(32, 40):
             _, dl = c.decode_step(tok[:, p], want_logits=True)
             err = float(np.abs(dl - lg[:, p]).max())
             assert err <= LOGIT_ATOL, (p, err)

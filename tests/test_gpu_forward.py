@@ -9,8 +9,8 @@ import pytest
 from rustane_amd import hip_bridge as hb
 from rustane_amd.engine import ModelConfig, ModelWeights, tiny_config
 
-from helpers import (LOGIT_ATOL, LOSS_RTOL, cosine, oracle_cfg, oracle_weights, reference_tokens,
-                     small_cfg, tokens_uniform)
+from helpers import (LOGIT_ATOL, LOSS_RTOL, cosine, oracle_cfg, oracle_weights, random_gammas,
+                     reference_tokens, small_cfg, tokens_uniform)
 
 pytestmark = pytest.mark.gpu
 
@@ -68,6 +68,14 @@ def test_forward_stream_k_shapes(orc):
     cfg = ModelConfig(1024, 8192, 8, 8, 128, 128, 1, 2048)
     w = ModelWeights.normal(cfg, seed=17)
     tok, tgt = tokens_uniform(18, cfg.vocab, 2, cfg.seq)
+    _compare(orc, cfg, w, tok, tgt)
+
+
+def test_forward_nonunit_gammas(orc):
+    """Distinct random gammas in both per-layer norms and the final norm."""
+    cfg = small_cfg(dim=512, hidden=1024, heads=4, hd=128, nlayers=2, vocab=2048, seq=96)
+    w = random_gammas(ModelWeights.normal(cfg, seed=19), seed=20)
+    tok, tgt = tokens_uniform(21, cfg.vocab, 2, cfg.seq)
     _compare(orc, cfg, w, tok, tgt)
 
 
