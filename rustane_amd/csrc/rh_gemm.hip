@@ -145,19 +145,59 @@ struct DTile {
         __builtin_amdgcn_s_barrier();
         issue(kb + min(NS - 1, n - 1), buf(NS - 1));
         readf(buf(0), f0);
+        // A full step, issued interleaved and pinned in that order: MFMA m,
+        // then LDS read m, then DMA m.  With one or two waves per SIMD a
+        // wave's in-order issue blocks whenever the vector-memory queue is
+        // full; spreading the reads and DMAs between MFMAs keeps the matrix
+        // pipe fed through those stalls (issued in bulk they idle it).
+        auto step_il = [&](int t, Frags& cur, Frags& nxt, f16* refill, const f16* next) {
+            __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((NS - 2) * LPS));
+            __builtin_amdgcn_s_barrier();
+            const int kt = kb + min(t + NS, n - 1);
+            constexpr int NM = 2 * TN * TM, NR = 2 * (TN + TM);
+            constexpr int NG = NM > NR ? (NM > LPS ? NM : LPS) : (NR > LPS ? NR : LPS);
+#pragma unroll
+            for (int m = 0; m < NG; ++m) {
+                if (m < NM) {
+                    const int ks = m / (TN * TM), i = (m / TM) % TN, j = m % TM;
+                    acc.v[i][j] = mfma32(cur.a[ks][i], cur.b[ks][j], acc.v[i][j]);
+                }
+                if (m < NR) {
+                    const int rks = m / (TN + TM), r = m % (TN + TM);
+                    if (r < TN) nxt.a[rks][r] = *(const f16x8*)&next[ao[r] + 256 * rks];
+                    else nxt.b[rks][r - TN] = *(const f16x8*)&next[bo[r - TN] + 256 * rks];
+                }
+                if (m < LPS)
+                    __builtin_amdgcn_global_load_lds((const void*)(gp[m] + (size_t)kt * gstep[m]),
+                                                     (__attribute__((address_space(3))) void*)(refill + loff[m]),
+                                                     16, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        // Tail step (past the last stage: a harmless read of a stale buffer,
+        // MFMAs skipped).
         auto step = [&](int t, Frags& cur, Frags& nxt, f16* refill, const f16* next) {
             __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((NS - 2) * LPS));
             __builtin_amdgcn_s_barrier();
             issue(kb + min(t + NS, n - 1), refill);
-            readf(next, nxt);  // past the last stage: a harmless read of a stale buffer
+            readf(next, nxt);
             if (t < n) mfmas(cur);
         };
-        // single exit: every pass runs NS steps (the vmcnt bookkeeping stays uniform)
-        for (int t = 0; t < n; t += NS) {
-            step(t, f0, f1, buf(0), buf(1));
-            step(t + 1, f1, f0, buf(1), buf(2));
-            step(t + 2, f0, f1, buf(2), buf(3));
-            step(t + 3, f1, f0, buf(3), buf(0));
+        // Whole groups of NS steps run interleaved; the remainder runs one
+        // more group of predicated steps.  Every step issues LPS DMAs, so the
+        // vmcnt bookkeeping stays uniform.
+        int t0 = 0;
+        for (; t0 + NS <= n; t0 += NS) {
+            step_il(t0, f0, f1, buf(0), buf(1));
+            step_il(t0 + 1, f1, f0, buf(1), buf(2));
+            step_il(t0 + 2, f0, f1, buf(2), buf(3));
+            step_il(t0 + 3, f1, f0, buf(3), buf(0));
+        }
+        if (t0 < n) {
+            step(t0, f0, f1, buf(0), buf(1));
+            step(t0 + 1, f1, f0, buf(1), buf(2));
+            step(t0 + 2, f0, f1, buf(2), buf(3));
+            step(t0 + 3, f1, f0, buf(3), buf(0));
         }
         // the trailing (unused) stage loads must land before the LDS is reused
         __builtin_amdgcn_s_waitcnt(vm_wait(0));
