@@ -42,7 +42,7 @@ extern "C" {
 
 /* ModelConfig (crates/engine/src/model.rs:5-17).  MHA only: kv_heads must
  * equal heads (the reference reshapes K/V with `heads`, sdpa_fwd.rs:162-181).
- * head_dim is 64 or 128; dim % 128 == 0; hidden % 128 == 0; vocab % 4 == 0. */
+ * head_dim is 64 or 128; dim % 128 == 0, dim <= 8192; hidden % 128 == 0; vocab % 4 == 0. */
 typedef struct rh_config {
     int32_t dim, hidden, heads, kv_heads, head_dim, seq, nlayers, vocab;
     float rms_eps;   /* 1e-5  (cpu/rmsnorm.rs:10)                */

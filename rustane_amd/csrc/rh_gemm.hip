@@ -26,6 +26,8 @@
 // (deterministic) and runs the epilogue.  Blocks never communicate inside a
 // kernel: on this multi-XCD part the per-XCD L2s are not coherent, and a
 // device-scope fence costs an L2 writeback + invalidate.
+#include <algorithm>
+
 #include "rh_device.h"
 #include "rh_kernels.h"
 
@@ -281,17 +283,35 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, int nw, int mw,
     }
 }
 
-template <class Tl, int EPI, bool SK>
+// MODE: MODE_DP one block per tile; MODE_SK stream-K over P blocks (T =
+// tiles x k-iterations); MODE_SPLIT P even k-splits per tile, each storing its
+// fp32 partial [M][N] at sk_part + split * M * N.
+enum { MODE_DP = 0, MODE_SK = 1, MODE_SPLIT = 2 };
+
+template <class Tl, int EPI, int MODE>
 __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long long T) {
     __shared__ __attribute__((aligned(16))) typename Tl::Smem sm;
     const int nbN = (a.N + Tl::BN - 1) / Tl::BN, nbM = (a.M + Tl::BM - 1) / Tl::BM;
     const int KT = a.K / Tl::KI;
     typename Tl::Acc acc;
-    if constexpr (!SK) {
+    if constexpr (MODE == MODE_DP) {
         const int t = xcd_remap(blockIdx.x, nbN * nbM);
         const int nb = t / nbM, mb = t - nb * nbM;
         Tl::run(a, nb * Tl::BN, mb * Tl::BM, 0, KT, acc, sm);
         epilogue<Tl::FTN, Tl::FTM, EPI>(a, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
+    } else if constexpr (MODE == MODE_SPLIT) {
+        // the splits of one tile and the tiles of one weight panel land on the
+        // same XCD
+        const int v = xcd_remap(blockIdx.x, nbN * nbM * P);
+        const int tile = v / P, sp = v - tile * P;
+        const int nb = tile / nbM, mb = tile - nb * nbM;
+        const int kb = (int)((long long)sp * KT / P), ke = (int)((long long)(sp + 1) * KT / P);
+        Tl::run(a, nb * Tl::BN, mb * Tl::BM, kb, ke, acc, sm);
+        GemmArgs b = a;
+        b.out_f32 = a.sk_part + (size_t)sp * a.M * a.N;
+        b.ldo = a.N;
+        b.softcap = 0.f;
+        epilogue<Tl::FTN, Tl::FTM, EPI_F32>(b, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
     } else {
         constexpr int TN = Tl::FTN, TM = Tl::FTM, NT = Tl::NT;
         constexpr int NV = TN * TM * 4;  // f32x4 per thread per partial tile
@@ -377,13 +397,23 @@ hipError_t launch_tile(const GemmArgs& a, bool sk, hipStream_t st) {
     const long long T = (long long)tiles * (a.K / Tl::KI);
     if (sk) {
         if (!a.sk_part || (size_t)SK_P * 2 * Tl::BN * Tl::BM > a.sk_part_floats) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((gemm_kernel<Tl, EPI, true>), dim3(SK_P), dim3(Tl::NT), 0, st, a, SK_P, T);
+        hipLaunchKernelGGL((gemm_kernel<Tl, EPI, MODE_SK>), dim3(SK_P), dim3(Tl::NT), 0, st, a, SK_P, T);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL((gemm_fixup_kernel<Tl, EPI>), dim3(tiles, Tl::FTN), dim3(Tl::NT), 0, st, a, SK_P, T);
     } else {
-        hipLaunchKernelGGL((gemm_kernel<Tl, EPI, false>), dim3(tiles), dim3(Tl::NT), 0, st, a, 1, T);
+        hipLaunchKernelGGL((gemm_kernel<Tl, EPI, MODE_DP>), dim3(tiles), dim3(Tl::NT), 0, st, a, 1, T);
     }
+    return hipGetLastError();
+}
+
+// S-way split-K of a residual GEMM: partials only (the row kernel reduces).
+template <class Tl>
+hipError_t launch_split(const GemmArgs& a, int S, hipStream_t st) {
+    const int tiles = ((a.N + Tl::BN - 1) / Tl::BN) * ((a.M + Tl::BM - 1) / Tl::BM);
+    if (S < 1 || S > a.K / Tl::KI || !a.sk_part || (size_t)S * a.M * a.N > a.sk_part_floats)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemm_kernel<Tl, EPI_F32, MODE_SPLIT>), dim3(tiles * S), dim3(Tl::NT), 0, st, a, S, 0LL);
     return hipGetLastError();
 }
 
@@ -443,6 +473,30 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
 }  // namespace
 
 size_t gemm_sk_part_floats() { return (size_t)SK_P * 2 * 256 * 256; }
+
+hipError_t launch_gemm_resid_norm(const GemmArgs& a, const float* gamma, float eps, f16* xn, hipStream_t st) {
+    if (a.K % 128 != 0 || a.N % 8 != 0 || a.N > 8192 || a.M <= 0 || a.ldo != a.N) return hipErrorInvalidValue;
+    // Split K when the output has too few tiles to fill the CUs: S splits per
+    // tile, at most 8 and at least 8 k-iterations each, within the workspace.
+    const bool wide_k = a.K >= 8192;
+    const int bn = wide_k ? 256 : 128, bm = 128;
+    const int tiles = ((a.N + bn - 1) / bn) * ((a.M + bm - 1) / bm);
+    int S = 1;
+    if (a.force_cfg == GCFG_AUTO && a.sk_part && tiles < 160) {
+        S = std::min(std::min(SK_P / tiles, 8), a.K / 32 / 8);
+        while (S > 1 && (size_t)S * a.M * a.N > a.sk_part_floats) --S;
+    }
+    if (S >= 2) {
+        const hipError_t e = wide_k ? launch_split<DTile<2, 2, 4, 2>>(a, S, st)
+                                    : launch_split<DTile<2, 2, 2, 2>>(a, S, st);
+        if (e != hipSuccess) return e;
+        return launch_resid_norm(a.out_f32, a.sk_part, S, (size_t)a.M * a.N, a.alpha, gamma, eps, xn, a.M,
+                                 a.N, st);
+    }
+    const hipError_t e = launch_epi<EPI_RESID>(a, st);
+    if (e != hipSuccess || !gamma) return e;
+    return launch_rmsnorm(a.out_f32, gamma, xn, a.M, a.N, eps, st, true);
+}
 
 hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
     if (a.K % 128 != 0 || a.N % 4 != 0 || a.M <= 0) return hipErrorInvalidValue;

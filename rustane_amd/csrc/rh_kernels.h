@@ -55,6 +55,16 @@ enum GemmCfg {
 // Floats of stream-K workspace any prefill GEMM needs.
 size_t gemm_sk_part_floats();
 hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st);
+// Residual projection followed by the next RMSNorm:
+//   x [M, N] += alpha * (X W^T)            (a.out_f32 = x, a.ldo = N)
+//   xn = rmsnorm(x) * gamma, fp16 in fragment order (skipped when gamma is null).
+// With few output tiles (narrow N, small M) K is split: every split writes an
+// fp32 partial into a.sk_part and one row kernel sums the partials in split
+// order (deterministic), adds the residual and normalises -- no stream-K
+// fix-up kernel and no separate norm pass.  Otherwise the GEMM's own residual
+// epilogue runs, then the norm.  Needs N % 8 == 0 and N <= 8192.
+hipError_t launch_gemm_resid_norm(const GemmArgs& a, const float* gamma, float eps, f16* xn,
+                                  hipStream_t st);
 
 // ---------------- attention ----------------
 // Causal prefill attention: q [B][H][S][hd], k/v [B][H][ctx][hd] (positions
@@ -117,6 +127,11 @@ hipError_t launch_rmsnorm(const float* x, const float* gamma, f16* out, int rows
 // rmsnorm of rows x[(r*stride + offset)] -> out[r]  (last-position gather)
 hipError_t launch_rmsnorm_strided(const float* x, const float* gamma, f16* out, int rows, int D,
                                   float eps, int stride_rows, int offset_rows, hipStream_t st);
+// x [rows, D] += alpha * sum_s part[s*split_stride + row*D ...] (s = 0..S-1 in
+// order), then out = rmsnorm(x) * gamma in fragment order when gamma is set.
+// D % 8 == 0, D <= 8192.
+hipError_t launch_resid_norm(float* x, const float* part, int S, size_t split_stride, float alpha,
+                             const float* gamma, float eps, f16* out, int rows, int D, hipStream_t st);
 hipError_t launch_cross_entropy(const float* logits, const uint32_t* targets, float* loss,
                                 int rows, int V, int* err, hipStream_t st);
 hipError_t launch_mean_rows(const float* loss, float* mean, int B, int S, hipStream_t st);

@@ -80,6 +80,61 @@ __global__ __launch_bounds__(256) void rmsnorm_frag_kernel(const float* x, const
     }
 }
 
+// Split-K reduction + residual + RMSNorm: one block per row; each thread
+// owns 8 consecutive columns per 2048-column pass (up to 4 passes), keeps the
+// updated values in registers between the sum of squares and the normalised
+// 16-byte fragment-order writes.
+__global__ __launch_bounds__(256) void resid_norm_kernel(float* x, const float* part, int S,
+                                                         size_t split_stride, float alpha,
+                                                         const float* gamma, float eps, f16* out,
+                                                         int D) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    float* xr = x + (size_t)row * D;
+    const float* pr = part + (size_t)row * D;
+    f32x4 v[4][2];
+    float ss = 0.f;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int i = threadIdx.x * 8 + it * 2048;
+        if (i < D) {
+            f32x4 a0 = {}, a1 = {};
+            for (int sp = 0; sp < S; ++sp) {
+                a0 += *(const f32x4*)(pr + sp * split_stride + i);
+                a1 += *(const f32x4*)(pr + sp * split_stride + i + 4);
+            }
+            f32x4 x0 = *(const f32x4*)(xr + i), x1 = *(const f32x4*)(xr + i + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x0[e] = a0[e] * alpha + x0[e];
+                x1[e] = a1[e] * alpha + x1[e];
+                ss += x0[e] * x0[e] + x1[e] * x1[e];
+            }
+            *(f32x4*)(xr + i) = x0;
+            *(f32x4*)(xr + i + 4) = x1;
+            v[it][0] = x0;
+            v[it][1] = x1;
+        }
+    }
+    if (!gamma) return;  // uniform per launch
+    ss = block_sum_256(ss, red);
+    const float r = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int i = threadIdx.x * 8 + it * 2048;
+        if (i < D) {
+            const f32x4 g0 = *(const f32x4*)(gamma + i), g1 = *(const f32x4*)(gamma + i + 4);
+            f16x8 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                o[e] = (f16)(v[it][0][e] * r * g0[e]);
+                o[e + 4] = (f16)(v[it][1][e] * r * g1[e]);
+            }
+            *(f16x8*)(out + frag_off(row, i, D)) = o;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void ce_kernel(const float* logits, const uint32_t* targets,
                                                  float* loss, int V, int* err) {
     __shared__ float sm[4], ss[4];
@@ -245,6 +300,13 @@ hipError_t launch_rmsnorm_strided(const float* x, const float* gamma, f16* out, 
                                   float eps, int stride_rows, int offset_rows, hipStream_t st) {
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps,
                        stride_rows, offset_rows);
+    return hipGetLastError();
+}
+hipError_t launch_resid_norm(float* x, const float* part, int S, size_t split_stride, float alpha,
+                             const float* gamma, float eps, f16* out, int rows, int D, hipStream_t st) {
+    if (D % 8 != 0 || D > 8192 || S < 0 || (S > 0 && !part)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(resid_norm_kernel, dim3(rows), dim3(256), 0, st, x, part, S, split_stride, alpha,
+                       gamma, eps, out, D);
     return hipGetLastError();
 }
 hipError_t launch_cross_entropy(const float* logits, const uint32_t* targets, float* loss, int rows,

@@ -229,18 +229,22 @@ void set_sk(const rh_ctx* ctx, rh::GemmArgs& g) {
 // kv_k/kv_v: per-layer K/V destination base and ctx stride.  For a plain
 // forward they are the scratch buffers (ctx = S); for a prefill they are the
 // cache layers (ctx = max_ctx).
-int enqueue_body(rh_ctx* ctx, int B, int S, bool to_cache) {
+// Every residual GEMM (Wo, W2) also produces the next RMSNorm's output in xn:
+// Wo the layer's second norm, W2 the next layer's first norm -- or, after the
+// last layer, the final norm when final_norm is set (the forward's logits).
+int enqueue_body(rh_ctx* ctx, int B, int S, bool to_cache, bool final_norm) {
     const rh_config& c = ctx->cfg;
     const int M = B * S, D = c.dim, F = c.hidden;
     const float alpha = 1.0f / std::sqrt(2.0f * (float)c.nlayers);
     hipStream_t st = ctx->stream;
     LCK(rh::launch_embed(ctx->d_tok, ctx->embed, ctx->x, M, D, c.vocab, ctx->d_err, st));
+    LCK(rh::launch_rmsnorm(ctx->x, ctx->L[0].g1, ctx->xn, M, D, c.rms_eps, st, true));
     for (int l = 0; l < c.nlayers; ++l) {
         const Layer& W = ctx->L[l];
         f16* kc = to_cache ? ctx->kcache + (size_t)l * ctx->kv_layer : ctx->kbuf;
         f16* vc = to_cache ? ctx->vcache + (size_t)l * ctx->kv_layer : ctx->vbuf;
         const int kvctx = to_cache ? ctx->max_ctx : S;
-        LCK(rh::launch_rmsnorm(ctx->x, W.g1, ctx->xn, M, D, c.rms_eps, st, true));
+        const float* next_gamma = l + 1 < c.nlayers ? ctx->L[l + 1].g1 : (final_norm ? ctx->gfinal : nullptr);
         rh::GemmArgs g{};
         g.W = W.wqkv; g.X = ctx->xn; g.M = M; g.N = 3 * D; g.K = D;
         g.q = ctx->q; g.kc = kc; g.vc = vc; g.rope = ctx->rope;
@@ -254,8 +258,7 @@ int enqueue_body(rh_ctx* ctx, int B, int S, bool to_cache) {
         g.W = W.wo; g.X = ctx->attn; g.M = M; g.N = D; g.K = D;
         g.out_f32 = ctx->x; g.ldo = D; g.alpha = alpha;
         set_sk(ctx, g);
-        RCK(timed(ctx, RH_K_GEMM_WO, [&] { return rh::launch_gemm(rh::EPI_RESID, g, st); }));
-        LCK(rh::launch_rmsnorm(ctx->x, W.g2, ctx->xn, M, D, c.rms_eps, st, true));
+        RCK(timed(ctx, RH_K_GEMM_WO, [&] { return rh::launch_gemm_resid_norm(g, W.g2, c.rms_eps, ctx->xn, st); }));
         g = rh::GemmArgs{};
         g.W = W.w13; g.X = ctx->xn; g.M = M; g.N = 2 * F; g.K = D;
         g.out_f16 = ctx->gate; g.ldo = F;
@@ -265,16 +268,18 @@ int enqueue_body(rh_ctx* ctx, int B, int S, bool to_cache) {
         g.W = W.w2; g.X = ctx->gate; g.M = M; g.N = D; g.K = F;
         g.out_f32 = ctx->x; g.ldo = D; g.alpha = alpha;
         set_sk(ctx, g);
-        RCK(timed(ctx, RH_K_GEMM_W2, [&] { return rh::launch_gemm(rh::EPI_RESID, g, st); }));
+        RCK(timed(ctx, RH_K_GEMM_W2,
+                  [&] { return rh::launch_gemm_resid_norm(g, next_gamma, c.rms_eps, ctx->xn, st); }));
     }
     return RH_OK;
 }
 
+// Logits + loss from xn, which enqueue_body(final_norm = true) left holding
+// the final RMSNorm of every row.
 int enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss) {
     const rh_config& c = ctx->cfg;
     const int M = B * S, D = c.dim;
     hipStream_t st = ctx->stream;
-    LCK(rh::launch_rmsnorm(ctx->x, ctx->gfinal, ctx->xn, M, D, c.rms_eps, st, true));
     rh::GemmArgs g{};
     g.W = ctx->embed; g.X = ctx->xn; g.M = M; g.N = c.vocab; g.K = D;
     g.out_f32 = ctx->logits; g.ldo = c.vocab; g.softcap = c.softcap;
@@ -455,7 +460,7 @@ int rh_create(const rh_config* cfg, int device, int max_batch, int max_ctx, rh_c
     if (!cfg || !out) return RH_EINVAL;
     *out = nullptr;
     const rh_config& c = *cfg;
-    if (c.dim <= 0 || c.dim % 128 || c.hidden <= 0 || c.hidden % 128 || c.heads <= 0 ||
+    if (c.dim <= 0 || c.dim % 128 || c.dim > 8192 || c.hidden <= 0 || c.hidden % 128 || c.heads <= 0 ||
         c.kv_heads != c.heads || !(c.head_dim == 64 || c.head_dim == 128) ||
         c.heads * c.head_dim != c.dim || c.nlayers <= 0 || c.vocab <= 0 || c.vocab % 4 ||
         c.seq <= 0 || max_batch <= 0 || max_ctx < 0 || !(c.rms_eps > 0.f) || !(c.rope_base > 0.f) ||
@@ -615,7 +620,7 @@ int rh_forward_dev(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets,
     HCK(hipMemcpyAsync(ctx->d_tok, tokens, (size_t)M * sizeof(uint32_t), hipMemcpyDeviceToDevice, st));
     if (targets)
         HCK(hipMemcpyAsync(ctx->d_tgt, targets, (size_t)M * sizeof(uint32_t), hipMemcpyDeviceToDevice, st));
-    RCK(enqueue_body(ctx, batch, seq, false));
+    RCK(enqueue_body(ctx, batch, seq, false, true));
     RCK(enqueue_tail(ctx, batch, seq, targets != nullptr));
     const size_t V = V_(ctx);
     if (logits_out)
@@ -643,7 +648,7 @@ int rh_forward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int
     hipStream_t st = ctx->stream;
     HCK(hipMemcpyAsync(ctx->d_tok, tokens, M * sizeof(uint32_t), hipMemcpyHostToDevice, st));
     if (targets) HCK(hipMemcpyAsync(ctx->d_tgt, targets, M * sizeof(uint32_t), hipMemcpyHostToDevice, st));
-    RCK(enqueue_body(ctx, batch, seq, false));
+    RCK(enqueue_body(ctx, batch, seq, false, true));
     RCK(enqueue_tail(ctx, batch, seq, targets != nullptr));
     const size_t V = V_(ctx);
     if (logits_out) HCK(hipMemcpyAsync(logits_out, ctx->logits, M * V * sizeof(float), hipMemcpyDeviceToHost, st));
@@ -666,7 +671,7 @@ int rh_prefill(rh_ctx* ctx, const uint32_t* tokens, int batch, int len, uint32_t
     RCK(ensure_workspace(ctx, (int)M));
     hipStream_t st = ctx->stream;
     HCK(hipMemcpyAsync(ctx->d_tok, tokens, M * sizeof(uint32_t), hipMemcpyHostToDevice, st));
-    RCK(enqueue_body(ctx, batch, len, true));
+    RCK(enqueue_body(ctx, batch, len, true, false));
     const rh_config& c = ctx->cfg;
     LCK(rh::launch_rmsnorm_strided(ctx->x, ctx->gfinal, ctx->dxn, batch, c.dim, c.rms_eps, len, len - 1, st));
     rh::GemvArgs g{};
