@@ -28,9 +28,16 @@ CFLAGS = [
 ]
 
 
+# Per-file extras.  Attention rescales its MFMA accumulators with VALU ops
+# every key block; with accumulators in AGPRs each rescale costs two copies
+# per register, so its MFMAs take the VGPR form (the GEMMs keep AGPRs: their
+# accumulators exceed the 256 architectural VGPRs).
+FILE_FLAGS = {"rh_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *CFLAGS, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(src, []), "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:

@@ -25,7 +25,7 @@ namespace {
 
 constexpr float LOG2E = 1.4426950408889634f;
 
-template <int HD>
+template <int HD, int PF>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict__ Q,
                                                            const f16* __restrict__ Kc,
                                                            const f16* __restrict__ Vc,
@@ -63,67 +63,100 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
 
     const int kend = min(S, q0 + 64);
     const int nkb = (kend + KB - 1) / KB;
-    // K/V of the next key block are loaded into registers while the current
-    // one is computed, then stored to LDS at the top of the next iteration.
+    // K/V of key block kb + PF are loaded into register set kb % PF while
+    // block kb is computed; set kb % PF goes to LDS at the top of iteration
+    // kb.  The LDS-only barriers leave those loads in flight, so each has PF
+    // iterations of compute to land.
     constexpr int KL = KB * HD / 8 / 256;           // 16-byte K loads per thread
     constexpr int VL = (KB / 2) * (HD / 8) / 256;   // key pairs per thread
-    f16x8 rk[KL], rva[VL], rvb[VL];
-    auto gload = [&](int k0) {
-        const f16x8 z = {};
+    f16x8 rk[PF][KL], rva[PF][VL], rvb[PF][VL];
+    // Keys past the sequence read the last row instead (branch-free): their
+    // scores are masked to -inf, so they add p = 0 times a finite V row.
+    auto gload = [&](int k0, int set) {
 #pragma unroll
         for (int p = 0; p < KL; ++p) {
             const int c = tid + 256 * p, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
-            const int key = k0 + row;
-            rk[p] = key < S ? *(const f16x8*)(Kb + (size_t)key * HD + col) : z;
+            const int key = min(k0 + row, S - 1);
+            rk[set][p] = *(const f16x8*)(Kb + (size_t)key * HD + col);
         }
 #pragma unroll
         for (int p = 0; p < VL; ++p) {
             const int u = tid + 256 * p, kp = u & 31, col = (u >> 5) * 8;
-            const int key0 = k0 + 2 * kp;
-            rva[p] = key0 < S ? *(const f16x8*)(Vb + (size_t)key0 * HD + col) : z;
-            rvb[p] = key0 + 1 < S ? *(const f16x8*)(Vb + (size_t)(key0 + 1) * HD + col) : z;
+            const int key0 = min(k0 + 2 * kp, S - 1), key1 = min(k0 + 2 * kp + 1, S - 1);
+            rva[set][p] = *(const f16x8*)(Vb + (size_t)key0 * HD + col);
+            rvb[set][p] = *(const f16x8*)(Vb + (size_t)key1 * HD + col);
         }
     };
-    gload(0);
-    for (int kb = 0; kb < nkb; ++kb) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+        if (u < nkb) gload(u * KB, u);
+    for (int base = 0; base < nkb; base += PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+        const int kb = base + u;
+        if (kb >= nkb) break;  // uniform
         const int k0 = kb * KB;
-        __syncthreads();
+        lds_barrier();
         // K block -> sK[key][hd]
 #pragma unroll
         for (int p = 0; p < KL; ++p) {
             const int c = tid + 256 * p, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
-            *(f16x8*)&sK[row * LDK + col] = rk[p];
+            *(f16x8*)&sK[row * LDK + col] = rk[u][p];
         }
         // V block -> sVt[hd][key], two keys per 32-bit LDS store
 #pragma unroll
         for (int p = 0; p < VL; ++p) {
-            const int u = tid + 256 * p, kp = u & 31, col = (u >> 5) * 8;
+            const int v = tid + 256 * p, kp = v & 31, col = (v >> 5) * 8;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 typedef f16 f16x2 __attribute__((ext_vector_type(2)));
-                *(f16x2*)&sVt[(col + e) * LDV + 2 * kp] = f16x2{rva[p][e], rvb[p][e]};
+                *(f16x2*)&sVt[(col + e) * LDV + 2 * kp] = f16x2{rva[u][p][e], rvb[u][p][e]};
             }
         }
-        __syncthreads();
-        if (kb + 1 < nkb) gload(k0 + KB);
+        lds_barrier();
+        if (kb + PF < nkb) gload(k0 + PF * KB, u);
 
         // S^T tiles: chunk c (32 keys) x half u; tile row r -> key
         // 32c + 8(r/4) + 4u + r%4, so lane group g holds keys 32c + 8g + (0..7).
+        // All K fragments are read before the MFMAs and all V fragments
+        // before the softmax, so the LDS latency is paid once per block
+        // (read-one-use-one would serialise it under every MFMA).
+        f16x8 kf[2][2][NKK];
+        {
+            const int r = lane & 15;
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int krow = 32 * c + 8 * (r >> 2) + 4 * u + (r & 3);
+#pragma unroll
+                    for (int kk = 0; kk < NKK; ++kk)
+                        kf[c][u][kk] = *(const f16x8*)&sK[krow * LDK + kk * 32 + 8 * g];
+                }
+        }
+        __builtin_amdgcn_sched_barrier(0);
         f32x4 sc[2][2];
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int r = lane & 15;
-                const int krow = 32 * c + 8 * (r >> 2) + 4 * u + (r & 3);
-                f32x4 acc = {};
+            for (int u = 0; u < 2; ++u) sc[c][u] = f32x4{};
 #pragma unroll
-                for (int kk = 0; kk < NKK; ++kk) {
-                    const f16x8 ka = *(const f16x8*)&sK[krow * LDK + kk * 32 + 8 * g];
-                    acc = mfma16(ka, qf[kk], acc);
-                }
-                sc[c][u] = acc;
-            }
+        for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) sc[c][u] = mfma16(kf[c][u][kk], qf[kk], sc[c][u]);
+        __builtin_amdgcn_sched_barrier(0);
+        f16x8 vf[2][NHT];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int j = 0; j < NHT; ++j)
+                vf[c][j] = *(const f16x8*)&sVt[(16 * j + (lane & 15)) * LDV + 32 * c + 8 * g];
+        __builtin_amdgcn_sched_barrier(0);
+        // Mask keys past this query or past the sequence: key offsets within
+        // the block above lim are out (lim is large off the diagonal block).
+        const int lim = (k0 + KB > q0 || k0 + KB > S) ? min(qi, S - 1) - k0 - 8 * g : KB;
         float mloc = -INFINITY;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
@@ -131,16 +164,15 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
             for (int u = 0; u < 2; ++u)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int key = k0 + 32 * c + 8 * g + 4 * u + i;
                     float s = sc[c][u][i] * scale_log2;
-                    if (key > qi || key >= S) s = -INFINITY;
+                    if (32 * c + 4 * u + i > lim) s = -INFINITY;
                     sc[c][u][i] = s;
                     mloc = fmaxf(mloc, s);
                 }
         mloc = fmaxf(mloc, __shfl_xor(mloc, 16, RH_WAVE));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, RH_WAVE));
         const float m_new = fmaxf(m_run, mloc);
-        const float alpha = exp2f(m_run - m_new);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         m_run = m_new;
         float psum = 0.f;
         f16x8 pf[2];
@@ -150,7 +182,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
             for (int u = 0; u < 2; ++u)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float p = exp2f(sc[c][u][i] - m_new);
+                    const float p = __builtin_amdgcn_exp2f(sc[c][u][i] - m_new);
                     psum += p;
                     pf[c][4 * u + i] = (f16)p;
                 }
@@ -161,10 +193,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int j = 0; j < NHT; ++j) {
-                const f16x8 va = *(const f16x8*)&sVt[(16 * j + (lane & 15)) * LDV + 32 * c + 8 * g];
-                o[j] = mfma16(va, pf[c], o[j]);
-            }
+            for (int j = 0; j < NHT; ++j) o[j] = mfma16(vf[c][j], pf[c], o[j]);
+    }
     }
     float lt = l_run + __shfl_xor(l_run, 16, RH_WAVE);
     lt += __shfl_xor(lt, 32, RH_WAVE);
@@ -303,10 +333,11 @@ hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* ou
                                int S, int hd, int ctx, hipStream_t st) {
     const dim3 grid((S + 63) / 64, H, B);
     const float sl2 = (1.0f / sqrtf((float)hd)) * LOG2E;
+    constexpr int PF = 1;  // deeper register prefetch measured no faster
     if (hd == 128)
-        hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(256), 0, st, q, k, v, out, H, S, ctx, sl2);
+        hipLaunchKernelGGL((attn_prefill_kernel<128, PF>), grid, dim3(256), 0, st, q, k, v, out, H, S, ctx, sl2);
     else if (hd == 64)
-        hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(256), 0, st, q, k, v, out, H, S, ctx, sl2);
+        hipLaunchKernelGGL((attn_prefill_kernel<64, PF>), grid, dim3(256), 0, st, q, k, v, out, H, S, ctx, sl2);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

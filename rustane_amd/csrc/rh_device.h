@@ -53,6 +53,16 @@ __device__ __forceinline__ int xcd_remap(int b, int total) {
     return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + k;
 }
 
+// Workgroup barrier ordering LDS only: the release fence waits for this
+// wave's LDS accesses (lgkmcnt) but leaves global loads in flight, so
+// register prefetches issued before the barrier keep overlapping it
+// (__syncthreads would drain them with vmcnt(0)).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 
 // Fragment order of a [N, K] fp16 weight (rows padded to a multiple of 16,
