@@ -13,8 +13,12 @@ The same JSON line carries:
   forward_mfma  whole-forward algorithmic FLOPs / step time vs the fp16 peak
   decode        batch-1 greedy decode at ctx 2048 -> 2303 (graph replay) with
                 its HBM roofline (compulsory bytes / step time vs 8 TB/s)
+  prefill_batches / decode_batches / prefill_configs
+                the same measurements at batch 4 and 16, and batch-1 prefill
+                of the 600M and 5B shapes
   cpu_baseline  the CPU oracle (fp32 restatement of the reference forward)
-                timed on the host cores over a bounded sample
+                timed on the host cores over a bounded sample; likewise
+                cpu_baseline_decode for one KV-cached greedy step
 """
 from __future__ import annotations
 
@@ -50,7 +54,11 @@ def main():
     ap.add_argument("--decode-batch", type=int, default=1)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--extra-batches", default="", help="e.g. 4,16: also time these prefill batches")
+    ap.add_argument("--extra-batches", default="4,16", help="also time these prefill batches ('' for none)")
+    ap.add_argument("--extra-decode-batches", default="16",
+                    help="also time greedy decode at these batches ('' for none)")
+    ap.add_argument("--extra-configs", default="600m,5b",
+                    help="also time batch-1 prefill of these model shapes ('' for none)")
     ap.add_argument("--decode-only", action="store_true", help="skip the prefill timing")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run three 256 MiB device-to-device copies (a known-size kernel "
@@ -71,7 +79,8 @@ def main():
     cfg = {"7b": E.cfg_7b, "600m": E.cfg_600m, "5b": E.cfg_5b_deep, "tiny": E.tiny_config}[args.config]()
     cfg.seq = args.seq
     extra = [int(x) for x in args.extra_batches.split(",") if x]
-    max_batch = max([args.batch, args.decode_batch] + extra)
+    extra_dec = [] if args.no_decode else [int(x) for x in args.extra_decode_batches.split(",") if x]
+    max_batch = max([args.batch, args.decode_batch] + extra + extra_dec)
     max_ctx = 0 if args.no_decode else args.decode_ctx + args.decode_steps
     log(f"[bench] config={args.config} B={args.batch} S={cfg.seq} max_ctx={max_ctx}")
     t0 = time.time()
@@ -147,10 +156,19 @@ def main():
         log(f"[bench] prefill B={eb}: {extra_lines[f'B{eb}']}")
 
     decode = None
+    decode_lines = {}
     if not args.no_decode:
         decode = run_decode(ctx, cfg, args, hb, E, hip_rt, stream)
+        for db in extra_dec:
+            decode_lines[f"B{db}"] = run_decode(ctx, cfg, args, hb, E, hip_rt, stream, batch=db)
+    ctx.close()
+
+    config_lines = {}
+    for name in [x for x in args.extra_configs.split(",") if x]:
+        config_lines[name] = other_config_prefill(name, args, hb, E, hip_rt)
 
     cpu = None if args.no_cpu else cpu_baseline(cfg, args)
+    cpu_dec = None if (args.no_cpu or args.no_decode) else cpu_baseline_decode(cfg, args)
 
     line = {
         "metric": "prefill tok/s @7B seq512 fp16 (%MFMA); decode tok/s @7B b1 ctx2048 (%HBM)",
@@ -185,9 +203,46 @@ def main():
         line["prefill_batches"] = extra_lines
     if decode:
         line["decode"] = decode
+    if decode_lines:
+        line["decode_batches"] = decode_lines
+    if config_lines:
+        line["prefill_configs"] = config_lines
     if cpu:
         line["cpu_baseline"] = cpu
+    if cpu_dec:
+        line["cpu_baseline_decode"] = cpu_dec
     print(json.dumps(line), flush=True)
+
+
+def other_config_prefill(name, args, hb, E, hip_rt, steps=10, warmup=2):
+    """Batch-1 seq-512 prefill of another model shape (own context, device
+    weights N(0, 0.02)): tok/s and whole-forward MFMA fraction."""
+    cfg = {"7b": E.cfg_7b, "600m": E.cfg_600m, "5b": E.cfg_5b_deep, "tiny": E.tiny_config}[name]()
+    cfg.seq = 512
+    with hb.Context(cfg.to_rh(), 0, 1, 0) as c:
+        c.init_normal(seed=4321, std=0.02)
+        rng = np.random.default_rng(11)
+        toks = rng.integers(0, cfg.vocab, size=(1, cfg.seq + 1)).astype(np.uint32)
+        tok = hip_rt.DeviceArray.from_numpy(toks[:, :-1])
+        tgt = hip_rt.DeviceArray.from_numpy(toks[:, 1:])
+        mean = hip_rt.DeviceArray((1,), np.float32)
+        for _ in range(warmup):
+            c.forward_dev(tok.ptr, tgt.ptr, 1, cfg.seq, None, None, mean.ptr)
+        c.sync()
+        ev0, ev1 = hip_rt.Event(), hip_rt.Event()
+        ev0.record(c.stream)
+        for _ in range(steps):
+            c.forward_dev(tok.ptr, tgt.ptr, 1, cfg.seq, None, None, mean.ptr)
+        ev1.record(c.stream)
+        c.sync()
+        ms = ev0.elapsed_ms(ev1) / steps
+    fl = E.prefill_flops(cfg, cfg.seq, 1)["total"]
+    out = {"dim": cfg.dim, "hidden": cfg.hidden, "nlayers": cfg.nlayers, "heads": cfg.heads,
+           "vocab": cfg.vocab, "seq_len": cfg.seq, "tok_s": round(cfg.seq / (ms / 1e3), 1),
+           "ms_per_step": round(ms, 4), "flops_per_step": fl,
+           "forward_mfma_frac": round(fl / (ms / 1e3) / 1e12 / PEAK_FP16_TFLOPS, 4)}
+    log(f"[bench] prefill {name}: {out}")
+    return out
 
 
 def measured_traffic(config, batch, seq):
@@ -203,8 +258,8 @@ def measured_traffic(config, batch, seq):
         return None
 
 
-def run_decode(ctx, cfg, args, hb, E, hip_rt, stream):
-    B = args.decode_batch
+def run_decode(ctx, cfg, args, hb, E, hip_rt, stream, batch=None):
+    B = batch or args.decode_batch
     ctx.set_graphs(not args.decode_eager)
     rng = np.random.default_rng(7)
     prompt = rng.integers(0, cfg.vocab, size=(B, args.decode_ctx)).astype(np.uint32)
@@ -288,6 +343,51 @@ def cpu_baseline(cfg, args):
             "sample": f"oracle fp32 forward at dim {D}/hidden {F}/vocab {V}/seq {S} with 1 and 2 layers "
                       f"({times[1]:.2f}s, {times[2]:.2f}s), extrapolated linearly to {cfg.nlayers} layers "
                       f"({t_total:.1f}s per forward)"}
+
+
+def cpu_baseline_decode(cfg, args, steps=4):
+    """Oracle KV-cached greedy step at the same width over a bounded sample:
+    1 and 2 layers, a 2048-token prompt, median of a few steps, extrapolated
+    linearly in the layer count (the tied-logits GEMV is in both samples)."""
+    try:
+        import oracle
+    except Exception as e:  # pragma: no cover
+        log(f"[bench] no oracle: {e}")
+        return None
+    oracle.build()
+    L = oracle.lib()
+    D, F, V = cfg.dim, cfg.hidden, cfg.vocab
+    ctx_len = args.decode_ctx
+    rng = np.random.default_rng(6)
+
+    def mat(*s):
+        return (rng.standard_normal(s, dtype=np.float32) * np.float32(0.02))
+
+    lw = [mat(D, D), mat(D, D), mat(D, D), mat(D, D), mat(D, F), mat(D, F), mat(D, F),
+          np.ones(D, np.float32), np.ones(D, np.float32)]
+    embed = mat(V, D)
+    prompt = rng.integers(0, V, size=ctx_len).astype(np.uint32)
+    step_s = {}
+    for nl in (1, 2):
+        ocfg = oracle.make_config(D, F, cfg.heads, nl, V, head_dim=cfg.hd)
+        w = oracle.Weights(embed, np.ones(D, np.float32), [lw] * nl)
+        kv = oracle.KV(ocfg, ctx_len + steps + 1)
+        lg = kv.prefill(w, prompt)
+        tok = int(np.argmax(lg))
+        ts = []
+        for _ in range(steps):
+            t = time.perf_counter()
+            tok, _ = kv.step(w, tok)
+            ts.append(time.perf_counter() - t)
+        step_s[nl] = float(np.median(ts))
+    t_layer = max(step_s[2] - step_s[1], 1e-9)
+    t_step = step_s[1] + (cfg.nlayers - 1) * t_layer
+    return {"value": round(1.0 / t_step, 3), "unit": "tok/s", "cores": int(L.orc_num_threads()),
+            "kind": "port", "batch": 1,
+            "sample": f"oracle fp32 KV-cached greedy step at dim {D}/hidden {F}/vocab {V}, ctx {ctx_len}, "
+                      f"1 and 2 layers (median of {steps} steps: {step_s[1] * 1e3:.1f} ms, "
+                      f"{step_s[2] * 1e3:.1f} ms), extrapolated linearly to {cfg.nlayers} layers "
+                      f"({t_step * 1e3:.0f} ms per token)"}
 
 
 if __name__ == "__main__":
