@@ -39,6 +39,7 @@ extern "C" {
 #define RH_ENOMEM -3     /* device allocation failed                     */
 #define RH_EDEVICE -4    /* HIP runtime error                            */
 #define RH_ESTATE -5     /* call out of order (e.g. decode before prefill) */
+#define RH_EIO -6        /* file missing, unreadable or not in the format */
 
 /* ModelConfig (crates/engine/src/model.rs:5-17).  MHA only: kv_heads must
  * equal heads (the reference reshapes K/V with `heads`, sdpa_fwd.rs:162-181).
@@ -59,7 +60,11 @@ typedef struct rh_ctx rh_ctx;
  * No JIT: kernels are precompiled for gfx950. */
 int rh_create(const rh_config* cfg, int device, int max_batch, int max_ctx, rh_ctx** out);
 void rh_destroy(rh_ctx* ctx);
+/* Last error message of the context; with ctx NULL, of the calling thread's
+ * last context-free call (token files, checkpoint header, compute_bpb). */
 const char* rh_last_error(const rh_ctx* ctx);
+/* The context's configuration and capacities (any output may be NULL). */
+int rh_context_info(const rh_ctx* ctx, rh_config* cfg_out, int* max_batch_out, int* max_ctx_out);
 
 /* Uploads ModelWeights (full_model.rs:19-23) in the reference orientation,
  * fp32 -> fp16 for matrices, fp32 for gammas; replaces the per-call weight
@@ -152,6 +157,53 @@ int rh_profile_read(rh_ctx* ctx, int kernel_class, double* total_ms, int64_t* la
 
 /* Decode steps as a captured HIP graph (1, default) or eager launches (0). */
 int rh_set_graphs(rh_ctx* ctx, int enable);
+
+/* ---- on-disk formats either side of the forward ----------------------- */
+
+/* RSTK v1 checkpoint (bin/train.rs:238-345): "RSTK", then version, step, dim,
+ * nlayers, vocab, seq as little-endian u32 (28 bytes), then fp32 tensors
+ * embed[V*D], gamma_final[D] and per layer wq wk wv wo w1 w3 w2 gamma1
+ * gamma2 in the rh_load_weights_f32 orientation.  hidden is not stored. */
+typedef struct rh_ckpt_info {
+    uint32_t version, step, dim, nlayers, vocab, seq;
+    uint64_t file_bytes;
+} rh_ckpt_info;
+/* Reads the header only (context-free). */
+int rh_checkpoint_info(const char* path, rh_ckpt_info* out);
+/* load_checkpoint (bin/train.rs:296-345): maps the file and uploads its
+ * weights.  The header's dim/nlayers/vocab must match the context and the
+ * file must hold exactly the tensors of the context's config; step_out
+ * (nullable) receives the stored step. */
+int rh_load_checkpoint(rh_ctx* ctx, const char* path, uint32_t* step_out);
+/* save_checkpoint (bin/train.rs:238-275) of the device weights (fp16
+ * widened to fp32; seq = the context's seq); written to path.tmp, renamed. */
+int rh_save_checkpoint(rh_ctx* ctx, const char* path, uint32_t step);
+
+/* TokenData (data.rs:11-44): a memory-mapped flat little-endian uint16 token
+ * file (a trailing odd byte is ignored). */
+typedef struct rh_tokens rh_tokens;
+int rh_tokens_open(const char* path, rh_tokens** out);
+void rh_tokens_close(rh_tokens* tokens);
+int64_t rh_tokens_len(const rh_tokens* tokens);
+/* tokens(start, len) widened to u32; RH_ERANGE past the end. */
+int rh_tokens_read(const rh_tokens* tokens, int64_t start, int len, uint32_t* out);
+
+/* compute_bpb (data.rs:75-91): over the n (loss, target) pairs whose
+ * token_bytes[target] > 0, bpb = sum(loss) / (ln 2 * sum(bytes)), summed in
+ * order in fp32 (0 when no bytes).  token_bytes holds `vocab` int32 entries
+ * (token_bytes.bin, data.rs:46-71).  Any output may be NULL. */
+int rh_compute_bpb(const float* losses, const uint32_t* targets, int64_t n, const int32_t* token_bytes,
+                   int vocab, float* bpb_out, float* total_nats_out, int64_t* total_bytes_out);
+
+/* validate (bin/train.rs:196-236): `steps` windows of the context's seq at
+ * pos = (s * seq) % (len - seq - 1), input tokens(pos, seq), targets
+ * tokens(pos + 1, seq); per-token losses by the forward (forward_losses,
+ * full_model.rs:1603-1660), up to max_batch windows per launch.
+ * avg_loss_out = sum of losses / tokens; bpb_out = compute_bpb over all
+ * windows when token_bytes ([vocab]) is given, else 0.  Needs
+ * len >= seq + 2. */
+int rh_validate(rh_ctx* ctx, const rh_tokens* val, const int32_t* token_bytes, int steps,
+                float* avg_loss_out, float* bpb_out);
 
 #ifdef __cplusplus
 }

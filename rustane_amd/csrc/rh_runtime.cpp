@@ -14,6 +14,7 @@
 // step runs the same chain on B <= 16 tokens with GEMV kernels and a KV cache,
 // and is replayed as a captured HIP graph.
 #include "../../include/rustane_hip.h"
+#include "rh_internal.h"
 #include "rh_kernels.h"
 
 #include <hip/hip_runtime.h>
@@ -454,7 +455,19 @@ void destroy_ctx(rh_ctx* ctx) {
 
 extern "C" {
 
-const char* rh_last_error(const rh_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+const char* rh_last_error(const rh_ctx* ctx) { return ctx ? ctx->err.c_str() : rh_internal_tls_error(); }
+
+}  // extern "C"
+int rh_internal_fail(rh_ctx* ctx, int code, const std::string& msg) { return fail(ctx, code, msg); }
+extern "C" {
+
+int rh_context_info(const rh_ctx* ctx, rh_config* cfg_out, int* max_batch_out, int* max_ctx_out) {
+    if (!ctx) return RH_EINVAL;
+    if (cfg_out) *cfg_out = ctx->cfg;
+    if (max_batch_out) *max_batch_out = ctx->max_batch;
+    if (max_ctx_out) *max_ctx_out = ctx->max_ctx;
+    return RH_OK;
+}
 
 int rh_create(const rh_config* cfg, int device, int max_batch, int max_ctx, rh_ctx** out) {
     if (!cfg || !out) return RH_EINVAL;

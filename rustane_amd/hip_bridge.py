@@ -16,9 +16,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "librustane_hip.so")
 HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "rustane_hip.h")
 
-RH_OK, RH_EINVAL, RH_ERANGE, RH_ENOMEM, RH_EDEVICE, RH_ESTATE = 0, -1, -2, -3, -4, -5
+RH_OK, RH_EINVAL, RH_ERANGE, RH_ENOMEM, RH_EDEVICE, RH_ESTATE, RH_EIO = 0, -1, -2, -3, -4, -5, -6
 ERR_NAMES = {RH_EINVAL: "RH_EINVAL", RH_ERANGE: "RH_ERANGE", RH_ENOMEM: "RH_ENOMEM",
-             RH_EDEVICE: "RH_EDEVICE", RH_ESTATE: "RH_ESTATE"}
+             RH_EDEVICE: "RH_EDEVICE", RH_ESTATE: "RH_ESTATE", RH_EIO: "RH_EIO"}
 
 K_GEMM_QKV, K_GEMM_WO, K_GEMM_W13, K_GEMM_W2, K_GEMM_LOGITS, K_ATTN = range(6)
 K_GEMV_QKV, K_GEMV_WO, K_GEMV_W13, K_GEMV_W2, K_GEMV_LOGITS, K_DECODE_ATTN = range(6, 12)
@@ -40,6 +40,12 @@ class RhConfig(ctypes.Structure):
                 ("seq", ctypes.c_int32), ("nlayers", ctypes.c_int32), ("vocab", ctypes.c_int32),
                 ("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float),
                 ("softcap", ctypes.c_float)]
+
+
+class RhCkptInfo(ctypes.Structure):
+    _fields_ = [("version", ctypes.c_uint32), ("step", ctypes.c_uint32), ("dim", ctypes.c_uint32),
+                ("nlayers", ctypes.c_uint32), ("vocab", ctypes.c_uint32), ("seq", ctypes.c_uint32),
+                ("file_bytes", ctypes.c_uint64)]
 
 
 _lib = None
@@ -78,6 +84,21 @@ def lib():
     L.rh_profile_read.argtypes = [ctxp, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                   ctypes.POINTER(ctypes.c_int64)]
     L.rh_set_graphs.argtypes = [ctxp, ctypes.c_int]
+    L.rh_context_info.argtypes = [ctxp, ctypes.POINTER(RhConfig), ctypes.POINTER(ctypes.c_int),
+                                  ctypes.POINTER(ctypes.c_int)]
+    L.rh_checkpoint_info.argtypes = [ctypes.c_char_p, ctypes.POINTER(RhCkptInfo)]
+    L.rh_load_checkpoint.argtypes = [ctxp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32)]
+    L.rh_save_checkpoint.argtypes = [ctxp, ctypes.c_char_p, ctypes.c_uint32]
+    L.rh_tokens_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]
+    L.rh_tokens_close.argtypes = [ctypes.c_void_p]
+    L.rh_tokens_close.restype = None
+    L.rh_tokens_len.argtypes = [ctypes.c_void_p]
+    L.rh_tokens_len.restype = ctypes.c_int64
+    L.rh_tokens_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, _u32p]
+    L.rh_compute_bpb.argtypes = [_f32p, _u32p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int32), ctypes.c_int,
+                                 _f32p, _f32p, ctypes.POINTER(ctypes.c_int64)]
+    L.rh_validate.argtypes = [ctxp, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int32), ctypes.c_int, _f32p,
+                              _f32p]
     _lib = L
     return L
 
@@ -235,3 +256,87 @@ class Context:
 
     def set_graphs(self, on: bool):
         self._ck(lib().rh_set_graphs(self.h, int(on)), "rh_set_graphs")
+
+    # -- on-disk formats ----------------------------------------------------
+    def load_checkpoint(self, path: str) -> int:
+        """load_checkpoint (bin/train.rs:296-345); returns the stored step."""
+        step = ctypes.c_uint32()
+        self._ck(lib().rh_load_checkpoint(self.h, os.fsencode(path), ctypes.byref(step)),
+                 "rh_load_checkpoint")
+        return step.value
+
+    def save_checkpoint(self, path: str, step: int):
+        """save_checkpoint (bin/train.rs:238-275) of the device weights."""
+        self._ck(lib().rh_save_checkpoint(self.h, os.fsencode(path), step), "rh_save_checkpoint")
+
+    def validate(self, val: "TokenData", token_bytes: "TokenBytes | None", steps: int):
+        """validate (bin/train.rs:196-236) -> (avg_loss, bpb)."""
+        loss, bpb = ctypes.c_float(), ctypes.c_float()
+        tb = None if token_bytes is None else token_bytes.ptr()
+        self._ck(lib().rh_validate(self.h, val.h, tb, steps, ctypes.byref(loss), ctypes.byref(bpb)),
+                 "rh_validate")
+        return loss.value, bpb.value
+
+
+def _ck_free(rc: int, what: str):
+    if rc != RH_OK:
+        raise HipBridgeError(rc, f"{what}: {lib().rh_last_error(None).decode(errors='replace')}")
+
+
+def checkpoint_info(path: str) -> RhCkptInfo:
+    """RSTK header fields (bin/train.rs:249-256)."""
+    info = RhCkptInfo()
+    _ck_free(lib().rh_checkpoint_info(os.fsencode(path), ctypes.byref(info)), "rh_checkpoint_info")
+    return info
+
+
+class TokenData:
+    """TokenData (data.rs:11-44): a memory-mapped uint16 token file."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        _ck_free(lib().rh_tokens_open(os.fsencode(path), ctypes.byref(h)), "rh_tokens_open")
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().rh_tokens_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __len__(self) -> int:
+        return int(lib().rh_tokens_len(self.h))
+
+    def tokens(self, start: int, n: int) -> np.ndarray:
+        out = np.empty(n, np.uint32)
+        _ck_free(lib().rh_tokens_read(self.h, start, n, _u(out)), "rh_tokens_read")
+        return out
+
+
+class TokenBytes:
+    """TokenBytes (data.rs:46-71): int32 byte length per token id."""
+
+    def __init__(self, path: str | None = None, values=None):
+        self.bytes = (np.fromfile(path, dtype="<i4") if path is not None
+                      else np.ascontiguousarray(values, dtype=np.int32))
+
+    def ptr(self):
+        return self.bytes.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+
+
+def compute_bpb(losses, targets, token_bytes: TokenBytes):
+    """compute_bpb (data.rs:75-91) -> (bpb, total_nats, total_bytes)."""
+    losses = np.ascontiguousarray(losses, np.float32).ravel()
+    targets = np.ascontiguousarray(targets, np.uint32).ravel()
+    if losses.size != targets.size:
+        raise ValueError("losses and targets differ in length")
+    bpb, nats, nb = ctypes.c_float(), ctypes.c_float(), ctypes.c_int64()
+    _ck_free(lib().rh_compute_bpb(_f(losses), _u(targets), losses.size, token_bytes.ptr(),
+                                  token_bytes.bytes.size, ctypes.byref(bpb), ctypes.byref(nats),
+                                  ctypes.byref(nb)), "rh_compute_bpb")
+    return bpb.value, nats.value, nb.value

@@ -51,6 +51,18 @@ def random_gammas(w: ModelWeights, seed: int):
     return w
 
 
+def rstk_bytes(cfg: ModelConfig, w: ModelWeights, step: int) -> bytes:
+    """An RSTK v1 checkpoint built from the format definition
+    (bin/train.rs:238-275): 28-byte little-endian header, then every tensor
+    as little-endian fp32 in upload order."""
+    import struct
+    parts = [struct.pack("<4s6I", b"RSTK", 1, step, cfg.dim, cfg.nlayers, cfg.vocab, cfg.seq),
+             np.ascontiguousarray(w.embed, "<f4").tobytes(), np.ascontiguousarray(w.gamma_final, "<f4").tobytes()]
+    for lw in w.layers:
+        parts += [np.ascontiguousarray(t, "<f4").tobytes() for t in lw.tensors()]
+    return b"".join(parts)
+
+
 def cosine(a, b):
     a = a.ravel().astype(np.float64)
     b = b.ravel().astype(np.float64)

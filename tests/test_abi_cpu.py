@@ -115,5 +115,23 @@ def test_null_context_is_rejected_everywhere(lib):
     assert lib.rh_profile_enable(None, 0, 1) == hb.RH_EINVAL
     assert lib.rh_set_graphs(None, 1) == hb.RH_EINVAL
     assert lib.rh_stream(None) is None
-    assert lib.rh_last_error(None) == b"null context"
+    assert lib.rh_context_info(None, None, None, None) == hb.RH_EINVAL
+    assert lib.rh_load_checkpoint(None, b"x", None) == hb.RH_EINVAL
+    assert lib.rh_save_checkpoint(None, b"x", 0) == hb.RH_EINVAL
+    assert lib.rh_validate(None, None, None, 1, None, None) == hb.RH_EINVAL
     lib.rh_destroy(None)  # a no-op
+    lib.rh_tokens_close(None)  # a no-op
+    assert lib.rh_tokens_len(None) == 0
+
+
+def test_context_free_errors_are_per_thread(lib):
+    """rh_last_error(NULL) reports the calling thread's last context-free
+    failure."""
+    import threading
+    assert lib.rh_tokens_open(b"/nonexistent/tokens.bin", ctypes.byref(ctypes.c_void_p())) == hb.RH_EIO
+    assert b"/nonexistent/tokens.bin" in lib.rh_last_error(None)
+    seen = []
+    th = threading.Thread(target=lambda: seen.append(lib.rh_last_error(None)))
+    th.start()
+    th.join()
+    assert seen == [b""]
