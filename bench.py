@@ -53,6 +53,8 @@ def main():
     ap.add_argument("--decode-ctx", type=int, default=2048)
     ap.add_argument("--decode-batch", type=int, default=1)
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="only the headline configuration (no extra batches or model shapes)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--extra-batches", default="4,16", help="also time these prefill batches ('' for none)")
     ap.add_argument("--extra-decode-batches", default="16",
@@ -78,6 +80,8 @@ def main():
 
     cfg = {"7b": E.cfg_7b, "600m": E.cfg_600m, "5b": E.cfg_5b_deep, "tiny": E.tiny_config}[args.config]()
     cfg.seq = args.seq
+    if args.no_extra:
+        args.extra_batches = args.extra_decode_batches = args.extra_configs = ""
     extra = [int(x) for x in args.extra_batches.split(",") if x]
     extra_dec = [] if args.no_decode else [int(x) for x in args.extra_decode_batches.split(",") if x]
     max_batch = max([args.batch, args.decode_batch] + extra + extra_dec)
