@@ -205,6 +205,47 @@ int rh_compute_bpb(const float* losses, const uint32_t* targets, int64_t n, cons
 int rh_validate(rh_ctx* ctx, const rh_tokens* val, const int32_t* token_bytes, int steps,
                 float* avg_loss_out, float* bpb_out);
 
+/* ---- request scheduler (multistream::ForwardScheduler, multistream.rs:54-161) ----
+ * One worker thread owns the context and serves a bounded FIFO in batches:
+ * up to max_batch forward requests of equal length run as one rh_forward,
+ * generation requests of equal prompt length and step count as one
+ * rh_prefill + rh_decode (batch <= 16).  The worker waits up to max_wait_us
+ * after the oldest request for a batch to fill (0: serve what is queued).
+ * While a scheduler exists only its worker may use the context. */
+#define RH_JOB_FORWARD 0   /* tokens/targets [len] -> loss (forward_only_ws)   */
+#define RH_JOB_GENERATE 1  /* prompt [len] -> nsteps greedy tokens (out_tokens) */
+typedef struct rh_sched rh_sched;
+typedef struct rh_sched_config {
+    int max_batch;       /* requests per launch (also capped by the context)  */
+    int queue_capacity;  /* submit blocks while this many are queued           */
+    int max_wait_us;
+} rh_sched_config;
+typedef struct rh_sched_request {
+    uint64_t request_id;
+    int kind, len, nsteps;
+    const uint32_t* tokens;   /* copied at submit                              */
+    const uint32_t* targets;  /* forward only, copied at submit                */
+    uint32_t* out_tokens;     /* generate only: written before the result is posted */
+} rh_sched_request;
+typedef struct rh_sched_result {   /* ForwardBenchResult (multistream.rs:35-42) + batch/status */
+    uint64_t request_id;
+    int kind, status;         /* status: RH_OK or the failing call's code      */
+    float loss;               /* forward: mean CE over the request's tokens    */
+    int batch;                /* requests served in the same launch            */
+    float queue_wait_ms, service_ms, total_ms;
+    char message[128];        /* error text when status != RH_OK               */
+} rh_sched_result;
+int rh_sched_create(rh_ctx* ctx, const rh_sched_config* cfg, rh_sched** out);
+/* Drains the queue, then stops the worker. */
+void rh_sched_destroy(rh_sched* sched);
+int rh_sched_submit(rh_sched* sched, const rh_sched_request* request);
+/* Blocks for the next finished request (RH_ESTATE if none is outstanding). */
+int rh_sched_wait(rh_sched* sched, rh_sched_result* out);
+/* ForwardScheduler::run_batch: submits n requests, waits for all, results
+ * sorted by request id (no other requests may be outstanding). */
+int rh_sched_run_batch(rh_sched* sched, const rh_sched_request* requests, int n,
+                       rh_sched_result* results);
+
 #ifdef __cplusplus
 }
 #endif

@@ -48,6 +48,24 @@ class RhCkptInfo(ctypes.Structure):
                 ("file_bytes", ctypes.c_uint64)]
 
 
+class RhSchedConfig(ctypes.Structure):
+    _fields_ = [("max_batch", ctypes.c_int), ("queue_capacity", ctypes.c_int), ("max_wait_us", ctypes.c_int)]
+
+
+class RhSchedRequest(ctypes.Structure):
+    _fields_ = [("request_id", ctypes.c_uint64), ("kind", ctypes.c_int), ("len", ctypes.c_int),
+                ("nsteps", ctypes.c_int), ("tokens", ctypes.POINTER(ctypes.c_uint32)),
+                ("targets", ctypes.POINTER(ctypes.c_uint32)), ("out_tokens", ctypes.POINTER(ctypes.c_uint32))]
+
+
+class RhSchedResult(ctypes.Structure):
+    _fields_ = [("request_id", ctypes.c_uint64), ("kind", ctypes.c_int), ("status", ctypes.c_int),
+                ("loss", ctypes.c_float), ("batch", ctypes.c_int), ("queue_wait_ms", ctypes.c_float),
+                ("service_ms", ctypes.c_float), ("total_ms", ctypes.c_float), ("message", ctypes.c_char * 128)]
+
+
+JOB_FORWARD, JOB_GENERATE = 0, 1
+
 _lib = None
 
 
@@ -99,6 +117,13 @@ def lib():
                                  _f32p, _f32p, ctypes.POINTER(ctypes.c_int64)]
     L.rh_validate.argtypes = [ctxp, ctypes.c_void_p, ctypes.POINTER(ctypes.c_int32), ctypes.c_int, _f32p,
                               _f32p]
+    L.rh_sched_create.argtypes = [ctxp, ctypes.POINTER(RhSchedConfig), ctypes.POINTER(ctypes.c_void_p)]
+    L.rh_sched_destroy.argtypes = [ctypes.c_void_p]
+    L.rh_sched_destroy.restype = None
+    L.rh_sched_submit.argtypes = [ctypes.c_void_p, ctypes.POINTER(RhSchedRequest)]
+    L.rh_sched_wait.argtypes = [ctypes.c_void_p, ctypes.POINTER(RhSchedResult)]
+    L.rh_sched_run_batch.argtypes = [ctypes.c_void_p, ctypes.POINTER(RhSchedRequest), ctypes.c_int,
+                                     ctypes.POINTER(RhSchedResult)]
     _lib = L
     return L
 
@@ -340,3 +365,66 @@ def compute_bpb(losses, targets, token_bytes: TokenBytes):
                                   token_bytes.bytes.size, ctypes.byref(bpb), ctypes.byref(nats),
                                   ctypes.byref(nb)), "rh_compute_bpb")
     return bpb.value, nats.value, nb.value
+
+
+@dataclass
+class SchedResult:
+    request_id: int
+    kind: int
+    status: int
+    loss: float
+    batch: int
+    queue_wait_ms: float
+    service_ms: float
+    total_ms: float
+    message: str
+    tokens: np.ndarray | None = None  # generate requests
+
+
+class Scheduler:
+    """rh_sched over one Context (multistream::ForwardScheduler,
+    multistream.rs:54-161): forward requests (tokens, targets) -> loss and
+    generation requests (prompt, nsteps) -> greedy tokens, served in batches by
+    one worker thread.  While it exists only the worker uses the context."""
+
+    def __init__(self, ctx: Context, max_batch: int, queue_capacity: int | None = None,
+                 max_wait_us: int = 0):
+        cfg = RhSchedConfig(max_batch, queue_capacity or 2 * max_batch, max_wait_us)
+        h = ctypes.c_void_p()
+        ctx._ck(lib().rh_sched_create(ctx.h, ctypes.byref(cfg), ctypes.byref(h)), "rh_sched_create")
+        self.h, self.ctx = h, ctx
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().rh_sched_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @staticmethod
+    def _request(rid, kind, tokens, targets=None, nsteps=0):
+        tok = np.ascontiguousarray(tokens, np.uint32).ravel()
+        tgt = None if targets is None else np.ascontiguousarray(targets, np.uint32).ravel()
+        out = np.zeros(nsteps, np.uint32) if kind == JOB_GENERATE else None
+        rq = RhSchedRequest(rid, kind, tok.size, nsteps, _u(tok), _u(tgt), _u(out))
+        return rq, (tok, tgt, out)
+
+    def run_batch(self, requests):
+        """ForwardScheduler::run_batch.  requests: (id, tokens, targets) for a
+        forward or (id, prompt, None, nsteps) for a generation; results sorted
+        by id."""
+        built = [self._request(r[0], JOB_GENERATE if len(r) > 3 else JOB_FORWARD, r[1], r[2],
+                               r[3] if len(r) > 3 else 0) for r in requests]
+        arr = (RhSchedRequest * len(built))(*[b[0] for b in built])
+        res = (RhSchedResult * len(built))()
+        rc = lib().rh_sched_run_batch(self.h, arr, len(built), res)
+        if rc != RH_OK:
+            raise HipBridgeError(rc, "rh_sched_run_batch")
+        outs = {r[0]: keep[2] for r, (_, keep) in zip(requests, built)}
+        return [SchedResult(x.request_id, x.kind, x.status, x.loss, x.batch, x.queue_wait_ms, x.service_ms,
+                            x.total_ms, x.message.decode(errors="replace"), outs.get(x.request_id))
+                for x in res]

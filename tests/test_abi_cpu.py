@@ -122,6 +122,11 @@ def test_null_context_is_rejected_everywhere(lib):
     lib.rh_destroy(None)  # a no-op
     lib.rh_tokens_close(None)  # a no-op
     assert lib.rh_tokens_len(None) == 0
+    assert lib.rh_sched_create(None, None, None) == hb.RH_EINVAL
+    assert lib.rh_sched_submit(None, None) == hb.RH_EINVAL
+    assert lib.rh_sched_wait(None, None) == hb.RH_EINVAL
+    assert lib.rh_sched_run_batch(None, None, 0, None) == hb.RH_EINVAL
+    lib.rh_sched_destroy(None)  # a no-op
 
 
 def test_context_free_errors_are_per_thread(lib):
