@@ -16,6 +16,7 @@ The same JSON line carries:
   prefill_batches / decode_batches / prefill_configs
                 the same measurements at batch 4 and 16, and batch-1 prefill
                 of the 600M and 5B shapes
+  scheduler     32 forward requests through the request scheduler
   cpu_baseline  the CPU oracle (fp32 restatement of the reference forward)
                 timed on the host cores over a bounded sample; likewise
                 cpu_baseline_decode for one KV-cached greedy step
@@ -159,6 +160,10 @@ def main():
         }
         log(f"[bench] prefill B={eb}: {extra_lines[f'B{eb}']}")
 
+    sched = None
+    if not args.no_extra and max_batch >= 16:
+        sched = run_scheduler(ctx, cfg, hb, requests=32, max_batch=16)
+
     decode = None
     decode_lines = {}
     if not args.no_decode:
@@ -209,6 +214,8 @@ def main():
         line["decode"] = decode
     if decode_lines:
         line["decode_batches"] = decode_lines
+    if sched:
+        line["scheduler"] = sched
     if config_lines:
         line["prefill_configs"] = config_lines
     if cpu:
@@ -216,6 +223,29 @@ def main():
     if cpu_dec:
         line["cpu_baseline_decode"] = cpu_dec
     print(json.dumps(line), flush=True)
+
+
+def run_scheduler(ctx, cfg, hb, requests, max_batch):
+    """Forward requests (seq 512) submitted at once to the request scheduler
+    (the multistream ForwardScheduler analogue): served in batches of up to
+    max_batch; whole-run tok/s from the host clock, loss per request."""
+    rng = np.random.default_rng(21)
+    reqs = []
+    for i in range(requests):
+        t = rng.integers(0, cfg.vocab, size=cfg.seq + 1).astype(np.uint32)
+        reqs.append((i, t[:-1], t[1:]))
+    with hb.Scheduler(ctx, max_batch=max_batch, max_wait_us=2000) as s:
+        s.run_batch(reqs[:max_batch])  # warm-up
+        t = time.perf_counter()
+        res = s.run_batch(reqs)
+        wall = time.perf_counter() - t
+    bad = [r.request_id for r in res if r.status != 0]
+    out = {"requests": requests, "max_batch": max_batch, "seq_len": cfg.seq,
+           "tok_s": round(requests * cfg.seq / wall, 1), "wall_s": round(wall, 4),
+           "mean_batch": round(float(np.mean([r.batch for r in res])), 2),
+           "mean_total_ms": round(float(np.mean([r.total_ms for r in res])), 2), "failed": bad}
+    log(f"[bench] scheduler: {out}")
+    return out
 
 
 def other_config_prefill(name, args, hb, E, hip_rt, steps=10, warmup=2):
