@@ -17,6 +17,8 @@
 // scores its chunk with 16-byte K loads (hd/8 lanes per position) and keeps
 // (max, sum, P.V) partials; a small kernel merges them.  The position is read
 // from device memory so the step can be replayed as a graph.
+#include <type_traits>
+
 #include "rh_device.h"
 #include "rh_kernels.h"
 
@@ -154,26 +156,41 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
             for (int j = 0; j < NHT; ++j)
                 vf[c][j] = *(const f16x8*)&sVt[(16 * j + (lane & 15)) * LDV + 32 * c + 8 * g];
         __builtin_amdgcn_sched_barrier(0);
-        // Mask keys past this query or past the sequence: key offsets within
-        // the block above lim are out (lim is large off the diagonal block).
-        const int lim = (k0 + KB > q0 || k0 + KB > S) ? min(qi, S - 1) - k0 - 8 * g : KB;
-        float mloc = -INFINITY;
+        // Online softmax in the log2 domain on raw scores: the 1/sqrt(hd)
+        // scale rides in the exponent's fma.  The running max only moves when
+        // a row's block max exceeds it by more than 8 (log2 units); exp2 of
+        // (score - stale max) then stays <= 256, as exact in the fp16 P operand
+        // as values <= 1, and the O rescale (32 multiplies) is skipped for the
+        // whole wave in the common case.  Only the block holding the diagonal
+        // (or the sequence end) runs the mask: key offsets within the block
+        // above lim are out.
+        const int lim = min(qi, S - 1) - k0 - 8 * g;
+        auto block_max = [&](auto diag) {
+            float mx = -INFINITY;
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+            for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+                for (int u = 0; u < 2; ++u)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float s = sc[c][u][i] * scale_log2;
-                    if (32 * c + 4 * u + i > lim) s = -INFINITY;
-                    sc[c][u][i] = s;
-                    mloc = fmaxf(mloc, s);
-                }
+                    for (int i = 0; i < 4; ++i) {
+                        if constexpr (decltype(diag)::value)
+                            if (32 * c + 4 * u + i > lim) sc[c][u][i] = -INFINITY;
+                        mx = fmaxf(mx, sc[c][u][i]);
+                    }
+            return mx;
+        };
+        float mloc = (k0 + KB > q0 || k0 + KB > S) ? block_max(std::true_type{}) : block_max(std::false_type{});
         mloc = fmaxf(mloc, __shfl_xor(mloc, 16, RH_WAVE));
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, RH_WAVE));
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
+        mloc *= scale_log2;
+        if (__any(mloc > m_run + 8.0f)) {
+            const float m_new = fmaxf(m_run, mloc);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int j = 0; j < NHT; ++j) o[j] *= alpha;
+            m_run = m_new;
+        }
         float psum = 0.f;
         f16x8 pf[2];
 #pragma unroll
@@ -182,13 +199,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
             for (int u = 0; u < 2; ++u)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const float p = __builtin_amdgcn_exp2f(sc[c][u][i] - m_new);
+                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[c][u][i], scale_log2, -m_run));
                     psum += p;
                     pf[c][4 * u + i] = (f16)p;
                 }
-        l_run = l_run * alpha + psum;
-#pragma unroll
-        for (int j = 0; j < NHT; ++j) o[j] *= alpha;
+        l_run += psum;
         // O^T[hd][q] += V^T[hd][keys] . P^T[keys][q]
 #pragma unroll
         for (int c = 0; c < 2; ++c)
