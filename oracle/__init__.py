@@ -34,6 +34,10 @@ class OrcWeights(ctypes.Structure):
     _fields_ = [("embed", _f32p), ("gamma_final", _f32p), ("layers", ctypes.POINTER(_f32p))]
 
 
+class OrcGrads(ctypes.Structure):
+    _fields_ = [("dembed", _f32p), ("dgamma_final", _f32p), ("layers", ctypes.POINTER(_f32p))]
+
+
 def build(force: bool = False) -> str:
     """Compile liboracle.so with the committed Makefile."""
     if force or not os.path.exists(LIB_PATH):
@@ -85,6 +89,16 @@ def lib():
         L.orc_decode_step.argtypes = [ctypes.POINTER(OrcConfig), ctypes.POINTER(OrcWeights),
                                       ctypes.c_void_p, ctypes.c_uint32, _f32p]
         L.orc_num_threads.restype = ctypes.c_int
+        L.orc_forward_backward.argtypes = [ctypes.POINTER(OrcConfig), ctypes.POINTER(OrcWeights),
+                                           _u32p, _u32p, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                           ctypes.POINTER(OrcGrads), _f32p]
+        L.orc_forward_backward.restype = ctypes.c_int
+        L.orc_rmsnorm_backward_channel_first.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                                         sz, sz]
+        L.orc_silu_gate_backward.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, sz]
+        L.orc_sdpa_backward.argtypes = [ctypes.POINTER(OrcConfig), sz, _f32p, _f32p, _f32p, _f32p,
+                                        _f32p, _f32p, _f32p]
+        L.orc_rope_backward.argtypes = [ctypes.POINTER(OrcConfig), _f32p, sz]
         _lib = L
     return _lib
 
@@ -170,3 +184,34 @@ class KV:
         if best < 0:
             raise ValueError(f"orc_decode_step failed: {best}")
         return best, out
+
+
+class Grads:
+    """Zero-initialised fp32 gradient arrays shaped like Weights (reference
+    orientation, RSTK order); the oracle accumulates into them."""
+
+    def __init__(self, w: Weights):
+        self.embed = np.zeros_like(w.embed)
+        self.gamma_final = np.zeros_like(w.gamma_final)
+        self.layers = [[np.zeros_like(t) for t in lw] for lw in w.layers]
+        flat = [t for lw in self.layers for t in lw]
+        self._ptrs = (_f32p * len(flat))(*[fp(t) for t in flat])
+        self.c = OrcGrads(fp(self.embed), fp(self.gamma_final), self._ptrs)
+
+
+def forward_backward(cfg: OrcConfig, w: Weights, tokens: np.ndarray, targets: np.ndarray,
+                     grads: Grads | None = None, loss_scale: float = 1.0):
+    """Adds loss_scale x the gradient of each sequence's mean loss into grads
+    (new zero grads when None).  Returns (grads, mean_loss [B])."""
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+    if tokens.ndim == 1:
+        tokens = tokens[None, :]
+    B, S = tokens.shape
+    tg = np.ascontiguousarray(targets, dtype=np.uint32).reshape(B, S)
+    g = grads if grads is not None else Grads(w)
+    ml = np.zeros((B,), np.float32)
+    rc = lib().orc_forward_backward(ctypes.byref(cfg), ctypes.byref(w.c), up(tokens), up(tg), B, S,
+                                    float(loss_scale), ctypes.byref(g.c), fp(ml))
+    if rc != 0:
+        raise ValueError(f"orc_forward_backward failed: {rc}")
+    return g, ml

@@ -15,6 +15,11 @@
 //   layer.rs:4409-4624        layer::forward orchestration (alpha = 1/sqrt(2L))
 //   layer.rs:1556-1567        random_vec LCG
 //   full_model.rs:915-991,1603-1660  forward / forward_losses
+//   full_model.rs:592-702     backward_ws (CE grad, tied-embedding grads, final norm)
+//   layer.rs:7037-7407        layer::backward_into, accumulate_dw, rope_backward_inplace
+//   cpu/rmsnorm.rs:185-240    rmsnorm::backward_channel_first
+//   cpu/embedding.rs:34-44    embedding::backward_channel_first
+//   kernels/sdpa_bwd.rs:44-300    sdpa backward graphs (probs, dP, dS, dQ, dK, dV)
 #include "oracle.h"
 
 #include <cmath>
@@ -161,12 +166,18 @@ inline float rope_theta(size_t p, size_t i, size_t hd, float base) {
     return (float)p / std::pow(base, 2.0f * (float)i / (float)hd);
 }
 
+// Activations one layer keeps for its backward pass (the ForwardCache of
+// layer.rs:79-126), token-major [n, *].
+struct LayerCache {
+    std::vector<float> x, xn, rms1, q, k, v, attn, x2, x2n, rms2, h1, h3, gate;
+};
+
 // One layer over n token-major rows at absolute positions p0..p0+n-1.
 // kc/vc: [ctx, D] token-major caches; positions p0..p0+n-1 are written, and
 // attention runs over keys 0..p0+n-1 with the additive -65504 causal mask of
 // kernels/sdpa_fwd.rs:41-51 (masked keys contribute exp(-65504 - max) = 0).
 void layer_rows(const orc_config* cfg, const float* const* lw, float* x, size_t n, size_t p0,
-                float* kc, float* vc) {
+                float* kc, float* vc, LayerCache* cache = nullptr) {
     const size_t D = cfg->dim, F = cfg->hidden, H = cfg->heads, hd = cfg->head_dim;
     const float alpha = 1.0f / std::sqrt(2.0f * (float)cfg->nlayers);   // layer.rs:4640
     const float scale = 1.0f / std::sqrt((float)hd);                    // sdpa_fwd.rs:70
@@ -174,8 +185,9 @@ void layer_rows(const orc_config* cfg, const float* const* lw, float* x, size_t 
     const float* wo = lw[3]; const float* w1 = lw[4]; const float* w3 = lw[5];
     const float* w2 = lw[6]; const float* g1 = lw[7]; const float* g2 = lw[8];
 
-    std::vector<float> xn(n * D), q(n * D, 0.f), k(n * D, 0.f), v(n * D, 0.f);
-    rmsnorm_rows(x, g1, xn.data(), nullptr, n, D, cfg->rms_eps);
+    std::vector<float> xn(n * D), q(n * D, 0.f), k(n * D, 0.f), v(n * D, 0.f), rms1(n);
+    if (cache) cache->x.assign(x, x + n * D);
+    rmsnorm_rows(x, g1, xn.data(), rms1.data(), n, D, cfg->rms_eps);
     // Q/K/V = xn^T W  (sdpa_fwd.rs:115-117)
     gemm_nn(n, D, D, xn.data(), D, wq, D, q.data(), D);
     gemm_nn(n, D, D, xn.data(), D, wk, D, k.data(), D);
@@ -234,13 +246,19 @@ void layer_rows(const orc_config* cfg, const float* const* lw, float* x, size_t 
     std::vector<float> o(n * D, 0.f);
     gemm_nn(n, D, D, attn.data(), D, wo, D, o.data(), D);
     for (size_t i = 0; i < n * D; ++i) x[i] = o[i] * alpha + x[i];
+    if (cache) {
+        cache->xn = xn; cache->rms1 = rms1; cache->q = q; cache->k = k; cache->v = v;
+        cache->attn = attn; cache->x2.assign(x, x + n * D);
+    }
     // FFN (ffn_fused.rs:22-160): h1 = x2n W1, h3 = x2n W3, gate = silu(h1)*h3,
     // f = gate W2^T, x_next = f*alpha + x2.
-    std::vector<float> x2n(n * D), h1(n * F, 0.f), h3(n * F, 0.f);
-    rmsnorm_rows(x, g2, x2n.data(), nullptr, n, D, cfg->rms_eps);
+    std::vector<float> x2n(n * D), h1(n * F, 0.f), h3(n * F, 0.f), rms2(n);
+    rmsnorm_rows(x, g2, x2n.data(), rms2.data(), n, D, cfg->rms_eps);
     gemm_nn(n, F, D, x2n.data(), D, w1, F, h1.data(), F);
     gemm_nn(n, F, D, x2n.data(), D, w3, F, h3.data(), F);
+    if (cache) { cache->x2n = x2n; cache->rms2 = rms2; cache->h1 = h1; cache->h3 = h3; }
     orc_silu_gate(h1.data(), h3.data(), h1.data(), n * F);
+    if (cache) cache->gate = h1;
     std::vector<float> f(n * D, 0.f);
     gemm_nt(n, D, F, h1.data(), F, w2, F, f.data(), D);
     for (size_t i = 0; i < n * D; ++i) x[i] = f[i] * alpha + x[i];
@@ -259,6 +277,184 @@ void tail_logits(const orc_config* cfg, const orc_weights* w, const float* x, si
         const float c = cfg->softcap, ic = 1.0f / c;
         for (size_t i = 0; i < n * V; ++i) logits[i] = std::tanh(logits[i] * ic) * c;
     }
+}
+
+// C[M,N] += A[K,M]^T B[K,N] (accumulate_dw -> vdsp::sgemm_at, layer.rs:7368-7370,
+// with token-major operands): transposed copies, then the dot-product kernel.
+void gemm_tn(size_t M, size_t N, size_t K, const float* A, size_t lda, const float* B, size_t ldb,
+             float* C, size_t ldc) {
+    std::vector<float> at(M * K), bt(N * K);
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < M; ++i)
+        for (size_t k = 0; k < K; ++k) at[i * K + k] = A[k * lda + i];
+#pragma omp parallel for schedule(static)
+    for (size_t j = 0; j < N; ++j)
+        for (size_t k = 0; k < K; ++k) bt[j * K + k] = B[k * ldb + j];
+    gemm_nt(M, N, K, at.data(), K, bt.data(), K, C, ldc);
+}
+
+// rmsnorm::backward_channel_first (cpu/rmsnorm.rs:185-240) on token-major
+// rows, same arithmetic: x_hat = x * r; dgamma[d] += sum_s dy * x_hat (in
+// position order); dot[s] = (sum_d (dy * g) * x_hat, channel order) / dim;
+// dx = r * (dy * g - x_hat * dot).
+void rmsnorm_bwd_rows(const float* dy, const float* x, const float* g, const float* rms_inv, float* dx,
+                      float* dgamma, size_t rows, size_t dim) {
+    const float inv_dim = 1.0f / (float)dim;
+    std::vector<float> dot(rows);
+#pragma omp parallel for schedule(static)
+    for (size_t s = 0; s < rows; ++s) {
+        float acc = 0.f;
+        for (size_t d = 0; d < dim; ++d) acc += dy[s * dim + d] * g[d] * (x[s * dim + d] * rms_inv[s]);
+        dot[s] = acc * inv_dim;
+    }
+#pragma omp parallel for schedule(static)
+    for (size_t d = 0; d < dim; ++d) {
+        float acc = 0.f;
+        for (size_t s = 0; s < rows; ++s) acc += dy[s * dim + d] * (x[s * dim + d] * rms_inv[s]);
+        dgamma[d] += acc;
+    }
+#pragma omp parallel for schedule(static)
+    for (size_t s = 0; s < rows; ++s)
+        for (size_t d = 0; d < dim; ++d) {
+            const float xh = x[s * dim + d] * rms_inv[s];
+            dx[s * dim + d] = rms_inv[s] * (dy[s * dim + d] * g[d] - xh * dot[s]);
+        }
+}
+
+// SiLU-gate backward loop of layer::backward_into (layer.rs:7083-7104):
+// sig = 1/(1 + exp(-h1)); dh3 = dg * h1 * sig; dh1 = dg * h3 * sig * (1 + h1 * (1 - sig)).
+void silu_gate_bwd(const float* dg, const float* h1, const float* h3, float* dh1, float* dh3, size_t n) {
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n; ++i) {
+        const float sig = 1.0f / (1.0f + std::exp(-h1[i]));
+        const float silu_val = h1[i] * sig;
+        const float deriv = sig * (1.0f + h1[i] * (1.0f - sig));
+        dh3[i] = dg[i] * silu_val;
+        dh1[i] = dg[i] * h3[i] * deriv;
+    }
+}
+
+// sdpa_bwd graphs (kernels/sdpa_bwd.rs:44-300) over token-major q, k, v, da
+// [n, D] (q, k after RoPE): probabilities recomputed as in the forward (scale
+// 1/sqrt(hd), additive -65504 causal mask, softmax); dV = P^T dA; dP = dA V^T;
+// dS = P * (dP - rowsum(P * dP)) * scale; dQ = dS K; dK = dS^T Q.  Keys above
+// the query have P = exp(-65504 + ...) = 0 exactly, so they are skipped.
+void sdpa_bwd_rows(const orc_config* cfg, size_t n, const float* q, const float* k, const float* v,
+                   const float* da, float* dq, float* dk, float* dv) {
+    const size_t D = cfg->dim, H = cfg->heads, hd = cfg->head_dim;
+    const float scale = 1.0f / std::sqrt((float)hd);
+    std::fill(dq, dq + n * D, 0.f);
+    std::fill(dk, dk + n * D, 0.f);
+    std::fill(dv, dv + n * D, 0.f);
+#pragma omp parallel for schedule(dynamic)
+    for (size_t h = 0; h < H; ++h) {
+        std::vector<float> p(n), dp(n);
+        for (size_t t = 0; t < n; ++t) {
+            const float* qr = q + t * D + h * hd;
+            const float* ar = da + t * D + h * hd;
+            float mx = -INFINITY;
+            for (size_t t2 = 0; t2 <= t; ++t2) {
+                const float* kr = k + t2 * D + h * hd;
+                float d = 0.f;
+                for (size_t i = 0; i < hd; ++i) d += qr[i] * kr[i];
+                p[t2] = d * scale;
+                mx = std::max(mx, p[t2]);
+            }
+            float sum = 0.f;
+            for (size_t t2 = 0; t2 <= t; ++t2) { p[t2] = std::exp(p[t2] - mx); sum += p[t2]; }
+            const float inv = 1.0f / sum;
+            float pdp = 0.f;
+            for (size_t t2 = 0; t2 <= t; ++t2) {
+                p[t2] *= inv;
+                const float* vr = v + t2 * D + h * hd;
+                float d = 0.f;
+                for (size_t i = 0; i < hd; ++i) d += ar[i] * vr[i];
+                dp[t2] = d;
+                pdp += p[t2] * d;
+            }
+            float* dqr = dq + t * D + h * hd;
+            for (size_t t2 = 0; t2 <= t; ++t2) {
+                const float ds = p[t2] * (dp[t2] - pdp) * scale;
+                const float* kr = k + t2 * D + h * hd;
+                float* dkr = dk + t2 * D + h * hd;
+                float* dvr = dv + t2 * D + h * hd;
+                for (size_t i = 0; i < hd; ++i) {
+                    dqr[i] += ds * kr[i];
+                    dkr[i] += ds * qr[i];
+                    dvr[i] += p[t2] * ar[i];
+                }
+            }
+        }
+    }
+}
+
+// rope_backward_inplace (layer.rs:7389-7407): the inverse rotation,
+// d[2i] = c*d0 + s*d1, d[2i+1] = -s*d0 + c*d1, rows at positions 0..n-1.
+void rope_bwd_rows(const orc_config* cfg, float* dx, size_t n) {
+    const size_t D = cfg->dim, H = cfg->heads, hd = cfg->head_dim;
+#pragma omp parallel for schedule(static)
+    for (size_t t = 0; t < n; ++t)
+        for (size_t h = 0; h < H; ++h)
+            for (size_t i = 0; i < hd / 2; ++i) {
+                const float th = rope_theta(t, i, hd, cfg->rope_base);
+                const float c = std::cos(th), sn = std::sin(th);
+                float* r = dx + t * D + h * hd + 2 * i;
+                const float d0 = r[0], d1 = r[1];
+                r[0] = c * d0 + sn * d1;
+                r[1] = -sn * d0 + c * d1;
+            }
+}
+
+// layer::backward_into (layer.rs:7037-7366) for one sequence, token-major:
+// dy [n, D] -> dx_out [n, D]; gradients accumulate into lg[9] (RSTK order).
+void layer_backward_rows(const orc_config* cfg, const float* const* lw, const LayerCache& c,
+                         const float* dy, float* const* lg, float* dx_out, size_t n) {
+    const size_t D = cfg->dim, F = cfg->hidden;
+    const float alpha = 1.0f / std::sqrt(2.0f * (float)cfg->nlayers);  // layer.rs:7054
+    const float* wq = lw[0]; const float* wk = lw[1]; const float* wv = lw[2];
+    const float* wo = lw[3]; const float* w1 = lw[4]; const float* w3 = lw[5];
+    const float* w2 = lw[6]; const float* g1 = lw[7]; const float* g2 = lw[8];
+    // 1-3: dffn = alpha dy; dsilu = dffn W2 (W2 [D, F] out x in); SiLU-gate backward
+    std::vector<float> dffn(n * D), dg(n * F, 0.f), dh1(n * F), dh3(n * F);
+    for (size_t i = 0; i < n * D; ++i) dffn[i] = dy[i] * alpha;
+    gemm_nn(n, F, D, dffn.data(), D, w2, F, dg.data(), F);
+    silu_gate_bwd(dg.data(), c.h1.data(), c.h3.data(), dh1.data(), dh3.data(), n * F);
+    // 4-5: dx_ffn = dh1 W1^T + dh3 W3^T; dW3 += x2n^T dh3
+    std::vector<float> dxf(n * D, 0.f);
+    gemm_nt(n, D, F, dh1.data(), F, w1, F, dxf.data(), D);
+    gemm_nt(n, D, F, dh3.data(), F, w3, F, dxf.data(), D);
+    gemm_tn(D, F, n, c.x2n.data(), D, dh3.data(), F, lg[5], F);
+    // 6: RMSNorm2 backward, dx2 += dy
+    std::vector<float> dx2(n * D);
+    rmsnorm_bwd_rows(dxf.data(), c.x2.data(), g2, c.rms2.data(), dx2.data(), lg[8], n, D);
+    for (size_t i = 0; i < n * D; ++i) dx2[i] = dx2[i] + dy[i];
+    // 7: da = (alpha dx2) Wo^T (Wo [q_dim, D] in x out)
+    std::vector<float> dx2s(n * D), da(n * D, 0.f);
+    for (size_t i = 0; i < n * D; ++i) dx2s[i] = dx2[i] * alpha;
+    gemm_nt(n, D, D, dx2s.data(), D, wo, D, da.data(), D);
+    // 9: dWo += attn^T dx2s; dW2 += dffn^T gate
+    gemm_tn(D, D, n, c.attn.data(), D, dx2s.data(), D, lg[3], D);
+    gemm_tn(D, F, n, dffn.data(), D, c.gate.data(), F, lg[6], F);
+    // 10: attention backward; dW1 += x2n^T dh1
+    std::vector<float> dq(n * D), dk(n * D), dv(n * D);
+    sdpa_bwd_rows(cfg, n, c.q.data(), c.k.data(), c.v.data(), da.data(), dq.data(), dk.data(), dv.data());
+    gemm_tn(D, F, n, c.x2n.data(), D, dh1.data(), F, lg[4], F);
+    // 11: RoPE backward on dq, dk
+    rope_bwd_rows(cfg, dq.data(), n);
+    rope_bwd_rows(cfg, dk.data(), n);
+    // 13: dx_attn = dq Wq^T; dx_kv = dk Wk^T + dv Wv^T; dWq/dWk/dWv += xn^T d{q,k,v}
+    std::vector<float> dxa(n * D, 0.f), dxkv(n * D, 0.f);
+    gemm_nt(n, D, D, dq.data(), D, wq, D, dxa.data(), D);
+    gemm_nt(n, D, D, dk.data(), D, wk, D, dxkv.data(), D);
+    gemm_nt(n, D, D, dv.data(), D, wv, D, dxkv.data(), D);
+    gemm_tn(D, D, n, c.xn.data(), D, dq.data(), D, lg[0], D);
+    gemm_tn(D, D, n, c.xn.data(), D, dk.data(), D, lg[1], D);
+    gemm_tn(D, D, n, c.xn.data(), D, dv.data(), D, lg[2], D);
+    // 15-16: RMSNorm1 backward of the merged input gradient; dx = dx_rms1 + dx2
+    std::vector<float> dxm(n * D), dxr(n * D);
+    for (size_t i = 0; i < n * D; ++i) dxm[i] = dxa[i] + dxkv[i];
+    rmsnorm_bwd_rows(dxm.data(), c.x.data(), g1, c.rms1.data(), dxr.data(), lg[7], n, D);
+    for (size_t i = 0; i < n * D; ++i) dx_out[i] = dxr[i] + dx2[i];
 }
 
 }  // namespace
@@ -485,6 +681,86 @@ int orc_forward(const orc_config* cfg, const orc_weights* w, const uint32_t* tok
     }
     return 0;
 }
+
+// full_model::forward + backward_ws (full_model.rs:915-991, 592-702) for
+// `batch` independent sequences; every gradient accumulates (+=).
+int orc_forward_backward(const orc_config* cfg, const orc_weights* w, const uint32_t* tokens,
+                         const uint32_t* targets, int batch, int seq, float loss_scale,
+                         const orc_grads* g, float* mean_loss_out) {
+    if (!cfg || !w || !g || !tokens || !targets || batch <= 0 || seq <= 0) return -1;
+    const size_t D = cfg->dim, V = cfg->vocab, S = seq;
+    const int L = cfg->nlayers;
+    for (size_t i = 0; i < (size_t)batch * S; ++i)
+        if (tokens[i] >= V || targets[i] >= V) return -2;
+    std::vector<float> x(S * D), kc(S * D), vc(S * D), xf(S * D), rmsf(S), logits(S * V), t(S * V);
+    std::vector<float> dl(S * V), dxf(S * D), dy(S * D), dxo(S * D);
+    std::vector<LayerCache> caches(L);
+    for (int b = 0; b < batch; ++b) {
+        const uint32_t* tk = tokens + (size_t)b * S;
+        const uint32_t* tg = targets + (size_t)b * S;
+        orc_embedding_forward(w->embed, D, tk, S, x.data());
+        for (int l = 0; l < L; ++l)
+            layer_rows(cfg, w->layers + 9 * l, x.data(), S, 0, kc.data(), vc.data(), &caches[l]);
+        // finalize_logits_and_loss (full_model.rs:283-329); t = tanh(z / c) when softcapped
+        rmsnorm_rows(x.data(), w->gamma_final, xf.data(), rmsf.data(), S, D, cfg->rms_eps);
+        std::fill(logits.begin(), logits.end(), 0.f);
+        gemm_nt(S, V, D, xf.data(), D, w->embed, D, logits.data(), V);
+        const bool cap = cfg->softcap > 0.f;
+        if (cap) {
+            const float c = cfg->softcap, ic = 1.0f / c;
+            for (size_t i = 0; i < S * V; ++i) { t[i] = std::tanh(logits[i] * ic); logits[i] = t[i] * c; }
+        }
+        std::vector<float> per(S);
+#pragma omp parallel for schedule(static)
+        for (size_t s = 0; s < S; ++s)
+            per[s] = orc_cross_entropy_forward_backward_batch(logits.data() + s * V, tg + s, 1, V,
+                                                              dl.data() + s * V, 1.0f / (float)S);
+        float total = 0.f;
+        for (size_t s = 0; s < S; ++s) total += per[s];
+        if (mean_loss_out) mean_loss_out[b] = total / (float)S;
+        // backward_ws steps 1-2: dl = dlogits * loss_scale (* (1 - t^2) when softcapped)
+        for (size_t i = 0; i < S * V; ++i)
+            dl[i] = cap ? dl[i] * loss_scale * (1.0f - t[i] * t[i]) : dl[i] * loss_scale;
+        // 3a: dx_final = dl E; 3b: dembed += dl^T x_final
+        std::fill(dxf.begin(), dxf.end(), 0.f);
+        gemm_nn(S, D, V, dl.data(), V, w->embed, D, dxf.data(), D);
+        gemm_tn(V, D, S, dl.data(), V, xf.data(), D, g->dembed, D);
+        // 4: final RMSNorm backward (x_prenorm = x after the last layer)
+        rmsnorm_bwd_rows(dxf.data(), x.data(), w->gamma_final, rmsf.data(), dy.data(), g->dgamma_final, S, D);
+        // 5: layers in reverse
+        for (int l = L - 1; l >= 0; --l) {
+            layer_backward_rows(cfg, w->layers + 9 * l, caches[l], dy.data(), g->layers + 9 * l, dxo.data(), S);
+            std::swap(dy, dxo);
+        }
+        // 6: embedding::backward_channel_first (cpu/embedding.rs:34-44), positions in order
+        for (size_t s = 0; s < S; ++s)
+            for (size_t d = 0; d < D; ++d) g->dembed[(size_t)tk[s] * D + d] += dy[s * D + d];
+    }
+    return 0;
+}
+
+void orc_rmsnorm_backward_channel_first(const float* dy, const float* x, const float* gamma,
+                                        const float* rms_inv, float* dx, float* dgamma, size_t dim,
+                                        size_t seq) {
+    // channel-first [dim, seq] in and out, through the token-major routine
+    std::vector<float> dyt(seq * dim), xt(seq * dim), dxt(seq * dim);
+    orc_mtrans(dy, seq, dyt.data(), dim, dim, seq);
+    orc_mtrans(x, seq, xt.data(), dim, dim, seq);
+    rmsnorm_bwd_rows(dyt.data(), xt.data(), gamma, rms_inv, dxt.data(), dgamma, seq, dim);
+    orc_mtrans(dxt.data(), dim, dx, seq, seq, dim);
+}
+
+void orc_silu_gate_backward(const float* dgate, const float* h1, const float* h3, float* dh1,
+                            float* dh3, size_t n) {
+    silu_gate_bwd(dgate, h1, h3, dh1, dh3, n);
+}
+
+void orc_sdpa_backward(const orc_config* cfg, size_t seq, const float* q, const float* k,
+                       const float* v, const float* da, float* dq, float* dk, float* dv) {
+    sdpa_bwd_rows(cfg, seq, q, k, v, da, dq, dk, dv);
+}
+
+void orc_rope_backward(const orc_config* cfg, float* dx, size_t seq) { rope_bwd_rows(cfg, dx, seq); }
 
 orc_kv* orc_kv_create(const orc_config* cfg, int max_ctx) {
     if (!cfg || max_ctx <= 0) return nullptr;

@@ -33,6 +33,15 @@
  *   orc_forward (body)        layer = independent numpy float64 restatement on tiny shapes;
  *                             FFN/attention branch linearity in Wo and W2
  *   orc_decode_*              decode logits at position p == orc_forward logits at p
+ *   orc_forward_backward      every gradient vs float64 autograd of an independent
+ *                             torch restatement of the forward (tiny shapes, softcap on
+ *                             and off, loss_scale); accumulation (+=) across calls
+ *   orc_rmsnorm_backward_*, orc_silu_gate_backward
+ *                             reference numerical-gradient KATs (cpu/rmsnorm.rs:278-316,
+ *                             cpu/silu.rs:68-90) + float64 autograd
+ *   orc_sdpa_backward, orc_rope_backward
+ *                             float64 autograd of the textbook forward; RoPE backward
+ *                             is the inverse rotation (round trip to identity)
  *
  * Parity unpinned: the ANE's bit-level fp16 numerics (accumulation order, its
  * softmax) that the reference executes inside the un-vendored `ane` crate; no
@@ -109,6 +118,35 @@ void orc_layer_forward(const orc_config* cfg, size_t seq, const float* const* lw
 int orc_forward(const orc_config* cfg, const orc_weights* w, const uint32_t* tokens,
                 const uint32_t* targets, int batch, int seq, float* logits_out,
                 float* token_losses_out, float* mean_loss_out);
+
+/* ---- backward (the training pass) ---- */
+/* ModelGrads (full_model.rs) + LayerGrads: the shapes and orientation of
+ * orc_weights, every array accumulated into (+=), as the reference does. */
+typedef struct {
+    float* dembed;       /* [V, D] */
+    float* dgamma_final; /* [D]    */
+    float* const* layers; /* layers[9*l + j], RSTK order as in orc_weights */
+} orc_grads;
+/* full_model::forward then backward_ws (full_model.rs:915-991, 592-702;
+ * layer::backward_into, layer.rs:7037-7366) for `batch` independent
+ * sequences; each adds loss_scale x its gradient of its mean loss into g.
+ * mean_loss_out nullable [B].  Returns 0 on success. */
+int orc_forward_backward(const orc_config* cfg, const orc_weights* w, const uint32_t* tokens,
+                         const uint32_t* targets, int batch, int seq, float loss_scale,
+                         const orc_grads* g, float* mean_loss_out);
+/* rmsnorm::backward_channel_first (cpu/rmsnorm.rs:185-240): [dim, seq]. */
+void orc_rmsnorm_backward_channel_first(const float* dy, const float* x, const float* gamma,
+                                        const float* rms_inv, float* dx, float* dgamma, size_t dim,
+                                        size_t seq);
+/* SiLU-gate backward of layer::backward_into (layer.rs:7083-7104). */
+void orc_silu_gate_backward(const float* dgate, const float* h1, const float* h3, float* dh1,
+                            float* dh3, size_t n);
+/* sdpa_bwd graphs (kernels/sdpa_bwd.rs:44-300), token-major [seq, D] (q, k
+ * after RoPE); dq, dk, dv are overwritten. */
+void orc_sdpa_backward(const orc_config* cfg, size_t seq, const float* q, const float* k,
+                       const float* v, const float* da, float* dq, float* dk, float* dv);
+/* rope_backward_inplace (layer.rs:7389-7407), token-major [seq, D]. */
+void orc_rope_backward(const orc_config* cfg, float* dx, size_t seq);
 
 /* ---- single-token decode with a KV cache (no reference implementation;
  *      contract: logits at step p equal the forward's logits at position p) ---- */
