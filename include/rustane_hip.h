@@ -105,6 +105,23 @@ int rh_forward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int
 int rh_forward_dev(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch,
                    int seq, float* logits_out, float* token_losses_out, float* mean_loss_out);
 
+/* Training pass: full_model::forward then full_model::backward / backward_ws
+ * (full_model.rs:592-702, 915-991; layer::backward_into, layer.rs:7037-7366)
+ * for `batch` independent sequences of `seq` tokens.  Adds loss_scale times
+ * the gradient of each sequence's mean loss to the context's fp32 gradients
+ * (they accumulate across calls, as the reference's ModelGrads do; see
+ * rh_zero_grads).  The first call allocates the gradients (the parameter
+ * count in fp32), transposed fp16 weight copies and per-layer activation
+ * caches.  mean_loss_out nullable [batch].  Needs hidden % 64 == 0. */
+int rh_forward_backward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
+                        float loss_scale, float* mean_loss_out);
+/* ModelGrads::zero_out: sets every gradient to 0. */
+int rh_zero_grads(rh_ctx* ctx);
+/* Copies the gradients to host fp32 arrays in the orientation and RSTK order
+ * of rh_load_weights_f32 (every pointer nullable; layer_grads[9*l + j] may be
+ * NULL to skip a tensor).  RH_ESTATE before the first rh_forward_backward. */
+int rh_read_grads_f32(rh_ctx* ctx, float* dembed, float* dgamma_final, float* const* layer_grads);
+
 /* Fills the KV cache from `batch` prompts of `len` tokens (planned
  * metal-decode path, crates/metal-decode/src/lib.rs:1-8) and sets the decode
  * position to len.  next_tok_out (nullable [batch]) receives the argmax of

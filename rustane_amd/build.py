@@ -18,7 +18,8 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librustane_hip.so")
 
-SOURCES = ["rh_gemm.hip", "rh_attn.hip", "rh_gemv.hip", "rh_rowops.hip", "rh_runtime.cpp", "rh_data.cpp", "rh_sched.cpp"]
+SOURCES = ["rh_gemm.hip", "rh_attn.hip", "rh_attn_bwd.hip", "rh_gemv.hip", "rh_rowops.hip", "rh_trainops.hip",
+           "rh_runtime.cpp", "rh_train.cpp", "rh_data.cpp", "rh_sched.cpp"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CFLAGS = [
@@ -32,7 +33,8 @@ CFLAGS = [
 # every key block; with accumulators in AGPRs each rescale costs two copies
 # per register, so its MFMAs take the VGPR form (the GEMMs keep AGPRs: their
 # accumulators exceed the 256 architectural VGPRs).
-FILE_FLAGS = {"rh_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
+FILE_FLAGS = {"rh_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+              "rh_attn_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
 
 
 def _compile(src: str) -> str:

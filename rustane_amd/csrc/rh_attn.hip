@@ -31,8 +31,8 @@ template <int HD, int PF>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict__ Q,
                                                            const f16* __restrict__ Kc,
                                                            const f16* __restrict__ Vc,
-                                                           f16* __restrict__ out, int H, int S,
-                                                           int ctx, float scale_log2) {
+                                                           f16* __restrict__ out, float* __restrict__ lse,
+                                                           int H, int S, int ctx, float scale_log2) {
     constexpr int KB = 64;             // keys per block
     constexpr int LDK = HD + 8;        // padded K row (halfs)
     constexpr int LDV = KB + 8;        // padded V^T row (halfs)
@@ -214,6 +214,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
     float lt = l_run + __shfl_xor(l_run, 16, RH_WAVE);
     lt += __shfl_xor(lt, 32, RH_WAVE);
     if (qi < S) {
+        // Log-sum-exp of the scaled scores in the log2 domain, for the
+        // backward pass: P[q][k] = exp2(score * scale_log2 - lse[q]).
+        if (lse && g == 0) lse[bh * S + qi] = m_run + log2f(lt);
         // token-major [B*S][H*HD] in fragment order (the Wo GEMM's operand layout)
         const float inv = 1.0f / lt;
         const int row = b * S + qi;
@@ -345,14 +348,14 @@ __global__ void attn_merge_kernel(const float* part_m, const float* part_l, cons
 }  // namespace
 
 hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* out, int B, int H,
-                               int S, int hd, int ctx, hipStream_t st) {
+                               int S, int hd, int ctx, hipStream_t st, float* lse) {
     const dim3 grid((S + 63) / 64, H, B);
     const float sl2 = (1.0f / sqrtf((float)hd)) * LOG2E;
     constexpr int PF = 1;  // deeper register prefetch measured no faster
     if (hd == 128)
-        hipLaunchKernelGGL((attn_prefill_kernel<128, PF>), grid, dim3(256), 0, st, q, k, v, out, H, S, ctx, sl2);
+        hipLaunchKernelGGL((attn_prefill_kernel<128, PF>), grid, dim3(256), 0, st, q, k, v, out, lse, H, S, ctx, sl2);
     else if (hd == 64)
-        hipLaunchKernelGGL((attn_prefill_kernel<64, PF>), grid, dim3(256), 0, st, q, k, v, out, H, S, ctx, sl2);
+        hipLaunchKernelGGL((attn_prefill_kernel<64, PF>), grid, dim3(256), 0, st, q, k, v, out, lse, H, S, ctx, sl2);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

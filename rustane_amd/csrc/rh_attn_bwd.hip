@@ -1,0 +1,279 @@
+// rh_attn_bwd.hip -- causal attention backward (the training pass).
+//
+// Semantics of the sdpaBwd1/sdpaBwd2 graphs (kernels/sdpa_bwd.rs:44-300):
+// probabilities recomputed from q_rope, k_rope (scale 1/sqrt(hd), causal
+// mask), dV = P^T dO, dP = dO V^T, dS = P * (dP - D) with D[q] = sum_k
+// P dP = sum_d dO[q][d] O[q][d], dQ = scale dS K, dK = scale dS^T Q.  The
+// reference materialises the S x S probabilities on the ANE; here they are
+// recomputed tile by tile from the forward's per-query log-sum-exp, as in a
+// flash-attention backward, and nothing S x S touches HBM.
+//
+// Two deterministic kernels (no atomics):
+//   attn_bwd_dq_kernel    a block owns 64 queries of one (sequence, head), 4
+//                         waves x 16 queries, and walks the key blocks up to
+//                         the diagonal: S^T = K Q^T, dP^T = V dO^T, then
+//                         dQ^T += K^T dS^T.  Every lane owns one query column
+//                         (the forward kernel's arrangement), so the row
+//                         statistics (lse, D) are lane scalars.
+//   attn_bwd_dkdv_kernel  a block owns 64 keys, 4 waves x 16 keys, and walks
+//                         the query blocks from the diagonal on: S = Q K^T,
+//                         dP = dO V^T, then dV^T += dO^T P and dK^T += Q^T dS.
+//                         Every lane owns one key column.
+// The row permutation of the first MFMA's A operand (tile row r reads row
+// 32c + 8(r/4) + 4u + r%4 of a 32-row chunk) makes the output tile's lane
+// group g hold rows 32c + 8g + 0..7, which is exactly the k layout of the
+// second MFMA's B operand, so P and dS go from accumulators to operands
+// without data movement.  Operands needed transposed (K^T, Q^T, dO^T) are
+// written transposed into LDS when the tile is staged.
+#include "rh_device.h"
+#include "rh_kernels.h"
+
+namespace rh {
+namespace {
+
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Stages rows r0..r0+63 (clamped to S - 1) of a [S][HD] fp16 matrix into
+// LDS: row-major (ld HD + 8) when rm is set, and transposed [HD][64] (ld 72)
+// when tr is set, two rows per 32-bit LDS store.
+template <int HD>
+__device__ __forceinline__ void stage_rows(const f16* __restrict__ src, int r0, int S, f16* rm, f16* tr) {
+    constexpr int LD = HD + 8, LT = 64 + 8;
+    const int tid = threadIdx.x;
+    if (rm) {
+#pragma unroll
+        for (int p = 0; p < 64 * HD / 8 / 256; ++p) {
+            const int c = tid + 256 * p, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+            *(f16x8*)&rm[row * LD + col] = *(const f16x8*)(src + (size_t)min(r0 + row, S - 1) * HD + col);
+        }
+    }
+    if (tr) {
+#pragma unroll
+        for (int p = 0; p < 32 * (HD / 8) / 256; ++p) {
+            const int u = tid + 256 * p, rp = u & 31, col = (u >> 5) * 8;
+            const f16x8 a = *(const f16x8*)(src + (size_t)min(r0 + 2 * rp, S - 1) * HD + col);
+            const f16x8 b = *(const f16x8*)(src + (size_t)min(r0 + 2 * rp + 1, S - 1) * HD + col);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) *(f16x2*)&tr[(col + e) * LT + 2 * rp] = f16x2{a[e], b[e]};
+        }
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
+                                                          const f16* __restrict__ V, const f16* __restrict__ dO,
+                                                          const float* __restrict__ lse,
+                                                          const float* __restrict__ Drow, float* __restrict__ dqkv,
+                                                          int H, int S, float scale_log2, float scale) {
+    constexpr int KB = 64, LD = HD + 8, LT = KB + 8, NKK = HD / 32, NHT = HD / 16;
+    __shared__ __attribute__((aligned(16))) f16 sK[KB * LD];
+    __shared__ __attribute__((aligned(16))) f16 sV[KB * LD];
+    __shared__ __attribute__((aligned(16))) f16 sKt[HD * LT];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r = lane & 15;
+    const int nqt = (S + 63) / 64;
+    const int qt = nqt - 1 - (int)blockIdx.x;  // longest rows first
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int q0 = qt * 64, qi = q0 + w * 16 + r, qrow = min(qi, S - 1);
+    const size_t bh = (size_t)b * H + h;
+    const f16* Kb = K + bh * S * HD;
+    const f16* Vb = V + bh * S * HD;
+    f16x8 qf[NKK], df[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+        qf[kk] = *(const f16x8*)(Q + (bh * S + qrow) * HD + 32 * kk + 8 * g);
+        df[kk] = *(const f16x8*)(dO + (bh * S + qrow) * HD + 32 * kk + 8 * g);
+    }
+    const float L = lse[bh * S + qrow], Dq = Drow[bh * S + qrow];
+    f32x4 acc[NHT];
+#pragma unroll
+    for (int j = 0; j < NHT; ++j) acc[j] = f32x4{};
+    const int nkb = (min(S, q0 + 64) + KB - 1) / KB;
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int k0 = kb * KB;
+        __syncthreads();
+        stage_rows<HD>(Kb, k0, S, sK, sKt);
+        stage_rows<HD>(Vb, k0, S, sV, nullptr);
+        __syncthreads();
+        // S^T and dP^T: chunk c (32 keys) x half u; lane group g then holds
+        // keys k0 + 32c + 8g + 4u + i in element [c][u][i].
+        f32x4 sc[2][2], dp[2][2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                sc[c][u] = f32x4{};
+                dp[c][u] = f32x4{};
+                const int krow = 32 * c + 8 * (r >> 2) + 4 * u + (r & 3);
+#pragma unroll
+                for (int kk = 0; kk < NKK; ++kk) {
+                    sc[c][u] = mfma16(*(const f16x8*)&sK[krow * LD + 32 * kk + 8 * g], qf[kk], sc[c][u]);
+                    dp[c][u] = mfma16(*(const f16x8*)&sV[krow * LD + 32 * kk + 8 * g], df[kk], dp[c][u]);
+                }
+            }
+        const int lim = qrow - k0 - 8 * g;  // key offsets above lim are masked (or past S)
+        f16x8 dsf[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const bool live = 32 * c + 4 * u + i <= lim;
+                    const float p = live ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[c][u][i], scale_log2, -L)) : 0.f;
+                    dsf[c][4 * u + i] = (f16)(p * (dp[c][u][i] - Dq));
+                }
+        // dQ^T[hd][q] += K^T[hd][keys] . dS^T[keys][q]
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int j = 0; j < NHT; ++j)
+                acc[j] = mfma16(*(const f16x8*)&sKt[(16 * j + r) * LT + 32 * c + 8 * g], dsf[c], acc[j]);
+    }
+    if (qi < S) {
+        float* dst = dqkv + (size_t)(b * S + qi) * (3 * H * HD) + h * HD + 4 * g;
+#pragma unroll
+        for (int j = 0; j < NHT; ++j) *(f32x4*)(dst + 16 * j) = acc[j] * scale;
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
+                                                            const f16* __restrict__ V, const f16* __restrict__ dO,
+                                                            const float* __restrict__ lse,
+                                                            const float* __restrict__ Drow,
+                                                            float* __restrict__ dqkv, int H, int S,
+                                                            float scale_log2, float scale) {
+    constexpr int QB = 64, LD = HD + 8, LT = QB + 8, NKK = HD / 32, NHT = HD / 16;
+    __shared__ __attribute__((aligned(16))) f16 sQ[QB * LD];
+    __shared__ __attribute__((aligned(16))) f16 sdO[QB * LD];
+    __shared__ __attribute__((aligned(16))) f16 sQt[HD * LT];
+    __shared__ __attribute__((aligned(16))) f16 sdOt[HD * LT];
+    __shared__ float sL[QB], sD[QB];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r = lane & 15;
+    const int kt = blockIdx.x;  // the first key blocks see the most queries: launched first
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int k0 = kt * 64, ki = k0 + w * 16 + r, krow = min(ki, S - 1);
+    const size_t bh = (size_t)b * H + h;
+    const f16* Qb = Q + bh * S * HD;
+    const f16* dOb = dO + bh * S * HD;
+    f16x8 kf[NKK], vf[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+        kf[kk] = *(const f16x8*)(K + (bh * S + krow) * HD + 32 * kk + 8 * g);
+        vf[kk] = *(const f16x8*)(V + (bh * S + krow) * HD + 32 * kk + 8 * g);
+    }
+    f32x4 dk[NHT], dv[NHT];
+#pragma unroll
+    for (int j = 0; j < NHT; ++j) dk[j] = dv[j] = f32x4{};
+    const int nqb = (S + QB - 1) / QB;
+    for (int qb = kt; qb < nqb; ++qb) {
+        const int q0 = qb * QB;
+        __syncthreads();
+        stage_rows<HD>(Qb, q0, S, sQ, sQt);
+        stage_rows<HD>(dOb, q0, S, sdO, sdOt);
+        if (tid < QB) {
+            const int q = min(q0 + tid, S - 1);
+            sL[tid] = lse[bh * S + q];
+            sD[tid] = Drow[bh * S + q];
+        }
+        __syncthreads();
+        // S and dP: chunk c (32 queries) x half u; lane group g then holds
+        // queries q0 + 32c + 8g + 4u + i in element [c][u][i].
+        f32x4 s[2][2], dp[2][2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                s[c][u] = f32x4{};
+                dp[c][u] = f32x4{};
+                const int qr = 32 * c + 8 * (r >> 2) + 4 * u + (r & 3);
+#pragma unroll
+                for (int kk = 0; kk < NKK; ++kk) {
+                    s[c][u] = mfma16(*(const f16x8*)&sQ[qr * LD + 32 * kk + 8 * g], kf[kk], s[c][u]);
+                    dp[c][u] = mfma16(*(const f16x8*)&sdO[qr * LD + 32 * kk + 8 * g], vf[kk], dp[c][u]);
+                }
+            }
+        f16x8 pf[2], dsf[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int qo = 32 * c + 8 * g + 4 * u + i, q = q0 + qo;
+                    const bool live = q >= ki && q < S;
+                    const float p = live ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[c][u][i], scale_log2, -sL[qo])) : 0.f;
+                    pf[c][4 * u + i] = (f16)p;
+                    dsf[c][4 * u + i] = (f16)(p * (dp[c][u][i] - sD[qo]));
+                }
+        // dV^T[hd][key] += dO^T[hd][q] . P[q][key];  dK^T += Q^T . dS
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int j = 0; j < NHT; ++j) {
+                dv[j] = mfma16(*(const f16x8*)&sdOt[(16 * j + r) * LT + 32 * c + 8 * g], pf[c], dv[j]);
+                dk[j] = mfma16(*(const f16x8*)&sQt[(16 * j + r) * LT + 32 * c + 8 * g], dsf[c], dk[j]);
+            }
+    }
+    if (ki < S) {
+        const int D = H * HD;
+        float* dst = dqkv + (size_t)(b * S + ki) * (3 * D) + h * HD + 4 * g;
+#pragma unroll
+        for (int j = 0; j < NHT; ++j) {
+            *(f32x4*)(dst + D + 16 * j) = dk[j] * scale;
+            *(f32x4*)(dst + 2 * D + 16 * j) = dv[j];
+        }
+    }
+}
+
+// dO [M, H*hd] fp32 (token-major GEMM output) -> fp16 [B][H][S][hd], and
+// D[b][h][s] = sum_d dO * O with O the forward's attention output (fragment
+// order).  One wave per (token, head); lane d covers dims d, d + 64.
+__global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const float* __restrict__ dOf, const f16* __restrict__ O,
+                                                            f16* __restrict__ dOh, float* __restrict__ Drow,
+                                                            int B, int H, int S, int HD) {
+    const int lane = threadIdx.x & 63;
+    const long long item = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= (long long)B * S * H) return;
+    const int h = (int)(item % H);
+    const long long m = item / H;  // token row b*S + s
+    const int b = (int)(m / S), s = (int)(m % S);
+    const int D = H * HD;
+    float acc = 0.f;
+    for (int d = lane; d < HD; d += 64) {
+        const float v = dOf[m * D + h * HD + d];
+        acc += v * (float)O[frag_off((int)m, h * HD + d, D)];
+        dOh[(((size_t)b * H + h) * S + s) * HD + d] = (f16)v;
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) Drow[((size_t)b * H + h) * S + s] = acc;
+}
+
+}  // namespace
+
+hipError_t launch_attn_backward(const f16* q, const f16* k, const f16* v, const f16* o, const float* dOf,
+                                const float* lse, f16* dOh, float* Drow, float* dqkv, int B, int H, int S, int hd,
+                                hipStream_t st) {
+    if (hd != 128 && hd != 64) return hipErrorInvalidValue;
+    const long long items = (long long)B * S * H;
+    hipLaunchKernelGGL(attn_bwd_prep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st, dOf, o, dOh, Drow,
+                       B, H, S, hd);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 grid((S + 63) / 64, H, B);
+    const float scale = 1.0f / sqrtf((float)hd), sl2 = scale * 1.4426950408889634f;
+    if (hd == 128) {
+        hipLaunchKernelGGL((attn_bwd_dq_kernel<128>), grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S,
+                           sl2, scale);
+        hipLaunchKernelGGL((attn_bwd_dkdv_kernel<128>), grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S,
+                           sl2, scale);
+    } else {
+        hipLaunchKernelGGL((attn_bwd_dq_kernel<64>), grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S,
+                           sl2, scale);
+        hipLaunchKernelGGL((attn_bwd_dkdv_kernel<64>), grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S,
+                           sl2, scale);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace rh

@@ -1,0 +1,159 @@
+// rh_ctx.h -- the context object and the host helpers shared by the
+// runtime's translation units (forward/decode runtime, training pass).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "../../include/rustane_hip.h"
+#include "rh_internal.h"
+#include "rh_kernels.h"
+
+namespace rhrt {
+
+struct Layer {
+    f16 *wqkv = nullptr, *wo = nullptr, *w13 = nullptr, *w2 = nullptr;
+    float *g1 = nullptr, *g2 = nullptr;
+};
+
+struct Prof {
+    bool on = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
+    double ms = 0;
+    int64_t n = 0;
+};
+
+struct TrainState;                 // rh_train.cpp
+void train_state_free(TrainState* t);  // host side only; device buffers are context allocations
+
+}  // namespace rhrt
+
+struct rh_ctx {
+    rh_config cfg{};
+    int device = 0, max_batch = 0, max_ctx = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    std::vector<void*> allocs;
+
+    f16* embed = nullptr;
+    float* gfinal = nullptr;
+    std::vector<rhrt::Layer> L;
+    float2* rope = nullptr;
+    int rope_len = 0;
+
+    // forward / prefill workspace (grow-only, sized for M = B*S rows)
+    int ws_M = 0;
+    float *x = nullptr, *logits = nullptr, *tok_loss = nullptr, *mean = nullptr;
+    f16 *xn = nullptr, *q = nullptr, *kbuf = nullptr, *vbuf = nullptr, *attn = nullptr, *gate = nullptr;
+    uint32_t *d_tok = nullptr, *d_tgt = nullptr;
+    size_t logits_rows = 0;
+    int* d_err = nullptr;
+
+    // KV cache [L][max_batch][H][max_ctx][hd]
+    f16 *kcache = nullptr, *vcache = nullptr;
+    size_t kv_layer = 0;
+
+    // decode (B <= 16)
+    float *dx = nullptr, *dlogits = nullptr, *pm = nullptr, *pl = nullptr, *po = nullptr;
+    f16 *dxn = nullptr, *dq = nullptr, *dattn = nullptr, *dgate = nullptr;
+    int* dstate = nullptr;
+    uint32_t *dtok = nullptr, *dout = nullptr, *dseq = nullptr;
+    float* dam_v = nullptr;  // [argmax blocks][16] argmax partials of the logits GEMV
+    int* dam_i = nullptr;
+    int dec_B = 0, host_pos = 0;
+    bool have_prefill = false;
+    bool use_graphs = true;
+    hipGraphExec_t dgraph = nullptr;
+    int dgraph_B = 0;
+    bool capturing = false;
+
+    float* staging = nullptr;
+    size_t staging_elems = 0;
+
+    // stream-K workspace of the prefill GEMMs (fp32 partial tiles)
+    float* sk_part = nullptr;
+    size_t sk_part_floats = 0;
+
+    rhrt::Prof prof[RH_K_NCLASSES];
+
+    // bumped whenever the weights change (derived copies are rebuilt lazily)
+    uint64_t wgen = 1;
+    // training state (rh_train.cpp), allocated by the first backward call
+    rhrt::TrainState* train = nullptr;
+};
+
+
+namespace rhrt {
+
+// Records m as the context's last error and returns code.
+int fail(rh_ctx* c, int code, const std::string& m);
+
+#define HCK(expr)                                                                     \
+    do {                                                                              \
+        hipError_t e_ = (expr);                                                       \
+        if (e_ != hipSuccess)                                                         \
+            return rhrt::fail(ctx, RH_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define RCK(expr)                   \
+    do {                            \
+        int r_ = (expr);            \
+        if (r_ != RH_OK) return r_; \
+    } while (0)
+
+#define LCK(expr)                                                                              \
+    do {                                                                                       \
+        hipError_t e_ = (expr);                                                                \
+        if (e_ != hipSuccess)                                                                  \
+            return rhrt::fail(ctx, RH_EDEVICE, std::string("launch ") + #expr + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+// Device allocation owned by the context (freed with it).
+template <typename T>
+int dalloc(rh_ctx* ctx, T** p, size_t elems) {
+    void* q = nullptr;
+    if (elems == 0) elems = 1;
+    if (hipMalloc(&q, elems * sizeof(T)) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(ctx, RH_ENOMEM, "hipMalloc of " + std::to_string(elems * sizeof(T)) + " bytes failed");
+    }
+    ctx->allocs.push_back(q);
+    *p = (T*)q;
+    return RH_OK;
+}
+void dfree(rh_ctx* ctx, void* p);
+
+// Launches fn(); when profiling class cls is on (and no graph is being
+// captured) brackets it with events.
+template <typename Fn>
+int timed(rh_ctx* ctx, int cls, Fn&& fn) {
+    Prof& p = ctx->prof[cls];
+    const bool on = p.on && !ctx->capturing;
+    hipEvent_t a = nullptr, b = nullptr;
+    if (on) {
+        HCK(hipEventCreate(&a));
+        HCK(hipEventCreate(&b));
+        HCK(hipEventRecord(a, ctx->stream));
+    }
+    hipError_t e = fn();
+    if (e != hipSuccess) return fail(ctx, RH_EDEVICE, std::string("kernel launch: ") + hipGetErrorString(e));
+    if (on) {
+        HCK(hipEventRecord(b, ctx->stream));
+        p.ev.emplace_back(a, b);
+    }
+    return RH_OK;
+}
+
+void set_sk(const rh_ctx* ctx, rh::GemmArgs& g);
+int ensure_rope(rh_ctx* ctx, int npos);
+int ensure_workspace(rh_ctx* ctx, int M);
+int check_tokens(rh_ctx* ctx, const uint32_t* t, size_t n);
+int check_err_flag(rh_ctx* ctx);
+// Logits (+ CE loss rows and per-sequence means) from the final-norm rows in
+// ctx->xn, or in xf when given.
+int enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss, const f16* xf = nullptr);
+
+}  // namespace rhrt

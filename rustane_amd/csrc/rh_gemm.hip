@@ -218,7 +218,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, int nw, int mw,
     for (int j = 0; j < TM; ++j) {
         const int m = mw + j * 32 + (lane & 31);
         if (m >= M) continue;
-        if constexpr (EPI == EPI_SWIGLU) {
+        if constexpr (EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_SAVE) {
             // W1|W3 is interleaved in 16-row groups: rows 0..15 of 32-row tile T
             // are W1 rows of features 16T.., rows 16..31 the matching W3 rows,
             // and row r + 16 sits in the same lane as row r (accumulator + 8).
@@ -236,6 +236,15 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, int nw, int mw,
                         g[r] = (f16)(silu_f(h1) * h3);
                     }
                     *(f16x4*)(a.out_f16 + frag_off(m, f, a.ldo)) = g;
+                    if constexpr (EPI == EPI_SWIGLU_SAVE) {
+                        // the pre-activations for the backward pass: h1 | h3 planes [M][F]
+                        const size_t o = (size_t)m * a.ldo + f, plane = (size_t)M * a.ldo;
+                        *(f16x4*)(a.h13 + o) = f16x4{(f16)acc.v[i][j][4 * q4 + 0], (f16)acc.v[i][j][4 * q4 + 1],
+                                                     (f16)acc.v[i][j][4 * q4 + 2], (f16)acc.v[i][j][4 * q4 + 3]};
+                        *(f16x4*)(a.h13 + plane + o) =
+                            f16x4{(f16)acc.v[i][j][4 * q4 + 8], (f16)acc.v[i][j][4 * q4 + 9],
+                                  (f16)acc.v[i][j][4 * q4 + 10], (f16)acc.v[i][j][4 * q4 + 11]};
+                    }
                 }
             }
         } else {
@@ -507,6 +516,9 @@ hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
             if (a.N % 32 != 0) return hipErrorInvalidValue;
             return launch_epi<EPI_SWIGLU>(a, st);
         case EPI_QKV: return launch_epi<EPI_QKV>(a, st);
+        case EPI_SWIGLU_SAVE:
+            if (a.N % 32 != 0 || !a.h13) return hipErrorInvalidValue;
+            return launch_epi<EPI_SWIGLU_SAVE>(a, st);
     }
     return hipErrorInvalidValue;
 }

@@ -9,7 +9,9 @@ typedef _Float16 f16;
 namespace rh {
 
 // ---------------- prefill GEMM:  Y[m][n] = sum_k X[m][k] * W[n][k] -------------
-enum GemmEpi { EPI_F32 = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3 };
+// EPI_SWIGLU_SAVE is EPI_SWIGLU that also stores the fp16 pre-activations
+// h1, h3 (planes [M][F] at h13 and h13 + M*F) for the backward pass.
+enum GemmEpi { EPI_F32 = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3, EPI_SWIGLU_SAVE = 4 };
 
 struct GemmArgs {
     const f16* W;  // [N, K] weights ("out x in"), fragment order (frag_off), rows padded to 16
@@ -26,6 +28,7 @@ struct GemmArgs {
     f16* vc;         // [B][H][ctx][hd]
     const float2* rope;  // [pos][hd/2] (cos, sin)
     int S, D, H, hd, ctx, pos0;
+    f16* h13;        // EPI_SWIGLU_SAVE: h1 | h3 planes, [2][M][ldo] fp16 row-major
     // Stream-K workspace (optional): fp32 partial tiles.
     float* sk_part;
     size_t sk_part_floats;
@@ -69,8 +72,9 @@ hipError_t launch_gemm_resid_norm(const GemmArgs& a, const float* gamma, float e
 // ---------------- attention ----------------
 // Causal prefill attention: q [B][H][S][hd], k/v [B][H][ctx][hd] (positions
 // 0..S-1), out token-major [B*S][H*hd] in fragment order (rows padded to 16).
+// lse (nullable) [B][H][S]: per query log2-sum-exp2 of the scaled scores.
 hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* out, int B, int H,
-                               int S, int hd, int ctx, hipStream_t st);
+                               int S, int hd, int ctx, hipStream_t st, float* lse = nullptr);
 // Decode attention over positions 0..*pos (the current token is at *pos):
 // q [B][H*hd]; per (b, h, chunk) partial (m, l, o[hd]), then a merge kernel.
 // Partial buffers hold B*H*attn_decode_chunks(ctx) entries; dch (positions per
@@ -137,6 +141,42 @@ hipError_t launch_cross_entropy(const float* logits, const uint32_t* targets, fl
 hipError_t launch_mean_rows(const float* loss, float* mean, int B, int S, hipStream_t st);
 hipError_t launch_set_state(int* state, int pos, int step, hipStream_t st);
 hipError_t launch_fill_f32(float* p, float v, size_t n, hipStream_t st);
+
+// ---------------- training (backward pass) ----------------
+// Backward activations are held in internal units: the CE gradient is stored
+// as (softmax - onehot) * GRAD_UNIT (see rh_trainops.hip).
+constexpr float GRAD_UNIT = 16.0f;
+// dl [rows][ldd] fp16 fragment order (zero in columns V..ldd-1) from the
+// (softcapped when softcap > 0) logits [rows][V] and targets.
+hipError_t launch_ce_backward(const float* logits, const uint32_t* targets, f16* dl, int rows, int V, int ldd,
+                              float softcap, float unit, hipStream_t st);
+// dst [C][Rp] (fragment order) = transpose of src [R][C] (fragment order),
+// zero in columns R..Rp-1; map 1 reads the W1|W3 interleaved SwiGLU weight
+// as [W1 rows | W3 rows].  C % 128 == 0, Rp % 128 == 0.
+hipError_t launch_transpose_frag(const f16* src, f16* dst, int R, int C, int Rp, int map, hipStream_t st);
+// RMSNorm backward over M rows: dx = rmsnorm'(x)^T dy (+ dres), optional
+// fp16 fragment-order copy of hscale * dx, per-block dgamma partials
+// [rms_backward_blocks(M)][D].  dx may alias dres.
+int rms_backward_blocks(int M);
+hipError_t launch_rms_backward(const float* dy, const float* x, const float* gamma, const float* dres, float* dx,
+                               f16* outh, float hscale, float* dg_part, int M, int D, float eps, hipStream_t st);
+// dgamma[d] += kappa * sum_b part[b][d]
+hipError_t launch_dgamma_reduce(const float* part, int nblk, int D, float kappa, float* dgamma, hipStream_t st);
+// dh [M][2F] fp16 fragment order (dh1 | dh3) from dgate [M][F] fp32 and h13.
+hipError_t launch_silu_backward(const float* dg, const f16* h13, f16* dh, int M, int F, hipStream_t st);
+// RoPE backward on the q, k sections of dqkv [M][3D] fp32, out fp16 fragment order.
+hipError_t launch_rope_backward_pack(const float* dqkv, const float2* rope, f16* out, int M, int S, int D, int hd,
+                                     hipStream_t st);
+// dembed[utok[u]] += kappa * dy[idx[j]] for j in [start[u], start[u+1]).
+hipError_t launch_embed_backward(const float* dy, const uint32_t* utok, const int* start, const int* idx, int nuniq,
+                                 float kappa, float* dembed, int D, hipStream_t st);
+// Causal attention backward: q, k, v [B][H][S][hd] fp16 (q, k after RoPE), o
+// the forward output (fragment order [B*S][H*hd]), dOf [B*S][H*hd] fp32, lse
+// from the forward.  Workspace dOh (fp16 [B][H][S][hd]) and Drow ([B][H][S]).
+// Writes dqkv [B*S][3*H*hd] fp32 (dq | dk | dv, before the RoPE backward).
+hipError_t launch_attn_backward(const f16* q, const f16* k, const f16* v, const f16* o, const float* dOf,
+                                const float* lse, f16* dOh, float* Drow, float* dqkv, int B, int H, int S, int hd,
+                                hipStream_t st);
 
 // ---------------- weight packing ----------------
 // Device weights are fp16 [N, K] in fragment order (frag_off in rh_device.h),

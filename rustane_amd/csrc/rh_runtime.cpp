@@ -13,9 +13,7 @@
 // (full_model.rs:915-991) with a = 1/sqrt(2L) (layer.rs:4640).  The decode
 // step runs the same chain on B <= 16 tokens with GEMV kernels and a KV cache,
 // and is replayed as a captured HIP graph.
-#include "../../include/rustane_hip.h"
-#include "rh_internal.h"
-#include "rh_kernels.h"
+#include "rh_ctx.h"
 
 #include <hip/hip_runtime.h>
 
@@ -27,96 +25,11 @@
 #include <string>
 #include <vector>
 
-namespace {
-
-struct Layer {
-    f16 *wqkv = nullptr, *wo = nullptr, *w13 = nullptr, *w2 = nullptr;
-    float *g1 = nullptr, *g2 = nullptr;
-};
-
-struct Prof {
-    bool on = false;
-    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
-    double ms = 0;
-    int64_t n = 0;
-};
-
-}  // namespace
-
-struct rh_ctx {
-    rh_config cfg{};
-    int device = 0, max_batch = 0, max_ctx = 0;
-    hipStream_t stream = nullptr;
-    std::string err;
-    std::vector<void*> allocs;
-
-    f16* embed = nullptr;
-    float* gfinal = nullptr;
-    std::vector<Layer> L;
-    float2* rope = nullptr;
-    int rope_len = 0;
-
-    // forward / prefill workspace (grow-only, sized for M = B*S rows)
-    int ws_M = 0;
-    float *x = nullptr, *logits = nullptr, *tok_loss = nullptr, *mean = nullptr;
-    f16 *xn = nullptr, *q = nullptr, *kbuf = nullptr, *vbuf = nullptr, *attn = nullptr, *gate = nullptr;
-    uint32_t *d_tok = nullptr, *d_tgt = nullptr;
-    size_t logits_rows = 0;
-    int* d_err = nullptr;
-
-    // KV cache [L][max_batch][H][max_ctx][hd]
-    f16 *kcache = nullptr, *vcache = nullptr;
-    size_t kv_layer = 0;
-
-    // decode (B <= 16)
-    float *dx = nullptr, *dlogits = nullptr, *pm = nullptr, *pl = nullptr, *po = nullptr;
-    f16 *dxn = nullptr, *dq = nullptr, *dattn = nullptr, *dgate = nullptr;
-    int* dstate = nullptr;
-    uint32_t *dtok = nullptr, *dout = nullptr, *dseq = nullptr;
-    float* dam_v = nullptr;  // [argmax blocks][16] argmax partials of the logits GEMV
-    int* dam_i = nullptr;
-    int dec_B = 0, host_pos = 0;
-    bool have_prefill = false;
-    bool use_graphs = true;
-    hipGraphExec_t dgraph = nullptr;
-    int dgraph_B = 0;
-    bool capturing = false;
-
-    float* staging = nullptr;
-    size_t staging_elems = 0;
-
-    // stream-K workspace of the prefill GEMMs (fp32 partial tiles)
-    float* sk_part = nullptr;
-    size_t sk_part_floats = 0;
-
-    Prof prof[RH_K_NCLASSES];
-};
-
-namespace {
+namespace rhrt {
 
 int fail(rh_ctx* c, int code, const std::string& m) {
     if (c) c->err = m;
     return code;
-}
-
-#define HCK(expr)                                                                     \
-    do {                                                                              \
-        hipError_t e_ = (expr);                                                       \
-        if (e_ != hipSuccess)                                                         \
-            return fail(ctx, RH_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); \
-    } while (0)
-
-template <typename T>
-int dalloc(rh_ctx* ctx, T** p, size_t elems) {
-    void* q = nullptr;
-    if (elems == 0) elems = 1;
-    if (hipMalloc(&q, elems * sizeof(T)) != hipSuccess) {
-        (void)hipGetLastError();
-        return fail(ctx, RH_ENOMEM, "hipMalloc of " + std::to_string(elems * sizeof(T)) + " bytes failed");
-    }
-    ctx->allocs.push_back(q);
-    *p = (T*)q;
-    return RH_OK;
 }
 
 void dfree(rh_ctx* ctx, void* p) {
@@ -125,12 +38,6 @@ void dfree(rh_ctx* ctx, void* p) {
     if (it != ctx->allocs.end()) ctx->allocs.erase(it);
     (void)hipFree(p);
 }
-
-#define RCK(expr)                   \
-    do {                            \
-        int r_ = (expr);            \
-        if (r_ != RH_OK) return r_; \
-    } while (0)
 
 size_t D_(const rh_ctx* c) { return (size_t)c->cfg.dim; }
 size_t F_(const rh_ctx* c) { return (size_t)c->cfg.hidden; }
@@ -194,37 +101,16 @@ int ensure_staging(rh_ctx* ctx, size_t elems) {
     return RH_OK;
 }
 
-// ---- timed launches -------------------------------------------------------
-template <typename Fn>
-int timed(rh_ctx* ctx, int cls, Fn&& fn) {
-    Prof& p = ctx->prof[cls];
-    const bool on = p.on && !ctx->capturing;
-    hipEvent_t a = nullptr, b = nullptr;
-    if (on) {
-        HCK(hipEventCreate(&a));
-        HCK(hipEventCreate(&b));
-        HCK(hipEventRecord(a, ctx->stream));
-    }
-    hipError_t e = fn();
-    if (e != hipSuccess) return fail(ctx, RH_EDEVICE, std::string("kernel launch: ") + hipGetErrorString(e));
-    if (on) {
-        HCK(hipEventRecord(b, ctx->stream));
-        p.ev.emplace_back(a, b);
-    }
-    return RH_OK;
-}
-
-#define LCK(expr)                                                                              \
-    do {                                                                                       \
-        hipError_t e_ = (expr);                                                                \
-        if (e_ != hipSuccess)                                                                  \
-            return fail(ctx, RH_EDEVICE, std::string("launch ") + #expr + ": " + hipGetErrorString(e_)); \
-    } while (0)
-
 void set_sk(const rh_ctx* ctx, rh::GemmArgs& g) {
     g.sk_part = ctx->sk_part;
     g.sk_part_floats = ctx->sk_part_floats;
 }
+
+}  // namespace rhrt
+
+using namespace rhrt;
+
+namespace {
 
 // ---- the forward token loop -----------------------------------------------
 // kv_k/kv_v: per-layer K/V destination base and ctx stride.  For a plain
@@ -277,12 +163,14 @@ int enqueue_body(rh_ctx* ctx, int B, int S, bool to_cache, bool final_norm) {
 
 // Logits + loss from xn, which enqueue_body(final_norm = true) left holding
 // the final RMSNorm of every row.
-int enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss) {
+}  // namespace
+
+int rhrt::enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss, const f16* xf) {
     const rh_config& c = ctx->cfg;
     const int M = B * S, D = c.dim;
     hipStream_t st = ctx->stream;
     rh::GemmArgs g{};
-    g.W = ctx->embed; g.X = ctx->xn; g.M = M; g.N = c.vocab; g.K = D;
+    g.W = ctx->embed; g.X = xf ? xf : ctx->xn; g.M = M; g.N = c.vocab; g.K = D;
     g.out_f32 = ctx->logits; g.ldo = c.vocab; g.softcap = c.softcap;
     set_sk(ctx, g);
     RCK(timed(ctx, RH_K_GEMM_LOGITS, [&] { return rh::launch_gemm(rh::EPI_F32, g, st); }));
@@ -292,6 +180,8 @@ int enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss) {
     }
     return RH_OK;
 }
+
+namespace {
 
 // One decode step for B tokens at position dstate[0].  For small B the
 // RMSNorms run inside the QKV / W1|W3 / logits GEMVs (one launch fewer per
@@ -379,7 +269,9 @@ int run_decode_step(rh_ctx* ctx, int B) {
     return RH_OK;
 }
 
-int check_err_flag(rh_ctx* ctx) {
+}  // namespace
+
+int rhrt::check_err_flag(rh_ctx* ctx) {
     int h = 0;
     HCK(hipMemcpyAsync(&h, ctx->d_err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
     HCK(hipStreamSynchronize(ctx->stream));
@@ -391,13 +283,15 @@ int check_err_flag(rh_ctx* ctx) {
     return RH_OK;
 }
 
-int check_tokens(rh_ctx* ctx, const uint32_t* t, size_t n) {
+int rhrt::check_tokens(rh_ctx* ctx, const uint32_t* t, size_t n) {
     for (size_t i = 0; i < n; ++i)
         if (t[i] >= (uint32_t)ctx->cfg.vocab)
             return fail(ctx, RH_ERANGE, "token id " + std::to_string(t[i]) + " at index " +
                                             std::to_string(i) + " >= vocab " + std::to_string(ctx->cfg.vocab));
     return RH_OK;
 }
+
+namespace {
 
 struct TensorMap {
     int R, C, map, row_off;  // reference orientation [R][C]; map 0/1 or -1 for plain
@@ -446,6 +340,7 @@ void destroy_ctx(rh_ctx* ctx) {
     if (ctx->dgraph) (void)hipGraphExecDestroy(ctx->dgraph);
     for (auto& p : ctx->prof)
         for (auto& e : p.ev) { (void)hipEventDestroy(e.first); (void)hipEventDestroy(e.second); }
+    rhrt::train_state_free(ctx->train);
     for (void* p : ctx->allocs) (void)hipFree(p);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -559,6 +454,7 @@ int rh_load_weights_f32(rh_ctx* ctx, const float* embed, const float* gamma_fina
         HCK(hipMemcpyAsync(ctx->L[l].g2, t[8], D * sizeof(float), hipMemcpyHostToDevice, st));
     }
     HCK(hipStreamSynchronize(st));
+    ++ctx->wgen;
     return RH_OK;
 }
 
@@ -614,6 +510,7 @@ int rh_init_weights_normal(rh_ctx* ctx, uint64_t seed, float std_) {
         LCK(rh::launch_fill_f32(ctx->L[l].g2, 1.0f, D, st));
     }
     HCK(hipStreamSynchronize(st));
+    ++ctx->wgen;
     (void)F;
     return RH_OK;
 }

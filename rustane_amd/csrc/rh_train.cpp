@@ -1,0 +1,398 @@
+// rh_train.cpp -- the training pass behind include/rustane_hip.h:
+// full_model::forward + backward_ws (full_model.rs:915-991, 592-702) with
+// layer::backward_into (layer.rs:7037-7366) per layer.
+//
+// The forward is the inference forward's kernels with every activation the
+// backward needs kept per layer (the ForwardCache of layer.rs:79-126): the
+// layer input and post-attention residuals (fp32), the normalised GEMM
+// operands, q/k/v, the attention output and its log-sum-exp, the SwiGLU
+// pre-activations and gate.  The backward then runs, per layer in reverse:
+//
+//   dW2 += dffn^T gate          dgate = dffn W2          (SiLU backward) -> dh1|dh3
+//   dx_ffn = dh1 W1^T + dh3 W3^T    dW1, dW3 += x2n^T dh{1,3}
+//   dx2 = RMSNorm2'(dx_ffn) + dy    da = (a dx2) Wo^T    dWo += attn^T (a dx2)
+//   attention backward -> dq, dk, dv   (RoPE backward on dq, dk)
+//   dxn = dq Wq^T + dk Wk^T + dv Wv^T   dWq, dWk, dWv += xn^T d{q,k,v}
+//   dy' = RMSNorm1'(dxn) + dx2
+//
+// Every product is an NT GEMM of the forward's kernel: the data-gradient
+// GEMMs stream transposed copies of the weights (built once per weight
+// version), the weight-gradient GEMMs contract over tokens and take
+// token-inner (transposed) copies of their operands, and accumulate into the
+// fp32 gradients in their epilogue (C += kappa * acc).  Gradients keep the
+// reference's tensor shapes and orientation and accumulate across calls.
+#include "rh_ctx.h"
+
+#include <algorithm>
+#include <array>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <vector>
+
+namespace rhrt {
+
+struct TrainState {
+    int M = 0, Mp = 0, B = 0, S = 0;  // token capacity; Mp = M rounded up to 128
+    uint64_t packs_gen = 0;            // weight version the transposed copies hold
+    bool have_grads = false;
+    // fp32 gradients, reference orientation (RSTK order per layer)
+    float *dembed = nullptr, *dgf = nullptr;
+    std::vector<std::array<float*, 9>> dlay;
+    // transposed fp16 weights (fragment order)
+    f16* embed_t = nullptr;  // [D][Vp]
+    struct WT { f16 *qkvt, *ot, *w13t, *w2t; };
+    std::vector<WT> wt;
+    // per-layer forward caches
+    struct Cache {
+        float *xin, *x2, *lse;
+        f16 *xn, *q, *k, *v, *attn, *x2n, *h13, *gate;
+    };
+    std::vector<Cache> c;
+    float* xlast = nullptr;  // residual after the last layer
+    f16* xf = nullptr;       // final RMSNorm rows (fragment order)
+    // backward workspace
+    f16 *dlh = nullptr, *dlT = nullptr, *H1 = nullptr, *H2 = nullptr, *T1 = nullptr, *T2 = nullptr, *T3 = nullptr;
+    f16* dOh = nullptr;
+    float *gout = nullptr, *dres = nullptr, *Drow = nullptr, *dgp = nullptr;
+    uint32_t* utok = nullptr;
+    int *ustart = nullptr, *uidx = nullptr;
+};
+
+void train_state_free(TrainState* t) { delete t; }
+
+}  // namespace rhrt
+
+using namespace rhrt;
+
+namespace {
+
+size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
+
+// Gradients and transposed weights: allocated once per context.
+int ensure_train_static(rh_ctx* ctx) {
+    TrainState* T = ctx->train;
+    if (T && T->dembed) return RH_OK;
+    if (!T) {
+        T = new (std::nothrow) TrainState;
+        if (!T) return fail(ctx, RH_ENOMEM, "out of host memory");
+        ctx->train = T;
+    }
+    const rh_config& c = ctx->cfg;
+    const size_t D = c.dim, F = c.hidden, V = c.vocab, Vp = round_up(V, 128);
+    RCK(dalloc(ctx, &T->dembed, V * D));
+    RCK(dalloc(ctx, &T->dgf, D));
+    T->dlay.resize(c.nlayers);
+    const size_t sz[9] = {D * D, D * D, D * D, D * D, D * F, D * F, D * F, D, D};
+    for (auto& g : T->dlay)
+        for (int j = 0; j < 9; ++j) RCK(dalloc(ctx, &g[j], sz[j]));
+    RCK(dalloc(ctx, &T->embed_t, D * Vp));
+    T->wt.resize(c.nlayers);
+    for (auto& w : T->wt) {
+        RCK(dalloc(ctx, &w.qkvt, D * 3 * D));
+        RCK(dalloc(ctx, &w.ot, D * D));
+        RCK(dalloc(ctx, &w.w13t, D * 2 * F));
+        RCK(dalloc(ctx, &w.w2t, F * D));
+    }
+    return rh_zero_grads(ctx);
+}
+
+// Caches and workspace for B sequences of S tokens (grow-only).
+int ensure_train_ws(rh_ctx* ctx, int B, int S) {
+    TrainState* T = ctx->train;
+    const int M = B * S;
+    if (M <= T->M) {  // every buffer is indexed with the current B, S: any B*S within capacity fits
+        T->B = B;
+        T->S = S;
+        return RH_OK;
+    }
+    HCK(hipStreamSynchronize(ctx->stream));
+    // free the old per-shape buffers
+    for (auto& cc : T->c) {
+        void* ps[] = {cc.xin, cc.x2, cc.lse, cc.xn, cc.q, cc.k, cc.v, cc.attn, cc.x2n, cc.h13, cc.gate};
+        for (void* p : ps) dfree(ctx, p);
+    }
+    {
+        void* ps[] = {T->xlast, T->xf, T->dlh, T->dlT, T->H1, T->H2, T->T1, T->T2, T->T3, T->dOh,
+                      T->gout, T->dres, T->Drow, T->dgp, T->utok, T->ustart, T->uidx};
+        for (void* p : ps) dfree(ctx, p);
+    }
+    const rh_config& c = ctx->cfg;
+    const size_t D = c.dim, F = c.hidden, V = c.vocab, Vp = round_up(V, 128);
+    const size_t m = M, m16 = round_up(m, 16), mp = round_up(m, 128);
+    T->c.assign(c.nlayers, TrainState::Cache{});
+    for (auto& cc : T->c) {
+        RCK(dalloc(ctx, &cc.xin, m * D));
+        RCK(dalloc(ctx, &cc.x2, m * D));
+        RCK(dalloc(ctx, &cc.lse, (size_t)M * c.heads));
+        RCK(dalloc(ctx, &cc.xn, m16 * D));
+        RCK(dalloc(ctx, &cc.q, m * D));
+        RCK(dalloc(ctx, &cc.k, m * D));
+        RCK(dalloc(ctx, &cc.v, m * D));
+        RCK(dalloc(ctx, &cc.attn, m16 * D));
+        RCK(dalloc(ctx, &cc.x2n, m16 * D));
+        RCK(dalloc(ctx, &cc.h13, 2 * m * F));
+        RCK(dalloc(ctx, &cc.gate, m16 * F));
+    }
+    const size_t wide = std::max(2 * F, 3 * D);
+    RCK(dalloc(ctx, &T->xlast, m * D));
+    RCK(dalloc(ctx, &T->xf, m16 * D));
+    RCK(dalloc(ctx, &T->dlh, m16 * Vp));
+    RCK(dalloc(ctx, &T->dlT, Vp * mp));
+    RCK(dalloc(ctx, &T->H1, m16 * D));
+    RCK(dalloc(ctx, &T->H2, m16 * wide));
+    RCK(dalloc(ctx, &T->T1, D * mp));
+    RCK(dalloc(ctx, &T->T2, std::max(F, D) * mp));
+    RCK(dalloc(ctx, &T->T3, wide * mp));
+    RCK(dalloc(ctx, &T->dOh, m * D));
+    RCK(dalloc(ctx, &T->gout, m * std::max(F, 4 * D)));  // [M][F] dgate, or da [M][D] + dqkv [M][3D]
+    RCK(dalloc(ctx, &T->dres, m * D));
+    RCK(dalloc(ctx, &T->Drow, (size_t)M * c.heads));
+    RCK(dalloc(ctx, &T->dgp, (size_t)rh::rms_backward_blocks(M) * D));
+    RCK(dalloc(ctx, &T->utok, m));
+    RCK(dalloc(ctx, &T->ustart, m + 1));
+    RCK(dalloc(ctx, &T->uidx, m));
+    T->M = M;
+    T->Mp = (int)mp;
+    T->B = B;
+    T->S = S;
+    return RH_OK;
+}
+
+// Transposed weight copies for the data-gradient GEMMs, rebuilt when the
+// weights changed since they were made.
+int ensure_packs(rh_ctx* ctx) {
+    TrainState* T = ctx->train;
+    if (T->packs_gen == ctx->wgen) return RH_OK;
+    const rh_config& c = ctx->cfg;
+    const int D = c.dim, F = c.hidden, V = c.vocab, Vp = (int)round_up(V, 128);
+    hipStream_t st = ctx->stream;
+    LCK(rh::launch_transpose_frag(ctx->embed, T->embed_t, V, D, Vp, 0, st));
+    for (int l = 0; l < c.nlayers; ++l) {
+        const Layer& W = ctx->L[l];
+        LCK(rh::launch_transpose_frag(W.wqkv, T->wt[l].qkvt, 3 * D, D, 3 * D, 0, st));
+        LCK(rh::launch_transpose_frag(W.wo, T->wt[l].ot, D, D, D, 0, st));
+        LCK(rh::launch_transpose_frag(W.w13, T->wt[l].w13t, 2 * F, D, 2 * F, 1, st));
+        LCK(rh::launch_transpose_frag(W.w2, T->wt[l].w2t, D, F, D, 0, st));
+    }
+    T->packs_gen = ctx->wgen;
+    return RH_OK;
+}
+
+// The forward token loop of enqueue_body with the caches kept per layer.
+int enqueue_forward_train(rh_ctx* ctx, int B, int S) {
+    TrainState* T = ctx->train;
+    const rh_config& c = ctx->cfg;
+    const int M = B * S, D = c.dim, F = c.hidden;
+    const float alpha = 1.0f / std::sqrt(2.0f * (float)c.nlayers);
+    hipStream_t st = ctx->stream;
+    LCK(rh::launch_embed(ctx->d_tok, ctx->embed, ctx->x, M, D, c.vocab, ctx->d_err, st));
+    LCK(rh::launch_rmsnorm(ctx->x, ctx->L[0].g1, T->c[0].xn, M, D, c.rms_eps, st, true));
+    for (int l = 0; l < c.nlayers; ++l) {
+        const Layer& W = ctx->L[l];
+        const TrainState::Cache& cc = T->c[l];
+        HCK(hipMemcpyAsync(cc.xin, ctx->x, (size_t)M * D * sizeof(float), hipMemcpyDeviceToDevice, st));
+        rh::GemmArgs g{};
+        g.W = W.wqkv; g.X = cc.xn; g.M = M; g.N = 3 * D; g.K = D;
+        g.q = cc.q; g.kc = cc.k; g.vc = cc.v; g.rope = ctx->rope;
+        g.S = S; g.D = D; g.H = c.heads; g.hd = c.head_dim; g.ctx = S; g.pos0 = 0;
+        set_sk(ctx, g);
+        RCK(timed(ctx, RH_K_GEMM_QKV, [&] { return rh::launch_gemm(rh::EPI_QKV, g, st); }));
+        RCK(timed(ctx, RH_K_ATTN, [&] {
+            return rh::launch_attn_prefill(cc.q, cc.k, cc.v, cc.attn, B, c.heads, S, c.head_dim, S, st, cc.lse);
+        }));
+        g = rh::GemmArgs{};
+        g.W = W.wo; g.X = cc.attn; g.M = M; g.N = D; g.K = D;
+        g.out_f32 = ctx->x; g.ldo = D; g.alpha = alpha;
+        set_sk(ctx, g);
+        RCK(timed(ctx, RH_K_GEMM_WO, [&] { return rh::launch_gemm_resid_norm(g, W.g2, c.rms_eps, cc.x2n, st); }));
+        HCK(hipMemcpyAsync(cc.x2, ctx->x, (size_t)M * D * sizeof(float), hipMemcpyDeviceToDevice, st));
+        g = rh::GemmArgs{};
+        g.W = W.w13; g.X = cc.x2n; g.M = M; g.N = 2 * F; g.K = D;
+        g.out_f16 = cc.gate; g.ldo = F; g.h13 = cc.h13;
+        set_sk(ctx, g);
+        RCK(timed(ctx, RH_K_GEMM_W13, [&] { return rh::launch_gemm(rh::EPI_SWIGLU_SAVE, g, st); }));
+        const bool last = l + 1 == c.nlayers;
+        g = rh::GemmArgs{};
+        g.W = W.w2; g.X = cc.gate; g.M = M; g.N = D; g.K = F;
+        g.out_f32 = ctx->x; g.ldo = D; g.alpha = alpha;
+        set_sk(ctx, g);
+        const float* ng = last ? ctx->gfinal : ctx->L[l + 1].g1;
+        f16* nxn = last ? T->xf : T->c[l + 1].xn;
+        RCK(timed(ctx, RH_K_GEMM_W2, [&] { return rh::launch_gemm_resid_norm(g, ng, c.rms_eps, nxn, st); }));
+    }
+    HCK(hipMemcpyAsync(T->xlast, ctx->x, (size_t)M * D * sizeof(float), hipMemcpyDeviceToDevice, st));
+    return enqueue_tail(ctx, B, S, true, T->xf);
+}
+
+// C[rows][cols] += kappa * X W^T with X [rows][Mp], W [cols][Mp] (token-inner).
+int grad_gemm(rh_ctx* ctx, const f16* X, const f16* W, int rows, int cols, float kappa, float* out) {
+    rh::GemmArgs g{};
+    g.X = X; g.W = W; g.M = rows; g.N = cols; g.K = ctx->train->Mp;
+    g.out_f32 = out; g.ldo = cols; g.alpha = kappa;
+    set_sk(ctx, g);
+    LCK(rh::launch_gemm(rh::EPI_RESID, g, ctx->stream));
+    return RH_OK;
+}
+
+// out [M][N] fp32 = A W^T with A [M][K] and W [N][K] (fragment order).
+int data_gemm(rh_ctx* ctx, const f16* A, const f16* W, int M, int N, int K, float* out) {
+    rh::GemmArgs g{};
+    g.X = A; g.W = W; g.M = M; g.N = N; g.K = K;
+    g.out_f32 = out; g.ldo = N;
+    set_sk(ctx, g);
+    LCK(rh::launch_gemm(rh::EPI_F32, g, ctx->stream));
+    return RH_OK;
+}
+
+int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
+    TrainState* T = ctx->train;
+    const rh_config& c = ctx->cfg;
+    const int M = B * S, D = c.dim, F = c.hidden, V = c.vocab, Vp = (int)round_up(V, 128), Mp = T->Mp;
+    const int H = c.heads, hd = c.head_dim;
+    const float alpha = 1.0f / std::sqrt(2.0f * (float)c.nlayers);
+    const float kappa = loss_scale / ((float)S * rh::GRAD_UNIT);
+    const int nblk = rh::rms_backward_blocks(M);
+    hipStream_t st = ctx->stream;
+    // CE gradient (internal units), dx_final = dl E, dembed += dl^T x_final
+    LCK(rh::launch_ce_backward(ctx->logits, ctx->d_tgt, T->dlh, M, V, Vp, c.softcap, rh::GRAD_UNIT, st));
+    RCK(data_gemm(ctx, T->dlh, T->embed_t, M, D, Vp, T->gout));
+    LCK(rh::launch_transpose_frag(T->dlh, T->dlT, M, Vp, Mp, 0, st));
+    LCK(rh::launch_transpose_frag(T->xf, T->T1, M, D, Mp, 0, st));
+    RCK(grad_gemm(ctx, T->dlT, T->T1, V, D, kappa, T->dembed));
+    // final RMSNorm backward: dy -> dres, a*dy -> H1 (the last layer's dffn)
+    LCK(rh::launch_rms_backward(T->gout, T->xlast, ctx->gfinal, nullptr, T->dres, T->H1, alpha, T->dgp, M, D,
+                                c.rms_eps, st));
+    LCK(rh::launch_dgamma_reduce(T->dgp, nblk, D, kappa, T->dgf, st));
+    for (int l = c.nlayers - 1; l >= 0; --l) {
+        const Layer& W = ctx->L[l];
+        const TrainState::Cache& cc = T->c[l];
+        const TrainState::WT& wt = T->wt[l];
+        float* const* G = T->dlay[l].data();
+        // dW2 += dffn^T gate; dgate = dffn W2; SiLU backward
+        LCK(rh::launch_transpose_frag(T->H1, T->T1, M, D, Mp, 0, st));
+        LCK(rh::launch_transpose_frag(cc.gate, T->T2, M, F, Mp, 0, st));
+        RCK(grad_gemm(ctx, T->T1, T->T2, D, F, kappa, G[6]));
+        RCK(data_gemm(ctx, T->H1, wt.w2t, M, F, D, T->gout));
+        LCK(rh::launch_silu_backward(T->gout, cc.h13, T->H2, M, F, st));
+        // dx_ffn = [dh1 | dh3] [W1 | W3]^T; dW1, dW3 += x2n^T dh
+        RCK(data_gemm(ctx, T->H2, wt.w13t, M, D, 2 * F, T->gout));
+        LCK(rh::launch_transpose_frag(T->H2, T->T3, M, 2 * F, Mp, 0, st));
+        LCK(rh::launch_transpose_frag(cc.x2n, T->T1, M, D, Mp, 0, st));
+        RCK(grad_gemm(ctx, T->T1, T->T3, D, F, kappa, G[4]));
+        RCK(grad_gemm(ctx, T->T1, T->T3 + (size_t)F * Mp, D, F, kappa, G[5]));
+        // dx2 = RMSNorm2'(dx_ffn) + dy (in place in dres); a*dx2 -> H1
+        LCK(rh::launch_rms_backward(T->gout, cc.x2, W.g2, T->dres, T->dres, T->H1, alpha, T->dgp, M, D,
+                                    c.rms_eps, st));
+        LCK(rh::launch_dgamma_reduce(T->dgp, nblk, D, kappa, G[8], st));
+        // da = (a dx2) Wo^T; dWo += attn^T (a dx2)
+        RCK(data_gemm(ctx, T->H1, wt.ot, M, D, D, T->gout));
+        LCK(rh::launch_transpose_frag(T->H1, T->T1, M, D, Mp, 0, st));
+        LCK(rh::launch_transpose_frag(cc.attn, T->T2, M, D, Mp, 0, st));
+        RCK(grad_gemm(ctx, T->T2, T->T1, D, D, kappa, G[3]));
+        // attention backward -> dq | dk | dv, RoPE backward, fp16 pack
+        float* dqkv = T->gout + (size_t)M * D;  // past da, which the attention kernels read
+        LCK(rh::launch_attn_backward(cc.q, cc.k, cc.v, cc.attn, T->gout, cc.lse, T->dOh, T->Drow, dqkv, B, H, S,
+                                     hd, st));
+        LCK(rh::launch_rope_backward_pack(dqkv, ctx->rope, T->H2, M, S, D, hd, st));
+        // dxn = dqkv [Wq | Wk | Wv]^T; dWq, dWk, dWv += xn^T d{q,k,v}
+        RCK(data_gemm(ctx, T->H2, wt.qkvt, M, D, 3 * D, T->gout));
+        LCK(rh::launch_transpose_frag(T->H2, T->T3, M, 3 * D, Mp, 0, st));
+        LCK(rh::launch_transpose_frag(cc.xn, T->T1, M, D, Mp, 0, st));
+        for (int j = 0; j < 3; ++j) RCK(grad_gemm(ctx, T->T1, T->T3 + (size_t)j * D * Mp, D, D, kappa, G[j]));
+        // dy' = RMSNorm1'(dxn) + dx2 (in place); a*dy' -> H1 (the next layer's dffn)
+        LCK(rh::launch_rms_backward(T->gout, cc.xin, W.g1, T->dres, T->dres, T->H1, alpha, T->dgp, M, D,
+                                    c.rms_eps, st));
+        LCK(rh::launch_dgamma_reduce(T->dgp, nblk, D, kappa, G[7], st));
+    }
+    LCK(rh::launch_embed_backward(T->dres, T->utok, T->ustart, T->uidx, nuniq, kappa, T->dembed, D, st));
+    T->have_grads = true;
+    return RH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rh_zero_grads(rh_ctx* ctx) {
+    if (!ctx) return RH_EINVAL;
+    TrainState* T = ctx->train;
+    if (!T || !T->dembed) return RH_OK;  // nothing allocated yet: the first backward starts from zero
+    HCK(hipSetDevice(ctx->device));
+    const rh_config& c = ctx->cfg;
+    const size_t D = c.dim, F = c.hidden, V = c.vocab;
+    hipStream_t st = ctx->stream;
+    LCK(rh::launch_fill_f32(T->dembed, 0.f, V * D, st));
+    LCK(rh::launch_fill_f32(T->dgf, 0.f, D, st));
+    const size_t sz[9] = {D * D, D * D, D * D, D * D, D * F, D * F, D * F, D, D};
+    for (auto& g : T->dlay)
+        for (int j = 0; j < 9; ++j) LCK(rh::launch_fill_f32(g[j], 0.f, sz[j], st));
+    HCK(hipStreamSynchronize(st));
+    T->have_grads = false;
+    return RH_OK;
+}
+
+int rh_forward_backward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
+                        float loss_scale, float* mean_loss_out) {
+    if (!ctx || !tokens || !targets) return fail(ctx, RH_EINVAL, "null argument");
+    if (batch <= 0 || seq <= 0 || batch > ctx->max_batch)
+        return fail(ctx, RH_ERANGE, "batch must be in [1, max_batch] and seq >= 1");
+    if (!(loss_scale > 0.f) || !std::isfinite(loss_scale)) return fail(ctx, RH_EINVAL, "loss_scale must be > 0");
+    const rh_config& c = ctx->cfg;
+    if (c.hidden % 64 != 0) return fail(ctx, RH_EINVAL, "the backward pass needs hidden % 64 == 0");
+    const size_t M = (size_t)batch * seq;
+    RCK(check_tokens(ctx, tokens, M));
+    RCK(check_tokens(ctx, targets, M));
+    HCK(hipSetDevice(ctx->device));
+    RCK(ensure_workspace(ctx, (int)M));
+    RCK(ensure_rope(ctx, seq));
+    RCK(ensure_train_static(ctx));
+    RCK(ensure_train_ws(ctx, batch, seq));
+    RCK(ensure_packs(ctx));
+    TrainState* T = ctx->train;
+    hipStream_t st = ctx->stream;
+    // positions of each distinct token, in increasing order (embedding backward)
+    std::map<uint32_t, std::vector<int>> pos;
+    for (size_t i = 0; i < M; ++i) pos[tokens[i]].push_back((int)i);
+    std::vector<uint32_t> utok;
+    std::vector<int> start{0}, idx;
+    for (auto& kv : pos) {
+        utok.push_back(kv.first);
+        idx.insert(idx.end(), kv.second.begin(), kv.second.end());
+        start.push_back((int)idx.size());
+    }
+    HCK(hipMemcpyAsync(ctx->d_tok, tokens, M * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(ctx->d_tgt, targets, M * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(T->utok, utok.data(), utok.size() * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(T->ustart, start.data(), start.size() * sizeof(int), hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(T->uidx, idx.data(), idx.size() * sizeof(int), hipMemcpyHostToDevice, st));
+    RCK(enqueue_forward_train(ctx, batch, seq));
+    RCK(enqueue_backward(ctx, batch, seq, loss_scale, (int)utok.size()));
+    if (mean_loss_out)
+        HCK(hipMemcpyAsync(mean_loss_out, ctx->mean, batch * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    return check_err_flag(ctx);
+}
+
+int rh_read_grads_f32(rh_ctx* ctx, float* dembed, float* dgamma_final, float* const* layer_grads) {
+    if (!ctx) return RH_EINVAL;
+    TrainState* T = ctx->train;
+    if (!T || !T->dembed) return fail(ctx, RH_ESTATE, "no gradients: run rh_forward_backward first");
+    HCK(hipSetDevice(ctx->device));
+    const rh_config& c = ctx->cfg;
+    const size_t D = c.dim, F = c.hidden, V = c.vocab;
+    hipStream_t st = ctx->stream;
+    if (dembed) HCK(hipMemcpyAsync(dembed, T->dembed, V * D * sizeof(float), hipMemcpyDeviceToHost, st));
+    if (dgamma_final) HCK(hipMemcpyAsync(dgamma_final, T->dgf, D * sizeof(float), hipMemcpyDeviceToHost, st));
+    const size_t sz[9] = {D * D, D * D, D * D, D * D, D * F, D * F, D * F, D, D};
+    if (layer_grads)
+        for (int l = 0; l < c.nlayers; ++l)
+            for (int j = 0; j < 9; ++j)
+                if (layer_grads[9 * l + j])
+                    HCK(hipMemcpyAsync(layer_grads[9 * l + j], T->dlay[l][j], sz[j] * sizeof(float),
+                                       hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    return RH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,341 @@
+// rh_trainops.hip -- row and elementwise kernels of the backward pass.
+//
+// Gradient units.  Backward activations that feed a GEMM are fp16, and a
+// sequence's true gradients are O(1/S) small (the CE gradient carries 1/S,
+// full_model.rs:325), below fp16's normal range for typical weights.  So the
+// backward runs in internal units: the CE gradient is stored as
+// (softmax - onehot) * GRAD_UNIT, and every quantity downstream is the true
+// one divided by kappa = loss_scale / (S * GRAD_UNIT).  Weight gradients are
+// scaled back by kappa where they are accumulated (GEMM epilogue alpha, the
+// gamma reductions, the embedding scatter), in fp32.
+#include "rh_device.h"
+#include "rh_kernels.h"
+
+namespace rh {
+namespace {
+
+int grid_for(size_t n, int per) {
+    const size_t g = (n + per - 1) / per;
+    return (int)(g > 65535 ? 65535 : (g ? g : 1));
+}
+
+// Softmax cross-entropy gradient of one logits row (cross_entropy.rs:58-96
+// without the 1/S, which kappa carries): dl = (softmax - onehot) * unit, times
+// 1 - (z/c)^2 when the logits z were softcapped (full_model.rs:608-615), fp16
+// in fragment order [rows][ldd], zero in columns V..ldd-1.
+__global__ __launch_bounds__(256) void ce_backward_kernel(const float* __restrict__ logits,
+                                                          const uint32_t* __restrict__ targets,
+                                                          f16* __restrict__ dl, int V, int ldd, float softcap,
+                                                          float unit) {
+    __shared__ float sm[4], ss[4];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float* l = logits + (size_t)row * V;
+    float m = -INFINITY, s = 0.f;
+    for (int i = tid * 4; i < V; i += 1024) {
+        const f32x4 v = *(const f32x4*)(l + i);
+        const float vm = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+        if (vm > m) { s *= __expf(m - vm); m = vm; }
+        s += __expf(v[0] - m) + __expf(v[1] - m) + __expf(v[2] - m) + __expf(v[3] - m);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float om = __shfl_xor(m, o, RH_WAVE), os = __shfl_xor(s, o, RH_WAVE);
+        const float nm = fmaxf(m, om);
+        s = (m == -INFINITY ? 0.f : s * __expf(m - nm)) + (om == -INFINITY ? 0.f : os * __expf(om - nm));
+        m = nm;
+    }
+    if ((tid & 63) == 0) { sm[tid >> 6] = m; ss[tid >> 6] = s; }
+    __syncthreads();
+    const float M = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+    float S = 0.f;
+    for (int w = 0; w < 4; ++w) S += ss[w] * __expf(sm[w] - M);
+    const float inv = unit / S;
+    const uint32_t t = targets[row];
+    const float ic = softcap > 0.f ? 1.0f / softcap : 0.f;
+    for (int i = tid * 8; i < ldd; i += 2048) {
+        f16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int v = i + e;
+            float d = 0.f;
+            if (v < V) {
+                const float z = l[v];
+                d = __expf(z - M) * inv - (v == (int)t ? unit : 0.f);
+                if (softcap > 0.f) {
+                    const float tz = z * ic;
+                    d *= 1.0f - tz * tz;
+                }
+            }
+            o[e] = (f16)d;
+        }
+        *(f16x8*)(dl + frag_off(row, i, ldd)) = o;
+    }
+}
+
+// Fragment-order transpose: dst [C][Rp] (fragment order, K = Rp) from src
+// [R][C] (fragment order, K = C): dst(c, r) = src(src_row(r), c) for r < R,
+// 0 for R <= r < Rp.  map 1 reads the W1|W3 16-row interleave of the SwiGLU
+// weight as [W1 rows | W3 rows] (R = 2F).  64 x 64 tiles through LDS.
+__device__ __forceinline__ int src_row(int r, int map, int R) {
+    if (map == 1) {
+        const int F = R / 2, w3 = r >= F, f = w3 ? r - F : r;
+        return 32 * (f >> 4) + 16 * w3 + (f & 15);
+    }
+    return r;
+}
+
+__global__ __launch_bounds__(256) void transpose_frag_kernel(const f16* __restrict__ src, f16* __restrict__ dst,
+                                                             int R, int C, int Rp, int map) {
+    __shared__ f16 tile[64][64 + 2];
+    const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64, tid = threadIdx.x;
+    // load: 64 rows x 8 column groups of 8
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int u = tid + 256 * p, rr = u >> 3, cg = (u & 7) * 8;
+        const int r = r0 + rr, c = c0 + cg;
+        f16x8 v = {};
+        if (r < R && c < C) v = *(const f16x8*)(src + frag_off(src_row(r, map, R), c, C));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tile[rr][cg + e] = v[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int u = tid + 256 * p, cc = u >> 3, rg = (u & 7) * 8;
+        const int c = c0 + cc, r = r0 + rg;
+        if (c < C && r < Rp) {
+            f16x8 v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = tile[rg + e][cc];
+            *(f16x8*)(dst + frag_off(c, r, Rp)) = v;
+        }
+    }
+}
+
+// rmsnorm::backward_channel_first (cpu/rmsnorm.rs:185-240) on token-major
+// rows, RB rows per block: r = 1/sqrt(sum(x^2)/D + eps) recomputed from x;
+// x_hat = x*r; dot = sum(dy*g*x_hat)/D; dx = r*(dy*g - x_hat*dot) (+ dres).
+// Writes dx (fp32, may alias dres), optionally hscale*dx as fp16 in fragment
+// order, and this block's dgamma partial sum(dy*x_hat) over its rows.
+constexpr int RB = 8;
+__global__ __launch_bounds__(256) void rms_backward_kernel(const float* __restrict__ dy, const float* __restrict__ x,
+                                                           const float* __restrict__ gamma, const float* dres,
+                                                           float* dx, f16* __restrict__ outh, float hscale,
+                                                           float* __restrict__ dg_part, int M, int D, float eps) {
+    __shared__ float red[4];
+    constexpr int NIT = 4;  // 8 columns x 256 threads x 4 = up to 8192
+    f32x4 gm[NIT][2], dgp[NIT][2];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int i = threadIdx.x * 8 + it * 2048;
+        if (i < D) {
+            gm[it][0] = *(const f32x4*)(gamma + i);
+            gm[it][1] = *(const f32x4*)(gamma + i + 4);
+        }
+        dgp[it][0] = dgp[it][1] = f32x4{};
+    }
+    const int rbeg = blockIdx.x * RB, rend = min(M, rbeg + RB);
+    for (int row = rbeg; row < rend; ++row) {
+        const float* xr = x + (size_t)row * D;
+        const float* dr = dy + (size_t)row * D;
+        f32x4 xv[NIT][2], dv[NIT][2];
+        float ss = 0.f;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int i = threadIdx.x * 8 + it * 2048;
+            if (i < D) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    xv[it][hh] = *(const f32x4*)(xr + i + 4 * hh);
+                    dv[it][hh] = *(const f32x4*)(dr + i + 4 * hh);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ss += xv[it][hh][e] * xv[it][hh][e];
+                }
+            }
+        }
+        ss = block_sum_256(ss, red);
+        const float r = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
+        float dot = 0.f;
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int i = threadIdx.x * 8 + it * 2048;
+            if (i < D) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float xh = xv[it][hh][e] * r;
+                        dot += dv[it][hh][e] * gm[it][hh][e] * xh;
+                        dgp[it][hh][e] += dv[it][hh][e] * xh;
+                    }
+            }
+        }
+        dot = block_sum_256(dot, red) * (1.0f / (float)D);
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int i = threadIdx.x * 8 + it * 2048;
+            if (i < D) {
+                f16x8 h;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    f32x4 o;
+                    const f32x4 rv = dres ? *(const f32x4*)(dres + (size_t)row * D + i + 4 * hh) : f32x4{};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float xh = xv[it][hh][e] * r;
+                        o[e] = r * (dv[it][hh][e] * gm[it][hh][e] - xh * dot) + rv[e];
+                        h[4 * hh + e] = (f16)(o[e] * hscale);
+                    }
+                    *(f32x4*)(dx + (size_t)row * D + i + 4 * hh) = o;
+                }
+                if (outh) *(f16x8*)(outh + frag_off(row, i, D)) = h;
+            }
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int i = threadIdx.x * 8 + it * 2048;
+        if (i < D) {
+            *(f32x4*)(dg_part + (size_t)blockIdx.x * D + i) = dgp[it][0];
+            *(f32x4*)(dg_part + (size_t)blockIdx.x * D + i + 4) = dgp[it][1];
+        }
+    }
+}
+
+// dgamma[d] += kappa * sum of the partials in block order (deterministic).
+__global__ void dgamma_reduce_kernel(const float* __restrict__ part, int nblk, int D, float kappa,
+                                     float* __restrict__ dgamma) {
+    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= D) return;
+    float s = 0.f;
+    for (int b = 0; b < nblk; ++b) s += part[(size_t)b * D + d];
+    dgamma[d] += kappa * s;
+}
+
+// SiLU-gate backward (layer.rs:7083-7104) from the GEMM's dgate [M, F] fp32
+// and the saved fp16 pre-activations h1 | h3 ([2][M][F]): dh1, dh3 as fp16
+// in fragment order [M][2F] (dh1 in columns 0..F-1, dh3 in F..2F-1).
+__global__ __launch_bounds__(256) void silu_backward_kernel(const float* __restrict__ dg, const f16* __restrict__ h13,
+                                                            f16* __restrict__ dh, int M, int F) {
+    const size_t n8 = (size_t)M * F / 8;
+    for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n8; t += (size_t)gridDim.x * blockDim.x) {
+        const size_t base = t * 8;
+        const int m = (int)(base / F), f = (int)(base % F);
+        const f32x4 g0 = *(const f32x4*)(dg + base), g1 = *(const f32x4*)(dg + base + 4);
+        const f16x8 a = *(const f16x8*)(h13 + base), c = *(const f16x8*)(h13 + (size_t)M * F + base);
+        f16x8 o1, o3;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float g = e < 4 ? g0[e] : g1[e - 4];
+            const float h1 = (float)a[e], h3 = (float)c[e];
+            const float sig = 1.0f / (1.0f + __expf(-h1));
+            o3[e] = (f16)(g * (h1 * sig));
+            o1[e] = (f16)(g * h3 * (sig * (1.0f + h1 * (1.0f - sig))));
+        }
+        *(f16x8*)(dh + frag_off(m, f, 2 * F)) = o1;
+        *(f16x8*)(dh + frag_off(m, F + f, 2 * F)) = o3;
+    }
+}
+
+// RoPE backward (rope_backward_inplace, layer.rs:7389-7407) on the q and k
+// sections of dqkv [M][3D] fp32 (token m at position m % S), then fp16 in
+// fragment order [M][3D] for the dX GEMM.
+__global__ __launch_bounds__(256) void rope_backward_pack_kernel(const float* __restrict__ dqkv,
+                                                                 const float2* __restrict__ rope,
+                                                                 f16* __restrict__ out, int M, int S, int D, int hd) {
+    const int N = 3 * D;
+    const size_t n8 = (size_t)M * N / 8;
+    for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n8; t += (size_t)gridDim.x * blockDim.x) {
+        const size_t base = t * 8;
+        const int m = (int)(base / N), c = (int)(base % N);
+        const f32x4 a0 = *(const f32x4*)(dqkv + base), a1 = *(const f32x4*)(dqkv + base + 4);
+        float v[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        if (c < 2 * D) {
+            const int d = (c % D) % hd, pos = m % S;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const float2 cs = rope[(size_t)pos * (hd / 2) + d / 2 + p];
+                const float d0 = v[2 * p], d1 = v[2 * p + 1];
+                v[2 * p] = cs.x * d0 + cs.y * d1;
+                v[2 * p + 1] = -cs.y * d0 + cs.x * d1;
+            }
+        }
+        f16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (f16)v[e];
+        *(f16x8*)(out + frag_off(m, c, N)) = o;
+    }
+}
+
+// embedding::backward_channel_first (cpu/embedding.rs:34-44): dembed[tok] +=
+// kappa * dy[pos] for the positions of each distinct token in increasing
+// order (one block per distinct token; idx/start a CSR built on the host).
+__global__ __launch_bounds__(256) void embed_backward_kernel(const float* __restrict__ dy,
+                                                             const uint32_t* __restrict__ utok,
+                                                             const int* __restrict__ start,
+                                                             const int* __restrict__ idx, float kappa,
+                                                             float* __restrict__ dembed, int D) {
+    const int u = blockIdx.x;
+    float* row = dembed + (size_t)utok[u] * D;
+    const int a = start[u], b = start[u + 1];
+    for (int d = threadIdx.x; d < D; d += 256) {
+        float v = row[d];
+        for (int j = a; j < b; ++j) v += kappa * dy[(size_t)idx[j] * D + d];
+        row[d] = v;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_ce_backward(const float* logits, const uint32_t* targets, f16* dl, int rows, int V, int ldd,
+                              float softcap, float unit, hipStream_t st) {
+    if (V % 4 != 0 || ldd % 128 != 0 || ldd < V) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(ce_backward_kernel, dim3(rows), dim3(256), 0, st, logits, targets, dl, V, ldd, softcap, unit);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose_frag(const f16* src, f16* dst, int R, int C, int Rp, int map, hipStream_t st) {
+    if (C % 128 != 0 || Rp % 128 != 0 || Rp < R || (map == 1 && R % 32 != 0)) return hipErrorInvalidValue;
+    const dim3 grid(C / 64, Rp / 64);
+    hipLaunchKernelGGL(transpose_frag_kernel, grid, dim3(256), 0, st, src, dst, R, C, Rp, map);
+    return hipGetLastError();
+}
+
+int rms_backward_blocks(int M) { return (M + RB - 1) / RB; }
+
+hipError_t launch_rms_backward(const float* dy, const float* x, const float* gamma, const float* dres, float* dx,
+                               f16* outh, float hscale, float* dg_part, int M, int D, float eps, hipStream_t st) {
+    if (D % 8 != 0 || D > 8192) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rms_backward_kernel, dim3(rms_backward_blocks(M)), dim3(256), 0, st, dy, x, gamma, dres, dx,
+                       outh, hscale, dg_part, M, D, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_dgamma_reduce(const float* part, int nblk, int D, float kappa, float* dgamma, hipStream_t st) {
+    hipLaunchKernelGGL(dgamma_reduce_kernel, dim3((D + 255) / 256), dim3(256), 0, st, part, nblk, D, kappa, dgamma);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_backward(const float* dg, const f16* h13, f16* dh, int M, int F, hipStream_t st) {
+    if (F % 8 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(silu_backward_kernel, dim3(grid_for((size_t)M * F / 8, 256)), dim3(256), 0, st, dg, h13, dh,
+                       M, F);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_backward_pack(const float* dqkv, const float2* rope, f16* out, int M, int S, int D, int hd,
+                                     hipStream_t st) {
+    if (D % 8 != 0 || hd % 8 != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rope_backward_pack_kernel, dim3(grid_for((size_t)M * 3 * D / 8, 256)), dim3(256), 0, st, dqkv,
+                       rope, out, M, S, D, hd);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_backward(const float* dy, const uint32_t* utok, const int* start, const int* idx, int nuniq,
+                                 float kappa, float* dembed, int D, hipStream_t st) {
+    if (nuniq <= 0) return hipSuccess;
+    hipLaunchKernelGGL(embed_backward_kernel, dim3(nuniq), dim3(256), 0, st, dy, utok, start, idx, kappa, dembed, D);
+    return hipGetLastError();
+}
+
+}  // namespace rh

@@ -89,6 +89,9 @@ def lib():
     L.rh_read_weights_f32.argtypes = [ctxp, _f32p, _f32p, ctypes.POINTER(_f32p)]
     L.rh_init_weights_normal.argtypes = [ctxp, ctypes.c_uint64, ctypes.c_float]
     L.rh_forward.argtypes = [ctxp, _u32p, _u32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p, _f32p]
+    L.rh_forward_backward.argtypes = [ctxp, _u32p, _u32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, _f32p]
+    L.rh_zero_grads.argtypes = [ctxp]
+    L.rh_read_grads_f32.argtypes = [ctxp, _f32p, _f32p, ctypes.POINTER(_f32p)]
     L.rh_forward_dev.argtypes = [ctxp, _vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]
     L.rh_prefill.argtypes = [ctxp, _u32p, ctypes.c_int, ctypes.c_int, _u32p, _f32p]
     L.rh_decode_step.argtypes = [ctxp, _u32p, _u32p, _f32p]
@@ -204,6 +207,37 @@ class Context:
         flat = [t for lw in layers for t in lw]
         ptrs = (_f32p * len(flat))(*[_f(t) for t in flat])
         self._ck(lib().rh_read_weights_f32(self.h, _f(embed), _f(gf), ptrs), "rh_read_weights_f32")
+        return embed, gf, layers
+
+    # -- training pass ----------------------------------------------------
+    def forward_backward(self, tokens, targets, loss_scale: float = 1.0):
+        """Adds loss_scale x d(mean loss)/d(params) of every sequence to the
+        context's gradients; returns the mean losses [B]."""
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        if tokens.ndim == 1:
+            tokens = tokens[None]
+        B, S = tokens.shape
+        tg = np.ascontiguousarray(targets, np.uint32).reshape(B, S)
+        ml = np.empty((B,), np.float32)
+        self._ck(lib().rh_forward_backward(self.h, _u(tokens), _u(tg), B, S, float(loss_scale), _f(ml)),
+                 "rh_forward_backward")
+        return ml
+
+    def zero_grads(self):
+        self._ck(lib().rh_zero_grads(self.h), "rh_zero_grads")
+
+    def read_grads(self):
+        """(dembed [V, D], dgamma_final [D], [[9 per layer]]) in the weights'
+        orientation and RSTK order."""
+        c = self.cfg
+        D, F, V, L = c.dim, c.hidden, c.vocab, c.nlayers
+        embed = np.empty((V, D), np.float32)
+        gf = np.empty(D, np.float32)
+        shapes = [(D, D)] * 4 + [(D, F)] * 3 + [(D,), (D,)]
+        layers = [[np.empty(s, np.float32) for s in shapes] for _ in range(L)]
+        flat = [t for lw in layers for t in lw]
+        ptrs = (_f32p * len(flat))(*[_f(t) for t in flat])
+        self._ck(lib().rh_read_grads_f32(self.h, _f(embed), _f(gf), ptrs), "rh_read_grads_f32")
         return embed, gf, layers
 
     def init_normal(self, seed: int, std: float = 0.02):

@@ -127,6 +127,9 @@ def test_null_context_is_rejected_everywhere(lib):
     assert lib.rh_sched_wait(None, None) == hb.RH_EINVAL
     assert lib.rh_sched_run_batch(None, None, 0, None) == hb.RH_EINVAL
     lib.rh_sched_destroy(None)  # a no-op
+    assert lib.rh_forward_backward(None, tp, tp, 1, 4, 1.0, None) == hb.RH_EINVAL
+    assert lib.rh_zero_grads(None) == hb.RH_EINVAL
+    assert lib.rh_read_grads_f32(None, None, None, None) == hb.RH_EINVAL
 
 
 def test_context_free_errors_are_per_thread(lib):
