@@ -63,6 +63,10 @@ def main():
     ap.add_argument("--extra-configs", default="600m,5b",
                     help="also time batch-1 prefill of these model shapes ('' for none)")
     ap.add_argument("--decode-only", action="store_true", help="skip the prefill timing")
+    ap.add_argument("--train-only", action="store_true",
+                    help="time only the training step (forward + backward)")
+    ap.add_argument("--train-steps", type=int, default=5)
+    ap.add_argument("--train-batches", default="1,4", help="batches of the training-step timing")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run three 256 MiB device-to-device copies (a known-size kernel "
                          "for scaling hardware byte counters)")
@@ -85,7 +89,8 @@ def main():
         args.extra_batches = args.extra_decode_batches = args.extra_configs = ""
     extra = [int(x) for x in args.extra_batches.split(",") if x]
     extra_dec = [] if args.no_decode else [int(x) for x in args.extra_decode_batches.split(",") if x]
-    max_batch = max([args.batch, args.decode_batch] + extra + extra_dec)
+    train_b = [int(x) for x in args.train_batches.split(",") if x] if (args.train_only or not args.no_extra) else []
+    max_batch = max([args.batch, args.decode_batch] + extra + extra_dec + train_b)
     max_ctx = 0 if args.no_decode else args.decode_ctx + args.decode_steps
     log(f"[bench] config={args.config} B={args.batch} S={cfg.seq} max_ctx={max_ctx}")
     t0 = time.time()
@@ -126,6 +131,10 @@ def main():
     if args.decode_only:
         print(json.dumps({"decode": run_decode(ctx, cfg, args, hb, E, hip_rt, stream)}), flush=True)
         return
+    if args.train_only:
+        print(json.dumps({"train_step": {f"B{b}": run_train_step(ctx, cfg, args, E, b) for b in train_b}}),
+              flush=True)
+        return
 
     if args.copy_calibration:
         nb = 256 << 20
@@ -163,6 +172,8 @@ def main():
     sched = None
     if not args.no_extra and max_batch >= 16:
         sched = run_scheduler(ctx, cfg, hb, requests=32, max_batch=16)
+
+    train = {f"B{b}": run_train_step(ctx, cfg, args, E, b) for b in train_b} if train_b else None
 
     decode = None
     decode_lines = {}
@@ -216,6 +227,8 @@ def main():
         line["decode_batches"] = decode_lines
     if sched:
         line["scheduler"] = sched
+    if train:
+        line["train_step"] = train
     if config_lines:
         line["prefill_configs"] = config_lines
     if cpu:
@@ -223,6 +236,33 @@ def main():
     if cpu_dec:
         line["cpu_baseline_decode"] = cpu_dec
     print(json.dumps(line), flush=True)
+
+
+def run_train_step(ctx, cfg, args, E, B):
+    """One training step = zero the gradients, then forward + backward over
+    one batch of B sequences (the weights do not change), timed by wall clock
+    around rh_zero_grads + rh_forward_backward (each call synchronises)."""
+    S = cfg.seq
+    rng = np.random.default_rng(7)
+    toks = rng.integers(0, cfg.vocab, size=(B, S + 1)).astype(np.uint32)
+    tok, tgt = np.ascontiguousarray(toks[:, :-1]), np.ascontiguousarray(toks[:, 1:])
+    t0 = time.perf_counter()
+    ctx.forward_backward(tok, tgt)  # first call allocates gradients and transposed weights
+    first = time.perf_counter() - t0
+    ctx.forward_backward(tok, tgt)
+    t = time.perf_counter()
+    for _ in range(args.train_steps):
+        ctx.zero_grads()
+        loss = ctx.forward_backward(tok, tgt)
+    ms = (time.perf_counter() - t) * 1e3 / args.train_steps
+    flops = E.train_step_flops(cfg, S, B)
+    tf = flops / (ms / 1e3) / 1e12
+    out = {"tok_s": round(B * S / (ms / 1e3), 1), "ms_per_step": round(ms, 3), "steps": args.train_steps,
+           "batch": B, "seq_len": S, "flops_per_step": flops, "achieved_tflops": round(tf, 1),
+           "mfma_frac": round(tf / PEAK_FP16_TFLOPS, 4), "loss": float(loss[0]),
+           "first_call_s": round(first, 3)}
+    log(f"[bench] train step B={B}: {out}")
+    return out
 
 
 def run_scheduler(ctx, cfg, hb, requests, max_batch):

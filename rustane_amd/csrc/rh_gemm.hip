@@ -257,6 +257,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, int nw, int mw,
                     float v0 = acc.v[i][j][4 * q4 + 0], v1 = acc.v[i][j][4 * q4 + 1];
                     float v2 = acc.v[i][j][4 * q4 + 2], v3 = acc.v[i][j][4 * q4 + 3];
                     if constexpr (EPI == EPI_F32) {
+                        if (a.alpha != 0.f) {  // optional output scale (0 = none)
+                            v0 *= a.alpha; v1 *= a.alpha; v2 *= a.alpha; v3 *= a.alpha;
+                        }
                         if (a.softcap > 0.f) {
                             const float c = a.softcap, ic = 1.0f / c;
                             v0 = tanhf(v0 * ic) * c; v1 = tanhf(v1 * ic) * c;
@@ -320,6 +323,7 @@ __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long lo
         b.out_f32 = a.sk_part + (size_t)sp * a.M * a.N;
         b.ldo = a.N;
         b.softcap = 0.f;
+        b.alpha = 0.f;  // raw partials: the row kernel applies alpha once to their sum
         epilogue<Tl::FTN, Tl::FTM, EPI_F32>(b, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
     } else {
         constexpr int TN = Tl::FTN, TM = Tl::FTM, NT = Tl::NT;

@@ -20,7 +20,7 @@ struct GemmArgs {
     float* out_f32;  // EPI_F32: [M, ldo]; EPI_RESID: residual x [M, ldo], updated in place
     f16* out_f16;    // EPI_SWIGLU: gate [M, ldo] in fragment order
     int ldo;
-    float alpha;     // EPI_RESID: x += alpha * acc
+    float alpha;     // EPI_RESID: x += alpha * acc; EPI_F32: out = alpha * acc (0 = unscaled)
     float softcap;   // EPI_F32: c * tanh(acc / c) when c > 0
     // EPI_QKV: N = 3*D rows ordered q | k | v; RoPE on q and k.
     f16* q;          // [B][H][S][hd]
@@ -160,8 +160,9 @@ hipError_t launch_transpose_frag(const f16* src, f16* dst, int R, int C, int Rp,
 int rms_backward_blocks(int M);
 hipError_t launch_rms_backward(const float* dy, const float* x, const float* gamma, const float* dres, float* dx,
                                f16* outh, float hscale, float* dg_part, int M, int D, float eps, hipStream_t st);
-// dgamma[d] += kappa * sum_b part[b][d]
-hipError_t launch_dgamma_reduce(const float* part, int nblk, int D, float kappa, float* dgamma, hipStream_t st);
+// dgamma[d] += kappa * sum_b part[b][d]  (= instead of += when store is set)
+hipError_t launch_dgamma_reduce(const float* part, int nblk, int D, float kappa, float* dgamma, bool store,
+                                hipStream_t st);
 // dh [M][2F] fp16 fragment order (dh1 | dh3) from dgate [M][F] fp32 and h13.
 hipError_t launch_silu_backward(const float* dg, const f16* h13, f16* dh, int M, int F, hipStream_t st);
 // RoPE backward on the q, k sections of dqkv [M][3D] fp32, out fp16 fragment order.

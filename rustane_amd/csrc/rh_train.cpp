@@ -35,7 +35,7 @@ namespace rhrt {
 struct TrainState {
     int M = 0, Mp = 0, B = 0, S = 0;  // token capacity; Mp = M rounded up to 128
     uint64_t packs_gen = 0;            // weight version the transposed copies hold
-    bool have_grads = false;
+    bool zero = true;  // every gradient is 0: the weight-gradient GEMMs store instead of accumulating
     // fp32 gradients, reference orientation (RSTK order per layer)
     float *dembed = nullptr, *dgf = nullptr;
     std::vector<std::array<float*, 9>> dlay;
@@ -94,7 +94,8 @@ int ensure_train_static(rh_ctx* ctx) {
         RCK(dalloc(ctx, &w.w13t, D * 2 * F));
         RCK(dalloc(ctx, &w.w2t, F * D));
     }
-    return rh_zero_grads(ctx);
+    T->zero = true;
+    return RH_OK;
 }
 
 // Caches and workspace for B sequences of S tokens (grow-only).
@@ -225,13 +226,27 @@ int enqueue_forward_train(rh_ctx* ctx, int B, int S) {
     return enqueue_tail(ctx, B, S, true, T->xf);
 }
 
+// dgamma (+)= kappa * the partial sums of rms_backward (stores while the
+// gradients are logically zero).
+int gamma_grad(rh_ctx* ctx, int nblk, int D, float kappa, float* dgamma) {
+    LCK(rh::launch_dgamma_reduce(ctx->train->dgp, nblk, D, kappa, dgamma, ctx->train->zero, ctx->stream));
+    return RH_OK;
+}
+
 // C[rows][cols] += kappa * X W^T with X [rows][Mp], W [cols][Mp] (token-inner).
+// When every gradient is still zero the epilogue stores kappa * acc instead
+// (the same values; it skips reading the fp32 gradient back).  K is the
+// token count, short next to the fp32 output these GEMMs write, so they use
+// 192x128 tiles, whose 80 KB of LDS lets two blocks share a CU and one's
+// epilogue stores overlap the other's MFMAs (measured at 7B: 40.4 vs 44.1 ms
+// per B1 step with the 256x256 tiles the FLOP-rate heuristic picks).
 int grad_gemm(rh_ctx* ctx, const f16* X, const f16* W, int rows, int cols, float kappa, float* out) {
     rh::GemmArgs g{};
     g.X = X; g.W = W; g.M = rows; g.N = cols; g.K = ctx->train->Mp;
     g.out_f32 = out; g.ldo = cols; g.alpha = kappa;
+    g.force_cfg = rh::GCFG_D4_192x128;
     set_sk(ctx, g);
-    LCK(rh::launch_gemm(rh::EPI_RESID, g, ctx->stream));
+    LCK(rh::launch_gemm(ctx->train->zero ? rh::EPI_F32 : rh::EPI_RESID, g, ctx->stream));
     return RH_OK;
 }
 
@@ -263,7 +278,7 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
     // final RMSNorm backward: dy -> dres, a*dy -> H1 (the last layer's dffn)
     LCK(rh::launch_rms_backward(T->gout, T->xlast, ctx->gfinal, nullptr, T->dres, T->H1, alpha, T->dgp, M, D,
                                 c.rms_eps, st));
-    LCK(rh::launch_dgamma_reduce(T->dgp, nblk, D, kappa, T->dgf, st));
+    RCK(gamma_grad(ctx, nblk, D, kappa, T->dgf));
     for (int l = c.nlayers - 1; l >= 0; --l) {
         const Layer& W = ctx->L[l];
         const TrainState::Cache& cc = T->c[l];
@@ -284,7 +299,7 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         // dx2 = RMSNorm2'(dx_ffn) + dy (in place in dres); a*dx2 -> H1
         LCK(rh::launch_rms_backward(T->gout, cc.x2, W.g2, T->dres, T->dres, T->H1, alpha, T->dgp, M, D,
                                     c.rms_eps, st));
-        LCK(rh::launch_dgamma_reduce(T->dgp, nblk, D, kappa, G[8], st));
+        RCK(gamma_grad(ctx, nblk, D, kappa, G[8]));
         // da = (a dx2) Wo^T; dWo += attn^T (a dx2)
         RCK(data_gemm(ctx, T->H1, wt.ot, M, D, D, T->gout));
         LCK(rh::launch_transpose_frag(T->H1, T->T1, M, D, Mp, 0, st));
@@ -303,10 +318,10 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         // dy' = RMSNorm1'(dxn) + dx2 (in place); a*dy' -> H1 (the next layer's dffn)
         LCK(rh::launch_rms_backward(T->gout, cc.xin, W.g1, T->dres, T->dres, T->H1, alpha, T->dgp, M, D,
                                     c.rms_eps, st));
-        LCK(rh::launch_dgamma_reduce(T->dgp, nblk, D, kappa, G[7], st));
+        RCK(gamma_grad(ctx, nblk, D, kappa, G[7]));
     }
     LCK(rh::launch_embed_backward(T->dres, T->utok, T->ustart, T->uidx, nuniq, kappa, T->dembed, D, st));
-    T->have_grads = true;
+    T->zero = false;
     return RH_OK;
 }
 
@@ -314,21 +329,14 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
 
 extern "C" {
 
+// Zeroing is logical: the next backward's weight-gradient GEMMs and gamma
+// reductions store instead of accumulating, and reads return zeros until
+// then, so no pass over the gradient memory is needed.
 int rh_zero_grads(rh_ctx* ctx) {
     if (!ctx) return RH_EINVAL;
     TrainState* T = ctx->train;
-    if (!T || !T->dembed) return RH_OK;  // nothing allocated yet: the first backward starts from zero
-    HCK(hipSetDevice(ctx->device));
-    const rh_config& c = ctx->cfg;
-    const size_t D = c.dim, F = c.hidden, V = c.vocab;
-    hipStream_t st = ctx->stream;
-    LCK(rh::launch_fill_f32(T->dembed, 0.f, V * D, st));
-    LCK(rh::launch_fill_f32(T->dgf, 0.f, D, st));
-    const size_t sz[9] = {D * D, D * D, D * D, D * D, D * F, D * F, D * F, D, D};
-    for (auto& g : T->dlay)
-        for (int j = 0; j < 9; ++j) LCK(rh::launch_fill_f32(g[j], 0.f, sz[j], st));
-    HCK(hipStreamSynchronize(st));
-    T->have_grads = false;
+    if (!T) return RH_OK;  // nothing allocated yet: the first backward starts from zero
+    T->zero = true;
     return RH_OK;
 }
 
@@ -382,9 +390,18 @@ int rh_read_grads_f32(rh_ctx* ctx, float* dembed, float* dgamma_final, float* co
     const rh_config& c = ctx->cfg;
     const size_t D = c.dim, F = c.hidden, V = c.vocab;
     hipStream_t st = ctx->stream;
+    const size_t sz[9] = {D * D, D * D, D * D, D * D, D * F, D * F, D * F, D, D};
+    if (T->zero) {
+        if (dembed) std::memset(dembed, 0, V * D * sizeof(float));
+        if (dgamma_final) std::memset(dgamma_final, 0, D * sizeof(float));
+        if (layer_grads)
+            for (int l = 0; l < c.nlayers; ++l)
+                for (int j = 0; j < 9; ++j)
+                    if (layer_grads[9 * l + j]) std::memset(layer_grads[9 * l + j], 0, sz[j] * sizeof(float));
+        return RH_OK;
+    }
     if (dembed) HCK(hipMemcpyAsync(dembed, T->dembed, V * D * sizeof(float), hipMemcpyDeviceToHost, st));
     if (dgamma_final) HCK(hipMemcpyAsync(dgamma_final, T->dgf, D * sizeof(float), hipMemcpyDeviceToHost, st));
-    const size_t sz[9] = {D * D, D * D, D * D, D * D, D * F, D * F, D * F, D, D};
     if (layer_grads)
         for (int l = 0; l < c.nlayers; ++l)
             for (int j = 0; j < 9; ++j)

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void transpose_frag_kernel(const f16* __restri
 // x_hat = x*r; dot = sum(dy*g*x_hat)/D; dx = r*(dy*g - x_hat*dot) (+ dres).
 // Writes dx (fp32, may alias dres), optionally hscale*dx as fp16 in fragment
 // order, and this block's dgamma partial sum(dy*x_hat) over its rows.
-constexpr int RB = 8;
+constexpr int RB = 2;  // rows per block: M/2 blocks keep enough loads in flight
 __global__ __launch_bounds__(256) void rms_backward_kernel(const float* __restrict__ dy, const float* __restrict__ x,
                                                            const float* __restrict__ gamma, const float* dres,
                                                            float* dx, f16* __restrict__ outh, float hscale,
@@ -202,14 +202,26 @@ __global__ __launch_bounds__(256) void rms_backward_kernel(const float* __restri
     }
 }
 
-// dgamma[d] += kappa * sum of the partials in block order (deterministic).
-__global__ void dgamma_reduce_kernel(const float* __restrict__ part, int nblk, int D, float kappa,
-                                     float* __restrict__ dgamma) {
-    const int d = blockIdx.x * blockDim.x + threadIdx.x;
-    if (d >= D) return;
+// dgamma[d] += kappa * sum of the partials (deterministic: 16 fixed strided
+// partial sums per column, then a fixed pairwise tree).  16 columns per
+// block, so D/16 blocks keep enough loads in flight.
+__global__ __launch_bounds__(256) void dgamma_reduce_kernel(const float* __restrict__ part, int nblk, int D,
+                                                            float kappa, float* __restrict__ dgamma, int store) {
+    __shared__ float red[16][17];
+    const int c = threadIdx.x & 15, q = threadIdx.x >> 4, d = blockIdx.x * 16 + c;
     float s = 0.f;
-    for (int b = 0; b < nblk; ++b) s += part[(size_t)b * D + d];
-    dgamma[d] += kappa * s;
+    if (d < D)
+        for (int b = q; b < nblk; b += 16) s += part[(size_t)b * D + d];
+    red[q][c] = s;
+    __syncthreads();
+    for (int h = 8; h > 0; h >>= 1) {
+        if (q < h) red[q][c] += red[q + h][c];
+        __syncthreads();
+    }
+    if (q == 0 && d < D) {
+        const float v = kappa * red[0][c];
+        dgamma[d] = store ? v : dgamma[d] + v;
+    }
 }
 
 // SiLU-gate backward (layer.rs:7083-7104) from the GEMM's dgate [M, F] fp32
@@ -311,8 +323,10 @@ hipError_t launch_rms_backward(const float* dy, const float* x, const float* gam
     return hipGetLastError();
 }
 
-hipError_t launch_dgamma_reduce(const float* part, int nblk, int D, float kappa, float* dgamma, hipStream_t st) {
-    hipLaunchKernelGGL(dgamma_reduce_kernel, dim3((D + 255) / 256), dim3(256), 0, st, part, nblk, D, kappa, dgamma);
+hipError_t launch_dgamma_reduce(const float* part, int nblk, int D, float kappa, float* dgamma, bool store,
+                                hipStream_t st) {
+    hipLaunchKernelGGL(dgamma_reduce_kernel, dim3((D + 15) / 16), dim3(256), 0, st, part, nblk, D, kappa, dgamma,
+                       (int)store);
     return hipGetLastError();
 }
 

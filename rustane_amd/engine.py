@@ -331,6 +331,14 @@ def prefill_flops(cfg: ModelConfig, seq: int | None = None, batch: int = 1) -> d
     return {k: v * batch for k, v in per.items()}
 
 
+def train_step_flops(cfg: ModelConfig, seq: int | None = None, batch: int = 1) -> int:
+    """Algorithmic FLOPs of one forward + backward: every forward product is
+    matched by a data-gradient and a weight-gradient product of the same size
+    (GEMMs and the tied logits), and attention's backward is dQ, dK, dV, dP
+    (twice the forward's QK^T and PV), so 3x the forward's count."""
+    return 3 * prefill_flops(cfg, seq, batch)["total"]
+
+
 def decode_bytes(cfg: ModelConfig, ctx_len: float, batch: int = 1) -> dict:
     """Compulsory HBM bytes of one decode step: fp16 weights (layers + tied
     vocab projection) + per sequence K/V read at ctx_len and the K/V append."""
