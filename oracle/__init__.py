@@ -99,6 +99,16 @@ def lib():
         L.orc_sdpa_backward.argtypes = [ctypes.POINTER(OrcConfig), sz, _f32p, _f32p, _f32p, _f32p,
                                         _f32p, _f32p, _f32p]
         L.orc_rope_backward.argtypes = [ctypes.POINTER(OrcConfig), _f32p, sz]
+        L.orc_adam_step_fused.argtypes = [_f32p, _f32p, _f32p, _f32p, sz, ctypes.c_uint32, ctypes.c_float,
+                                          ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                          ctypes.c_float]
+        L.orc_powi.argtypes = [ctypes.c_float, ctypes.c_uint32]
+        L.orc_powi.restype = ctypes.c_float
+        L.orc_svesq.argtypes = [_f32p, sz]
+        L.orc_svesq.restype = ctypes.c_float
+        L.orc_learning_rate.argtypes = [ctypes.c_uint32, ctypes.c_float, ctypes.c_float, ctypes.c_uint32,
+                                        ctypes.c_uint32]
+        L.orc_learning_rate.restype = ctypes.c_float
         _lib = L
     return _lib
 
@@ -215,3 +225,84 @@ def forward_backward(cfg: OrcConfig, w: Weights, tokens: np.ndarray, targets: np
     if rc != 0:
         raise ValueError(f"orc_forward_backward failed: {rc}")
     return g, ml
+
+
+# ---------------------------------------------------------------- optimizer
+class TrainConfig:
+    """TrainConfig and its defaults (full_model.rs:42-78)."""
+
+    def __init__(self, **kw):
+        self.max_lr, self.min_lr_frac, self.warmup_steps, self.total_steps = 3e-4, 0.1, 100, 10000
+        self.beta1, self.beta2, self.eps, self.weight_decay = 0.9, 0.95, 1e-8, 0.1
+        self.matrix_lr_scale, self.embed_lr_scale, self.loss_scale = 0.05, 5.0, 256.0
+        self.accum_steps, self.grad_clip, self.softcap = 10, 1.0, 0.0
+        for k, v in kw.items():
+            assert hasattr(self, k), k
+            setattr(self, k, v)
+
+
+def adam_step_fused(param, grad, m, v, t, lr, beta1, beta2, eps, wd, grad_scale):
+    """step_fused (cpu/adam.rs:95-132) in place on fp32 numpy arrays."""
+    lib().orc_adam_step_fused(fp(param), fp(grad) if grad is not None else None, fp(m), fp(v), param.size,
+                              int(t), lr, beta1, beta2, eps, wd, grad_scale)
+
+
+def learning_rate(step, tc: TrainConfig) -> float:
+    return float(lib().orc_learning_rate(int(step), tc.max_lr, tc.min_lr_frac, int(tc.warmup_steps),
+                                         int(tc.total_steps)))
+
+
+def grad_norm(g: Grads) -> float:
+    """grad_norm (full_model.rs:1403-1450): per-tensor vDSP_svesq, summed as
+    (embed + gamma_final + first half of the layers) + (second half), sqrt."""
+    sq = lambda a: float(lib().orc_svesq(fp(a), a.size))
+    mid = len(g.layers) // 2
+    s1 = np.float32(sq(g.embed))
+    s1 = np.float32(s1 + np.float32(sq(g.gamma_final)))
+    for lw in g.layers[:mid]:
+        for t in lw:
+            s1 = np.float32(s1 + np.float32(sq(t)))
+    s2 = np.float32(0.0)
+    for lw in g.layers[mid:]:
+        for t in lw:
+            s2 = np.float32(s2 + np.float32(sq(t)))
+    return float(np.sqrt(np.float32(s1 + s2)))
+
+
+class OptState:
+    """ModelOptState: zero first and second moments shaped like the weights."""
+
+    def __init__(self, w: Weights):
+        self.embed_m, self.embed_v = np.zeros_like(w.embed), np.zeros_like(w.embed)
+        self.gf_m, self.gf_v = np.zeros_like(w.gamma_final), np.zeros_like(w.gamma_final)
+        self.m = [[np.zeros_like(t) for t in lw] for lw in w.layers]
+        self.v = [[np.zeros_like(t) for t in lw] for lw in w.layers]
+
+
+def update_weights(w: Weights, g: Grads, o: OptState, t: int, lr: float, tc: TrainConfig, grad_scale: float):
+    """update_weights (full_model.rs:1123-1241) + update_layer (:1243-1400):
+    embed at lr * embed_lr_scale and gamma_final at lr, both without weight
+    decay; per layer the seven matrices at lr * matrix_lr_scale with
+    weight_decay, the two gammas at lr without."""
+    b1, b2, eps = tc.beta1, tc.beta2, tc.eps
+    adam_step_fused(w.embed, g.embed, o.embed_m, o.embed_v, t, lr * tc.embed_lr_scale, b1, b2, eps, 0.0,
+                    grad_scale)
+    adam_step_fused(w.gamma_final, g.gamma_final, o.gf_m, o.gf_v, t, lr, b1, b2, eps, 0.0, grad_scale)
+    for lw, lg, lm, lv in zip(w.layers, g.layers, o.m, o.v):
+        for j in range(9):
+            mat = j < 7
+            adam_step_fused(lw[j], lg[j], lm[j], lv[j], t, lr * tc.matrix_lr_scale if mat else lr, b1, b2, eps,
+                            tc.weight_decay if mat else 0.0, grad_scale)
+
+
+def train_update(w: Weights, g: Grads, o: OptState, step: int, tc: TrainConfig):
+    """The update half of train_step_with_options (full_model.rs:1573-1600):
+    gsc = 1/(accum_steps*loss_scale); clip by the global norm; update_weights
+    at t = step + 1.  Returns (scaled_norm, combined_scale, lr)."""
+    gsc = np.float32(1.0) / (np.float32(tc.accum_steps) * np.float32(tc.loss_scale))
+    raw = np.float32(grad_norm(g))
+    scaled = np.float32(raw * gsc)
+    combined = np.float32(tc.grad_clip) / raw if scaled > np.float32(tc.grad_clip) else gsc
+    lr = learning_rate(step, tc)
+    update_weights(w, g, o, step + 1, lr, tc, float(combined))
+    return float(scaled), float(combined), lr

@@ -20,6 +20,7 @@
 //   cpu/rmsnorm.rs:185-240    rmsnorm::backward_channel_first
 //   cpu/embedding.rs:34-44    embedding::backward_channel_first
 //   kernels/sdpa_bwd.rs:44-300    sdpa backward graphs (probs, dP, dS, dQ, dK, dV)
+//   cpu/adam.rs:95-132        AdamW step_fused;  full_model.rs:903-913 learning_rate
 #include "oracle.h"
 
 #include <cmath>
@@ -761,6 +762,51 @@ void orc_sdpa_backward(const orc_config* cfg, size_t seq, const float* q, const 
 }
 
 void orc_rope_backward(const orc_config* cfg, float* dx, size_t seq) { rope_bwd_rows(cfg, dx, seq); }
+
+float orc_powi(float b, uint32_t t) {
+    float r = 1.0f, x = b;
+    for (uint32_t e = t; e; e >>= 1) {
+        if (e & 1u) r *= x;
+        x *= x;
+    }
+    return r;
+}
+
+// step_fused (cpu/adam.rs:95-132), one element at a time in the reference's
+// operation order (the library is built with -ffp-contract=off, like rustc).
+void orc_adam_step_fused(float* param, const float* grad, float* m, float* v, size_t n, uint32_t t, float lr,
+                         float beta1, float beta2, float eps, float weight_decay, float grad_scale) {
+    const float bc1 = 1.0f / (1.0f - orc_powi(beta1, t));
+    const float bc2 = 1.0f / (1.0f - orc_powi(beta2, t));
+    const float omb1 = 1.0f - beta1, omb2 = 1.0f - beta2;
+#pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n; ++i) {
+        const float g = (grad ? grad[i] : 0.0f) * grad_scale;
+        const float mi = beta1 * m[i] + omb1 * g;
+        const float vi = beta2 * v[i] + omb2 * g * g;
+        m[i] = mi;
+        v[i] = vi;
+        const float m_hat = mi * bc1;
+        const float v_hat = vi * bc2;
+        const float update = m_hat / (std::sqrt(v_hat) + eps);
+        param[i] -= lr * (update + weight_decay * param[i]);
+    }
+}
+
+float orc_svesq(const float* x, size_t n) {
+    float s = 0.f;
+    for (size_t i = 0; i < n; ++i) s += x[i] * x[i];
+    return s;
+}
+
+// learning_rate (full_model.rs:903-913).
+float orc_learning_rate(uint32_t step, float max_lr, float min_lr_frac, uint32_t warmup_steps,
+                        uint32_t total_steps) {
+    if (step < warmup_steps) return max_lr * (float)(step + 1) / (float)warmup_steps;
+    const float decay = (float)(step - warmup_steps) / (float)(total_steps - warmup_steps);
+    const float min_lr = max_lr * min_lr_frac;
+    return min_lr + 0.5f * (1.0f + std::cos(3.14159265358979323846f * decay)) * (max_lr - min_lr);
+}
 
 orc_kv* orc_kv_create(const orc_config* cfg, int max_ctx) {
     if (!cfg || max_ctx <= 0) return nullptr;

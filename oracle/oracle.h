@@ -39,6 +39,11 @@
  *   orc_rmsnorm_backward_*, orc_silu_gate_backward
  *                             reference numerical-gradient KATs (cpu/rmsnorm.rs:278-316,
  *                             cpu/silu.rs:68-90) + float64 autograd
+ *   orc_adam_step_fused       the reference's Adam unit tests (cpu/adam.rs:138-190:
+ *                             moves toward the minimum, weight decay alone shrinks,
+ *                             m = 0.1 and v = 0.001 after one unit-gradient step) +
+ *                             closed form of the first step (|update| = 1 when wd = 0)
+ *   orc_learning_rate         closed form at the warmup and cosine end points
  *   orc_sdpa_backward, orc_rope_backward
  *                             float64 autograd of the textbook forward; RoPE backward
  *                             is the inverse rotation (round trip to identity)
@@ -147,6 +152,23 @@ void orc_sdpa_backward(const orc_config* cfg, size_t seq, const float* q, const 
                        const float* v, const float* da, float* dq, float* dk, float* dv);
 /* rope_backward_inplace (layer.rs:7389-7407), token-major [seq, D]. */
 void orc_rope_backward(const orc_config* cfg, float* dx, size_t seq);
+
+/* ---- optimizer (the training step's update) ---- */
+/* AdamW step_fused (cpu/adam.rs:95-132; the Metal shader metal_adam.rs:16-40
+ * computes the same): g = grad*grad_scale; m = b1*m + (1-b1)*g;
+ * v = b2*v + (1-b2)*g*g; update = (m*bc1) / (sqrt(v*bc2) + eps);
+ * param -= lr*(update + wd*param), bc1 = 1/(1 - b1^t), bc2 = 1/(1 - b2^t).
+ * grad may be NULL (treated as zeros). */
+void orc_adam_step_fused(float* param, const float* grad, float* m, float* v, size_t n, uint32_t t, float lr,
+                         float beta1, float beta2, float eps, float weight_decay, float grad_scale);
+/* b^t by repeated squaring in fp32 (the f32::powi of the bias corrections). */
+float orc_powi(float b, uint32_t t);
+/* vDSP_svesq (cpu/vdsp.rs:329-335): sum of squares in fp32. */
+float orc_svesq(const float* x, size_t n);
+/* learning_rate (full_model.rs:903-913): linear warmup, then cosine to
+ * max_lr * min_lr_frac. */
+float orc_learning_rate(uint32_t step, float max_lr, float min_lr_frac, uint32_t warmup_steps,
+                        uint32_t total_steps);
 
 /* ---- single-token decode with a KV cache (no reference implementation;
  *      contract: logits at step p equal the forward's logits at position p) ---- */
