@@ -132,8 +132,8 @@ def main():
         print(json.dumps({"decode": run_decode(ctx, cfg, args, hb, E, hip_rt, stream)}), flush=True)
         return
     if args.train_only:
-        print(json.dumps({"train_step": {f"B{b}": run_train_step(ctx, cfg, args, E, b) for b in train_b}}),
-              flush=True)
+        tr = {f"B{b}": run_train_step(ctx, cfg, args, E, b) for b in train_b}
+        print(json.dumps({"train_step": tr, "optimizer": run_optimizer(ctx, cfg, hb)}), flush=True)
         return
 
     if args.copy_calibration:
@@ -174,6 +174,7 @@ def main():
         sched = run_scheduler(ctx, cfg, hb, requests=32, max_batch=16)
 
     train = {f"B{b}": run_train_step(ctx, cfg, args, E, b) for b in train_b} if train_b else None
+    optim = run_optimizer(ctx, cfg, hb) if train_b else None
 
     decode = None
     decode_lines = {}
@@ -229,6 +230,8 @@ def main():
         line["scheduler"] = sched
     if train:
         line["train_step"] = train
+    if optim:
+        line["optimizer"] = optim
     if config_lines:
         line["prefill_configs"] = config_lines
     if cpu:
@@ -262,6 +265,34 @@ def run_train_step(ctx, cfg, args, E, B):
            "mfma_frac": round(tf / PEAK_FP16_TFLOPS, 4), "loss": float(loss[0]),
            "first_call_s": round(first, 3)}
     log(f"[bench] train step B={B}: {out}")
+    return out
+
+
+def run_optimizer(ctx, cfg, hb, steps=3):
+    """The optimizer half of a training step over every parameter: the
+    global gradient norm (a read of the fp32 gradients) and the fused AdamW
+    update (per parameter: fp32 grad, m, v, master read; m, v, master written;
+    fp16 device copy written = 30 bytes), timed by wall clock (each call
+    synchronises)."""
+    P = cfg.param_count() - cfg.dim * (2 * cfg.nlayers + 1)  # matrices + embedding
+    G = cfg.param_count()                                      # + gammas
+    tc = hb.train_config()
+    ctx.update_weights(1, 1e-4, tc, 1.0)  # allocates the optimizer state
+    t = time.perf_counter()
+    for i in range(steps):
+        ctx.update_weights(2 + i, 1e-4, tc, 1.0)
+    upd_ms = (time.perf_counter() - t) * 1e3 / steps
+    t = time.perf_counter()
+    for _ in range(steps):
+        ctx.grad_norm()
+    norm_ms = (time.perf_counter() - t) * 1e3 / steps
+    upd_bytes = 30 * P + 28 * (G - P)
+    out = {"update_ms": round(upd_ms, 3), "update_bytes": upd_bytes,
+           "update_gb_s": round(upd_bytes / (upd_ms / 1e3) / 1e9, 1),
+           "update_hbm_frac": round(upd_bytes / (upd_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+           "grad_norm_ms": round(norm_ms, 3), "grad_norm_gb_s": round(4 * G / (norm_ms / 1e3) / 1e9, 1),
+           "params": G}
+    log(f"[bench] optimizer: {out}")
     return out
 
 

@@ -222,6 +222,47 @@ int rh_compute_bpb(const float* losses, const uint32_t* targets, int64_t n, cons
 int rh_validate(rh_ctx* ctx, const rh_tokens* val, const int32_t* token_bytes, int steps,
                 float* avg_loss_out, float* bpb_out);
 
+/* ---- optimizer and training step ---- */
+/* TrainConfig (full_model.rs:42-78). */
+typedef struct {
+    float max_lr, min_lr_frac;
+    uint32_t warmup_steps, total_steps;
+    float beta1, beta2, eps, weight_decay, matrix_lr_scale, embed_lr_scale, loss_scale;
+    uint32_t accum_steps;
+    float grad_clip, softcap;
+} rh_train_config;
+/* TrainConfig::default (full_model.rs:59-78). */
+void rh_train_config_default(rh_train_config* out);
+/* learning_rate (full_model.rs:903-913): linear warmup, cosine decay to
+ * max_lr * min_lr_frac. */
+float rh_learning_rate(uint32_t step, const rh_train_config* tc);
+/* grad_norm (full_model.rs:1403-1450): L2 norm of all gradients (per-tensor
+ * sums of squares added in double; 0 while the gradients are zero). */
+int rh_grad_norm(rh_ctx* ctx, float* norm_out);
+/* update_weights (full_model.rs:1123-1400): one AdamW step_fused
+ * (cpu/adam.rs:95-132) at step count t >= 1 over every parameter, gradients
+ * multiplied by grad_scale: the embedding at lr * embed_lr_scale and the
+ * gammas at lr without weight decay, the seven matrices per layer at
+ * lr * matrix_lr_scale with weight_decay.  The first call allocates the
+ * optimizer state: fp32 master weights (read from the device weights),
+ * first and second moments (zero).  Weights written by rh_load_weights_f32,
+ * rh_init_weights_normal or a checkpoint load reset the masters; the
+ * moments persist.  After an update rh_read_weights_f32 (and
+ * rh_save_checkpoint) return the fp32 masters. */
+int rh_update_weights(rh_ctx* ctx, uint32_t t, float lr, const rh_train_config* tc, float grad_scale);
+/* train_step / train_step_with_options (full_model.rs:1488-1600): zero the
+ * gradients; accum_steps sequences of the context's seq from `data` at
+ * pos = (step * 7919 + micro * 104729) % (len - seq - 1) (inputs
+ * tokens(pos, seq), targets shifted by one), forward + backward with
+ * tc->loss_scale (up to max_batch sequences per launch); clip by the global
+ * norm (combined scale = grad_clip / norm when norm / (accum_steps *
+ * loss_scale) > grad_clip, else 1 / (accum_steps * loss_scale)); AdamW at
+ * t = step + 1 with learning_rate(step).  Sets the softcap to tc->softcap
+ * (as rh_set_softcap).  loss_out: mean loss of the microbatches;
+ * grad_norm_out: the norm divided by accum_steps * loss_scale. */
+int rh_train_step(rh_ctx* ctx, const rh_tokens* data, uint32_t step, const rh_train_config* tc, float* loss_out,
+                  float* grad_norm_out);
+
 /* ---- request scheduler (multistream::ForwardScheduler, multistream.rs:54-161) ----
  * One worker thread owns the context and serves a bounded FIFO in batches:
  * up to max_batch forward requests of equal length run as one rh_forward,

@@ -285,13 +285,15 @@ def update_weights(w: Weights, g: Grads, o: OptState, t: int, lr: float, tc: Tra
     decay; per layer the seven matrices at lr * matrix_lr_scale with
     weight_decay, the two gammas at lr without."""
     b1, b2, eps = tc.beta1, tc.beta2, tc.eps
-    adam_step_fused(w.embed, g.embed, o.embed_m, o.embed_v, t, lr * tc.embed_lr_scale, b1, b2, eps, 0.0,
-                    grad_scale)
+    f32 = np.float32
+    embed_lr = float(f32(lr) * f32(tc.embed_lr_scale))   # fp32 products, as in the reference
+    matrix_lr = float(f32(lr) * f32(tc.matrix_lr_scale))
+    adam_step_fused(w.embed, g.embed, o.embed_m, o.embed_v, t, embed_lr, b1, b2, eps, 0.0, grad_scale)
     adam_step_fused(w.gamma_final, g.gamma_final, o.gf_m, o.gf_v, t, lr, b1, b2, eps, 0.0, grad_scale)
     for lw, lg, lm, lv in zip(w.layers, g.layers, o.m, o.v):
         for j in range(9):
             mat = j < 7
-            adam_step_fused(lw[j], lg[j], lm[j], lv[j], t, lr * tc.matrix_lr_scale if mat else lr, b1, b2, eps,
+            adam_step_fused(lw[j], lg[j], lm[j], lv[j], t, matrix_lr if mat else lr, b1, b2, eps,
                             tc.weight_decay if mat else 0.0, grad_scale)
 
 

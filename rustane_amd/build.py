@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librustane_hip.so")
 
-SOURCES = ["rh_gemm.hip", "rh_attn.hip", "rh_attn_bwd.hip", "rh_gemv.hip", "rh_rowops.hip", "rh_trainops.hip",
+SOURCES = ["rh_gemm.hip", "rh_attn.hip", "rh_attn_bwd.hip", "rh_gemv.hip", "rh_rowops.hip", "rh_trainops.hip", "rh_optim.hip",
            "rh_runtime.cpp", "rh_train.cpp", "rh_data.cpp", "rh_sched.cpp"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

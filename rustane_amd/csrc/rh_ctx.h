@@ -147,6 +147,20 @@ int timed(rh_ctx* ctx, int cls, Fn&& fn) {
     return RH_OK;
 }
 
+// Where weight tensor j (RSTK order, 0..6) of layer l lives on the device:
+// reference orientation [R][C] and its fp16 packing (map -1: rows as is,
+// K = C; map 0/1: transposed to rows dst_row(c), K = ldd, row_off).
+struct TensorMap {
+    int R, C, map, row_off;
+    f16* dst;
+    int ldd;
+};
+TensorMap layer_map(rh_ctx* ctx, int l, int j);
+// The fp32 master copy of weight tensor j of layer l (j = -1: the
+// embedding) kept by the optimizer, or null when there is none or the
+// device weights changed since it was written.
+const float* train_master(const rh_ctx* ctx, int l, int j);
+
 void set_sk(const rh_ctx* ctx, rh::GemmArgs& g);
 int ensure_rope(rh_ctx* ctx, int npos);
 int ensure_workspace(rh_ctx* ctx, int M);

@@ -179,6 +179,25 @@ hipError_t launch_attn_backward(const f16* q, const f16* k, const f16* v, const 
                                 const float* lse, f16* dOh, float* Drow, float* dqkv, int B, int H, int S, int hd,
                                 hipStream_t st);
 
+// ---------------- optimizer ----------------
+// One AdamW step (step_fused) with its constants: omb1 = 1 - beta1,
+// omb2 = 1 - beta2, bc1 = 1/(1 - beta1^t), bc2 = 1/(1 - beta2^t), gradients
+// multiplied by gscale.
+struct AdamArgs {
+    float lr, beta1, beta2, omb1, omb2, eps, wd, gscale, bc1, bc2;
+};
+// Elementwise AdamW over n fp32 values (grad null = zeros); when dst is set
+// also writes the fp16 row-packed copy (fragment order, K columns).
+hipError_t launch_adam_rows(float* p, const float* g, float* m, float* v, size_t n, const AdamArgs& a, f16* dst,
+                            int K, hipStream_t st);
+// AdamW over a [R][C] tensor whose fp16 copy is transposed (the packing of
+// launch_pack_transpose: row dst_row(c), k = r, K = ldd).
+hipError_t launch_adam_transpose(float* p, const float* g, float* m, float* v, int R, int C, const AdamArgs& a,
+                                 f16* dst, int ldd, int map, int row_off, hipStream_t st);
+// Per-block sums of squares of x[0..n) into part[0..sumsq_blocks(n)).
+int sumsq_blocks(size_t n);
+hipError_t launch_sumsq(const float* x, size_t n, float* part, hipStream_t st);
+
 // ---------------- weight packing ----------------
 // Device weights are fp16 [N, K] in fragment order (frag_off in rh_device.h),
 // N padded to a multiple of 16.

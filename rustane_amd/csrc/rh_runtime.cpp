@@ -271,6 +271,21 @@ int run_decode_step(rh_ctx* ctx, int B) {
 
 }  // namespace
 
+rhrt::TensorMap rhrt::layer_map(rh_ctx* ctx, int l, int j) {
+    const int D = ctx->cfg.dim, F = ctx->cfg.hidden;
+    Layer& W = ctx->L[l];
+    switch (j) {
+        case 0: return {D, D, 0, 0, W.wqkv, D};
+        case 1: return {D, D, 0, D, W.wqkv, D};
+        case 2: return {D, D, 0, 2 * D, W.wqkv, D};
+        case 3: return {D, D, 0, 0, W.wo, D};
+        case 4: return {D, F, 1, 0, W.w13, D};
+        case 5: return {D, F, 1, 16, W.w13, D};
+        case 6: return {D, F, -1, 0, W.w2, F};
+    }
+    return {0, 0, -1, 0, nullptr, 0};
+}
+
 int rhrt::check_err_flag(rh_ctx* ctx) {
     int h = 0;
     HCK(hipMemcpyAsync(&h, ctx->d_err, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
@@ -292,27 +307,6 @@ int rhrt::check_tokens(rh_ctx* ctx, const uint32_t* t, size_t n) {
 }
 
 namespace {
-
-struct TensorMap {
-    int R, C, map, row_off;  // reference orientation [R][C]; map 0/1 or -1 for plain
-    f16* dst;
-    int ldd;
-};
-
-TensorMap layer_map(rh_ctx* ctx, int l, int j) {
-    const int D = ctx->cfg.dim, F = ctx->cfg.hidden;
-    Layer& W = ctx->L[l];
-    switch (j) {
-        case 0: return {D, D, 0, 0, W.wqkv, D};
-        case 1: return {D, D, 0, D, W.wqkv, D};
-        case 2: return {D, D, 0, 2 * D, W.wqkv, D};
-        case 3: return {D, D, 0, 0, W.wo, D};
-        case 4: return {D, F, 1, 0, W.w13, D};
-        case 5: return {D, F, 1, 16, W.w13, D};
-        case 6: return {D, F, -1, 0, W.w2, F};
-    }
-    return {0, 0, -1, 0, nullptr, 0};
-}
 
 // staging (fp32, reference orientation) -> device fp16 layout
 int pack_from_staging(rh_ctx* ctx, const TensorMap& m) {
@@ -465,9 +459,15 @@ int rh_read_weights_f32(rh_ctx* ctx, float* embed, float* gamma_final, float* co
     const size_t D = c.dim, F = c.hidden, V = c.vocab;
     RCK(ensure_staging(ctx, std::max({V * D, D * F, D * D})));
     hipStream_t st = ctx->stream;
+    // After optimizer steps the fp32 masters are the weights; otherwise
+    // widen the fp16 device copy.
     if (embed) {
-        LCK(rh::launch_unpack_rows(ctx->embed, ctx->staging, (int)V, (int)D, st));
-        HCK(hipMemcpyAsync(embed, ctx->staging, V * D * sizeof(float), hipMemcpyDeviceToHost, st));
+        const float* src = train_master(ctx, 0, -1);
+        if (!src) {
+            LCK(rh::launch_unpack_rows(ctx->embed, ctx->staging, (int)V, (int)D, st));
+            src = ctx->staging;
+        }
+        HCK(hipMemcpyAsync(embed, src, V * D * sizeof(float), hipMemcpyDeviceToHost, st));
         HCK(hipStreamSynchronize(st));
     }
     if (gamma_final) HCK(hipMemcpyAsync(gamma_final, ctx->gfinal, D * sizeof(float), hipMemcpyDeviceToHost, st));
@@ -477,8 +477,12 @@ int rh_read_weights_f32(rh_ctx* ctx, float* embed, float* gamma_final, float* co
             for (int j = 0; j < 7; ++j) {
                 if (!t[j]) continue;
                 const TensorMap m = layer_map(ctx, l, j);
-                RCK(unpack_to_staging(ctx, m));
-                HCK(hipMemcpyAsync(t[j], ctx->staging, (size_t)m.R * m.C * sizeof(float), hipMemcpyDeviceToHost, st));
+                const float* src = train_master(ctx, l, j);
+                if (!src) {
+                    RCK(unpack_to_staging(ctx, m));
+                    src = ctx->staging;
+                }
+                HCK(hipMemcpyAsync(t[j], src, (size_t)m.R * m.C * sizeof(float), hipMemcpyDeviceToHost, st));
                 HCK(hipStreamSynchronize(st));
             }
             if (t[7]) HCK(hipMemcpyAsync(t[7], ctx->L[l].g1, D * sizeof(float), hipMemcpyDeviceToHost, st));

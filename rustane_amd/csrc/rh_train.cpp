@@ -57,9 +57,26 @@ struct TrainState {
     float *gout = nullptr, *dres = nullptr, *Drow = nullptr, *dgp = nullptr;
     uint32_t* utok = nullptr;
     int *ustart = nullptr, *uidx = nullptr;
+    // optimizer (ModelOptState + the fp32 master weights), created by the first update
+    struct Opt {
+        float* emb = nullptr;                  // master embedding [V][D]
+        std::vector<std::array<float*, 7>> w;  // masters of the 7 matrices per layer
+        float *emb_m = nullptr, *emb_v = nullptr, *gf_m = nullptr, *gf_v = nullptr;
+        std::vector<std::array<float*, 9>> m, v;
+        float* part = nullptr;  // sum-of-squares partials of the gradient norm
+        uint64_t synced = 0;    // weight version the masters hold
+    };
+    Opt* opt = nullptr;
+    ~TrainState() { delete opt; }
 };
 
 void train_state_free(TrainState* t) { delete t; }
+
+const float* train_master(const rh_ctx* ctx, int l, int j) {
+    const TrainState* T = ctx->train;
+    if (!T || !T->opt || T->opt->synced != ctx->wgen) return nullptr;
+    return j < 0 ? T->opt->emb : T->opt->w[l][j];
+}
 
 }  // namespace rhrt
 
@@ -325,9 +342,231 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
     return RH_OK;
 }
 
+const size_t* tensor_sizes(const rh_config& c, size_t out[9]) {
+    const size_t D = c.dim, F = c.hidden;
+    const size_t sz[9] = {D * D, D * D, D * D, D * D, D * F, D * F, D * F, D, D};
+    std::copy(sz, sz + 9, out);
+    return out;
+}
+
+// Optimizer state: moments (zeroed) and fp32 masters, re-read from the
+// device weights whenever those changed outside the optimizer.
+int ensure_opt(rh_ctx* ctx) {
+    RCK(ensure_train_static(ctx));
+    TrainState* T = ctx->train;
+    const rh_config& c = ctx->cfg;
+    const size_t D = c.dim, V = c.vocab;
+    size_t sz[9];
+    tensor_sizes(c, sz);
+    hipStream_t st = ctx->stream;
+    if (!T->opt) {
+        T->opt = new (std::nothrow) TrainState::Opt;
+        if (!T->opt) return fail(ctx, RH_ENOMEM, "out of host memory");
+        auto* o = T->opt;
+        RCK(dalloc(ctx, &o->emb, V * D));
+        RCK(dalloc(ctx, &o->emb_m, V * D));
+        RCK(dalloc(ctx, &o->emb_v, V * D));
+        RCK(dalloc(ctx, &o->gf_m, D));
+        RCK(dalloc(ctx, &o->gf_v, D));
+        o->w.resize(c.nlayers);
+        o->m.resize(c.nlayers);
+        o->v.resize(c.nlayers);
+        size_t nparts = rh::sumsq_blocks(V * D) + rh::sumsq_blocks(D);
+        for (int l = 0; l < c.nlayers; ++l) {
+            for (int j = 0; j < 9; ++j) {
+                if (j < 7) RCK(dalloc(ctx, &o->w[l][j], sz[j]));
+                RCK(dalloc(ctx, &o->m[l][j], sz[j]));
+                RCK(dalloc(ctx, &o->v[l][j], sz[j]));
+                LCK(rh::launch_fill_f32(o->m[l][j], 0.f, sz[j], st));
+                LCK(rh::launch_fill_f32(o->v[l][j], 0.f, sz[j], st));
+                nparts += rh::sumsq_blocks(sz[j]);
+            }
+        }
+        RCK(dalloc(ctx, &o->part, nparts));
+        LCK(rh::launch_fill_f32(o->emb_m, 0.f, V * D, st));
+        LCK(rh::launch_fill_f32(o->emb_v, 0.f, V * D, st));
+        LCK(rh::launch_fill_f32(o->gf_m, 0.f, D, st));
+        LCK(rh::launch_fill_f32(o->gf_v, 0.f, D, st));
+    }
+    auto* o = T->opt;
+    if (o->synced != ctx->wgen) {
+        LCK(rh::launch_unpack_rows(ctx->embed, o->emb, (int)V, (int)D, st));
+        for (int l = 0; l < c.nlayers; ++l)
+            for (int j = 0; j < 7; ++j) {
+                const TensorMap mp = layer_map(ctx, l, j);
+                if (mp.map < 0) {
+                    LCK(rh::launch_unpack_rows(mp.dst, o->w[l][j], mp.R, mp.C, st));
+                } else {
+                    LCK(rh::launch_unpack_transpose(mp.dst, o->w[l][j], mp.R, mp.C, mp.ldd, mp.map, mp.row_off, st));
+                }
+            }
+        o->synced = ctx->wgen;
+    }
+    return RH_OK;
+}
+
+// 1 - b^t in fp32 by repeated squaring (f32::powi of the bias corrections).
+float powi_f32(float b, uint32_t t) {
+    float r = 1.0f, x = b;
+    for (uint32_t e = t; e; e >>= 1) {
+        if (e & 1u) r *= x;
+        x *= x;
+    }
+    return r;
+}
+
 }  // namespace
 
 extern "C" {
+
+void rh_train_config_default(rh_train_config* tc) {
+    if (!tc) return;
+    *tc = rh_train_config{3e-4f, 0.1f, 100u, 10000u, 0.9f, 0.95f, 1e-8f, 0.1f, 0.05f, 5.0f, 256.0f, 10u, 1.0f, 0.0f};
+}
+
+float rh_learning_rate(uint32_t step, const rh_train_config* tc) {
+    if (!tc) return 0.f;
+    if (step < tc->warmup_steps) return tc->max_lr * (float)(step + 1) / (float)tc->warmup_steps;
+    const float decay = (float)(step - tc->warmup_steps) / (float)(tc->total_steps - tc->warmup_steps);
+    const float min_lr = tc->max_lr * tc->min_lr_frac;
+    return min_lr + 0.5f * (1.0f + std::cos(3.14159265358979323846f * decay)) * (tc->max_lr - min_lr);
+}
+
+int rh_grad_norm(rh_ctx* ctx, float* norm_out) {
+    if (!ctx || !norm_out) return fail(ctx, RH_EINVAL, "null argument");
+    TrainState* T = ctx->train;
+    if (!T || !T->dembed || T->zero) {
+        *norm_out = 0.f;
+        return RH_OK;
+    }
+    HCK(hipSetDevice(ctx->device));
+    RCK(ensure_opt(ctx));
+    const rh_config& c = ctx->cfg;
+    size_t sz[9];
+    tensor_sizes(c, sz);
+    hipStream_t st = ctx->stream;
+    // grad_norm's tensor order (full_model.rs:1403-1450)
+    std::vector<std::pair<const float*, size_t>> ts{{T->dembed, (size_t)c.vocab * c.dim}, {T->dgf, (size_t)c.dim}};
+    for (int l = 0; l < c.nlayers; ++l)
+        for (int j = 0; j < 9; ++j) ts.emplace_back(T->dlay[l][j], sz[j]);
+    std::vector<int> nb;
+    size_t off = 0;
+    for (auto& t : ts) {
+        LCK(rh::launch_sumsq(t.first, t.second, T->opt->part + off, st));
+        nb.push_back(rh::sumsq_blocks(t.second));
+        off += nb.back();
+    }
+    std::vector<float> part(off);
+    HCK(hipMemcpyAsync(part.data(), T->opt->part, off * sizeof(float), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
+    double total = 0.0;
+    size_t k = 0;
+    for (int n : nb) {
+        double s = 0.0;
+        for (int i = 0; i < n; ++i) s += part[k++];
+        total += s;
+    }
+    *norm_out = (float)std::sqrt(total);
+    return RH_OK;
+}
+
+int rh_update_weights(rh_ctx* ctx, uint32_t t, float lr, const rh_train_config* tc, float grad_scale) {
+    if (!ctx || !tc) return fail(ctx, RH_EINVAL, "null argument");
+    if (t == 0) return fail(ctx, RH_EINVAL, "the Adam step count t starts at 1");
+    HCK(hipSetDevice(ctx->device));
+    RCK(ensure_opt(ctx));
+    TrainState* T = ctx->train;
+    auto* o = T->opt;
+    const rh_config& c = ctx->cfg;
+    const size_t D = c.dim, V = c.vocab;
+    size_t sz[9];
+    tensor_sizes(c, sz);
+    hipStream_t st = ctx->stream;
+    const bool zg = T->zero;  // gradients logically zero: no grad reads
+    rh::AdamArgs a{};
+    a.beta1 = tc->beta1;
+    a.beta2 = tc->beta2;
+    a.omb1 = 1.0f - tc->beta1;
+    a.omb2 = 1.0f - tc->beta2;
+    a.eps = tc->eps;
+    a.gscale = grad_scale;
+    a.bc1 = 1.0f / (1.0f - powi_f32(tc->beta1, t));
+    a.bc2 = 1.0f / (1.0f - powi_f32(tc->beta2, t));
+    // update_weights (full_model.rs:1123-1241): embed at lr * embed_lr_scale, gamma_final at lr, no decay
+    rh::AdamArgs ae = a;
+    ae.lr = lr * tc->embed_lr_scale;
+    ae.wd = 0.f;
+    LCK(rh::launch_adam_rows(o->emb, zg ? nullptr : T->dembed, o->emb_m, o->emb_v, V * D, ae, ctx->embed, (int)D,
+                             st));
+    rh::AdamArgs ag = a;
+    ag.lr = lr;
+    ag.wd = 0.f;
+    LCK(rh::launch_adam_rows(ctx->gfinal, zg ? nullptr : T->dgf, o->gf_m, o->gf_v, D, ag, nullptr, 0, st));
+    // update_layer (:1243-1400): matrices at lr * matrix_lr_scale with decay, gammas at lr without
+    rh::AdamArgs am = a;
+    am.lr = lr * tc->matrix_lr_scale;
+    am.wd = tc->weight_decay;
+    for (int l = 0; l < c.nlayers; ++l) {
+        for (int j = 0; j < 7; ++j) {
+            const TensorMap mp = layer_map(ctx, l, j);
+            const float* g = zg ? nullptr : T->dlay[l][j];
+            if (mp.map < 0) {
+                LCK(rh::launch_adam_rows(o->w[l][j], g, o->m[l][j], o->v[l][j], sz[j], am, mp.dst, mp.C, st));
+            } else {
+                LCK(rh::launch_adam_transpose(o->w[l][j], g, o->m[l][j], o->v[l][j], mp.R, mp.C, am, mp.dst,
+                                              mp.ldd, mp.map, mp.row_off, st));
+            }
+        }
+        LCK(rh::launch_adam_rows(ctx->L[l].g1, zg ? nullptr : T->dlay[l][7], o->m[l][7], o->v[l][7], D, ag,
+                                 nullptr, 0, st));
+        LCK(rh::launch_adam_rows(ctx->L[l].g2, zg ? nullptr : T->dlay[l][8], o->m[l][8], o->v[l][8], D, ag,
+                                 nullptr, 0, st));
+    }
+    HCK(hipStreamSynchronize(st));
+    ++ctx->wgen;  // the transposed copies of the backward are rebuilt on its next call
+    o->synced = ctx->wgen;
+    return RH_OK;
+}
+
+int rh_train_step(rh_ctx* ctx, const rh_tokens* data, uint32_t step, const rh_train_config* tc, float* loss_out,
+                  float* grad_norm_out) {
+    if (!ctx || !data || !tc) return fail(ctx, RH_EINVAL, "null argument");
+    if (tc->accum_steps == 0 || !(tc->loss_scale > 0.f))
+        return fail(ctx, RH_EINVAL, "accum_steps must be >= 1 and loss_scale > 0");
+    const int S = ctx->cfg.seq;
+    const int64_t n = rh_tokens_len(data);
+    if (n < (int64_t)S + 2) return fail(ctx, RH_ERANGE, "token data shorter than seq + 2");
+    const uint64_t max_pos = (uint64_t)(n - S - 1);
+    RCK(rh_set_softcap(ctx, tc->softcap));
+    RCK(rh_zero_grads(ctx));
+    // train_step_with_options (full_model.rs:1510-1600): accum_steps sequences
+    // at pseudo-random positions (step*7919 + micro*104729) % max_pos, run as
+    // batches of up to max_batch independent sequences.
+    const int mb = std::max(1, std::min<int>((int)tc->accum_steps, ctx->max_batch));
+    std::vector<uint32_t> buf((size_t)S + 1), tok((size_t)mb * S), tgt((size_t)mb * S);
+    std::vector<float> losses(mb);
+    float total = 0.f;
+    for (uint32_t i0 = 0; i0 < tc->accum_steps; i0 += mb) {
+        const int nb = std::min<int>(mb, (int)(tc->accum_steps - i0));
+        for (int j = 0; j < nb; ++j) {
+            const uint64_t pos = ((uint64_t)step * 7919u + (uint64_t)(i0 + j) * 104729u) % max_pos;
+            RCK(rh_tokens_read(data, (int64_t)pos, S + 1, buf.data()));
+            std::memcpy(&tok[(size_t)j * S], buf.data(), (size_t)S * 4);
+            std::memcpy(&tgt[(size_t)j * S], buf.data() + 1, (size_t)S * 4);
+        }
+        RCK(rh_forward_backward(ctx, tok.data(), tgt.data(), nb, S, tc->loss_scale, losses.data()));
+        for (int j = 0; j < nb; ++j) total += losses[j];
+    }
+    const float gsc = 1.0f / ((float)tc->accum_steps * tc->loss_scale);
+    float raw = 0.f;
+    RCK(rh_grad_norm(ctx, &raw));
+    const float scaled = raw * gsc;
+    const float combined = scaled > tc->grad_clip ? tc->grad_clip / raw : gsc;
+    RCK(rh_update_weights(ctx, step + 1, rh_learning_rate(step, tc), tc, combined));
+    if (loss_out) *loss_out = total / (float)tc->accum_steps;
+    if (grad_norm_out) *grad_norm_out = scaled;
+    return RH_OK;
+}
 
 // Zeroing is logical: the next backward's weight-gradient GEMMs and gamma
 // reductions store instead of accumulating, and reads return zeros until

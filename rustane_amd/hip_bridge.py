@@ -48,6 +48,29 @@ class RhCkptInfo(ctypes.Structure):
                 ("file_bytes", ctypes.c_uint64)]
 
 
+class RhTrainConfig(ctypes.Structure):
+    """TrainConfig (full_model.rs:42-78)."""
+    _fields_ = [("max_lr", ctypes.c_float), ("min_lr_frac", ctypes.c_float), ("warmup_steps", ctypes.c_uint32),
+                ("total_steps", ctypes.c_uint32), ("beta1", ctypes.c_float), ("beta2", ctypes.c_float),
+                ("eps", ctypes.c_float), ("weight_decay", ctypes.c_float), ("matrix_lr_scale", ctypes.c_float),
+                ("embed_lr_scale", ctypes.c_float), ("loss_scale", ctypes.c_float),
+                ("accum_steps", ctypes.c_uint32), ("grad_clip", ctypes.c_float), ("softcap", ctypes.c_float)]
+
+
+def train_config(**overrides) -> RhTrainConfig:
+    """TrainConfig::default with fields overridden by keyword."""
+    tc = RhTrainConfig()
+    lib().rh_train_config_default(ctypes.byref(tc))
+    for k, v in overrides.items():
+        assert hasattr(tc, k), k
+        setattr(tc, k, v)
+    return tc
+
+
+def learning_rate(step: int, tc: RhTrainConfig) -> float:
+    return float(lib().rh_learning_rate(step, ctypes.byref(tc)))
+
+
 class RhSchedConfig(ctypes.Structure):
     _fields_ = [("max_batch", ctypes.c_int), ("queue_capacity", ctypes.c_int), ("max_wait_us", ctypes.c_int)]
 
@@ -91,6 +114,15 @@ def lib():
     L.rh_forward.argtypes = [ctxp, _u32p, _u32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p, _f32p]
     L.rh_forward_backward.argtypes = [ctxp, _u32p, _u32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, _f32p]
     L.rh_zero_grads.argtypes = [ctxp]
+    L.rh_train_config_default.argtypes = [ctypes.POINTER(RhTrainConfig)]
+    L.rh_train_config_default.restype = None
+    L.rh_learning_rate.argtypes = [ctypes.c_uint32, ctypes.POINTER(RhTrainConfig)]
+    L.rh_learning_rate.restype = ctypes.c_float
+    L.rh_grad_norm.argtypes = [ctxp, _f32p]
+    L.rh_update_weights.argtypes = [ctxp, ctypes.c_uint32, ctypes.c_float, ctypes.POINTER(RhTrainConfig),
+                                    ctypes.c_float]
+    L.rh_train_step.argtypes = [ctxp, ctypes.c_void_p, ctypes.c_uint32, ctypes.POINTER(RhTrainConfig), _f32p,
+                                _f32p]
     L.rh_read_grads_f32.argtypes = [ctxp, _f32p, _f32p, ctypes.POINTER(_f32p)]
     L.rh_forward_dev.argtypes = [ctxp, _vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]
     L.rh_prefill.argtypes = [ctxp, _u32p, ctypes.c_int, ctypes.c_int, _u32p, _f32p]
@@ -239,6 +271,21 @@ class Context:
         ptrs = (_f32p * len(flat))(*[_f(t) for t in flat])
         self._ck(lib().rh_read_grads_f32(self.h, _f(embed), _f(gf), ptrs), "rh_read_grads_f32")
         return embed, gf, layers
+
+    def grad_norm(self) -> float:
+        out = ctypes.c_float()
+        self._ck(lib().rh_grad_norm(self.h, ctypes.byref(out)), "rh_grad_norm")
+        return out.value
+
+    def update_weights(self, t: int, lr: float, tc: RhTrainConfig, grad_scale: float):
+        self._ck(lib().rh_update_weights(self.h, t, lr, ctypes.byref(tc), grad_scale), "rh_update_weights")
+
+    def train_step(self, data: "TokenData", step: int, tc: RhTrainConfig):
+        """train_step (full_model.rs:1488-1600); returns (mean loss, clipped-norm input)."""
+        loss, norm = ctypes.c_float(), ctypes.c_float()
+        self._ck(lib().rh_train_step(self.h, data.h, step, ctypes.byref(tc), ctypes.byref(loss), ctypes.byref(norm)),
+                 "rh_train_step")
+        return loss.value, norm.value
 
     def init_normal(self, seed: int, std: float = 0.02):
         self._ck(lib().rh_init_weights_normal(self.h, seed, std), "rh_init_weights_normal")

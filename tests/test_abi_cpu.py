@@ -130,6 +130,22 @@ def test_null_context_is_rejected_everywhere(lib):
     assert lib.rh_forward_backward(None, tp, tp, 1, 4, 1.0, None) == hb.RH_EINVAL
     assert lib.rh_zero_grads(None) == hb.RH_EINVAL
     assert lib.rh_read_grads_f32(None, None, None, None) == hb.RH_EINVAL
+    assert lib.rh_grad_norm(None, None) == hb.RH_EINVAL
+    assert lib.rh_update_weights(None, 1, 0.1, None, 1.0) == hb.RH_EINVAL
+    assert lib.rh_train_step(None, None, 0, None, None, None) == hb.RH_EINVAL
+
+
+def test_train_config_defaults_and_schedule():
+    """TrainConfig::default (full_model.rs:59-78) and learning_rate
+    (full_model.rs:903-913) are host-only and run without a GPU."""
+    tc = hb.train_config()
+    assert (tc.max_lr, tc.warmup_steps, tc.total_steps, tc.accum_steps) == (pytest.approx(3e-4), 100, 10000, 10)
+    assert (tc.beta1, tc.beta2, tc.weight_decay) == (pytest.approx(0.9), pytest.approx(0.95), pytest.approx(0.1))
+    assert (tc.loss_scale, tc.grad_clip, tc.softcap) == (256.0, 1.0, 0.0)
+    import oracle
+    otc = oracle.TrainConfig()
+    for step in (0, 1, 50, 99, 100, 101, 2500, 5050, 9999, 10000):
+        assert hb.learning_rate(step, tc) == oracle.learning_rate(step, otc)
 
 
 def test_context_free_errors_are_per_thread(lib):
