@@ -65,44 +65,67 @@ __device__ __forceinline__ int packed_row(int c, int map, int row_off) {
 }
 
 // A [R][C] tensor whose fp16 copy is transposed: element (r, c) goes to row
-// packed_row(c), k = r, K = ldd.  32 x 32 tiles: the update reads and writes
-// rows (coalesced), the fp16 copy is written from the LDS-transposed tile.
+// packed_row(c), k = r, K = ldd.  64 x 64 tiles: the update reads and writes
+// rows with 16-byte accesses (C % 4 == 0), the fp16 copy is written from the
+// LDS-transposed tile as 16-byte runs of 8 consecutive k.
 __global__ __launch_bounds__(256) void adam_transpose_kernel(float* __restrict__ p, const float* __restrict__ g,
                                                              float* __restrict__ m, float* __restrict__ v, int R,
                                                              int C, AdamArgs a, f16* __restrict__ dst, int ldd,
                                                              int map, int row_off) {
-    __shared__ float tile[32][33];
-    const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-    for (int y = ty; y < 32; y += 8) {
-        const int r = r0 + y, c = c0 + tx;
-        float np = 0.f;
+    __shared__ float tile[64][65];
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64, tid = threadIdx.x;
+    const int cq = (tid & 15) * 4, ry = tid >> 4;  // 16 column quads x 16 rows per pass
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        const int rr = ry + 16 * pass, r = r0 + rr, c = c0 + cq;
+        f32x4 np = {};
         if (r < R && c < C) {
             const size_t i = (size_t)r * C + c;
-            float mm = m[i], vv = v[i];
-            np = adam_elem(p[i], g ? g[i] : 0.f, mm, vv, a);
-            p[i] = np;
-            m[i] = mm;
-            v[i] = vv;
+            f32x4 pv = *(const f32x4*)(p + i), mv = *(const f32x4*)(m + i), vv = *(const f32x4*)(v + i);
+            const f32x4 gv = g ? *(const f32x4*)(g + i) : f32x4{};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float me = mv[e], ve = vv[e];
+                pv[e] = adam_elem(pv[e], gv[e], me, ve, a);
+                mv[e] = me;
+                vv[e] = ve;
+            }
+            *(f32x4*)(p + i) = pv;
+            *(f32x4*)(m + i) = mv;
+            *(f32x4*)(v + i) = vv;
+            np = pv;
         }
-        tile[y][tx] = np;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tile[rr][cq + e] = np[e];
     }
     __syncthreads();
-    for (int y = ty; y < 32; y += 8) {
-        const int c = c0 + y, r = r0 + tx;
-        if (c < C && r < R) dst[frag_off(packed_row(c, map, row_off), r, ldd)] = (f16)tile[tx][y];
+    // 64 columns x 8 runs of 8 rows: two 16-byte stores per thread
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        const int u = tid + 256 * pass, cc = u >> 3, rg = (u & 7) * 8;
+        const int c = c0 + cc, r = r0 + rg;
+        if (c < C && r < R) {
+            f16x8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (f16)tile[rg + e][cc];
+            *(f16x8*)(dst + frag_off(packed_row(c, map, row_off), r, ldd)) = o;
+        }
     }
 }
 
-// Sum of squares of x[0..n): block b covers [b*chunk, (b+1)*chunk).
+// Sum of squares of x[0..n) (n % 4 == 0): block b covers 16-byte groups
+// [b*chunk, (b+1)*chunk), four independent accumulators per thread.
 __global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ x, size_t n, size_t chunk,
                                                     float* __restrict__ part) {
     __shared__ float red[4];
-    const size_t b0 = blockIdx.x * chunk, b1 = min(n, b0 + chunk);
-    float s = 0.f;
-    for (size_t i = b0 + threadIdx.x; i < b1; i += 256) s += x[i] * x[i];
-    s = block_sum_256(s, red);
-    if (threadIdx.x == 0) part[blockIdx.x] = s;
+    const size_t n4 = n / 4, b0 = blockIdx.x * chunk, b1 = min(n4, b0 + chunk);
+    f32x4 s = {};
+    for (size_t i = b0 + threadIdx.x; i < b1; i += 256) {
+        const f32x4 v = *(const f32x4*)(x + 4 * i);
+        s += v * v;
+    }
+    const float t = block_sum_256((s[0] + s[1]) + (s[2] + s[3]), red);
+    if (threadIdx.x == 0) part[blockIdx.x] = t;
 }
 
 int grid_for(size_t n, int per) {
@@ -121,17 +144,19 @@ hipError_t launch_adam_rows(float* p, const float* g, float* m, float* v, size_t
 
 hipError_t launch_adam_transpose(float* p, const float* g, float* m, float* v, int R, int C, const AdamArgs& a,
                                  f16* dst, int ldd, int map, int row_off, hipStream_t st) {
-    if (!dst || ldd % 128 != 0) return hipErrorInvalidValue;
-    const dim3 grid((C + 31) / 32, (R + 31) / 32);
+    // rows in runs of 8 (R % 8) and 16-byte column quads (C % 4)
+    if (!dst || ldd % 128 != 0 || R % 8 != 0 || C % 4 != 0) return hipErrorInvalidValue;
+    const dim3 grid((C + 63) / 64, (R + 63) / 64);
     hipLaunchKernelGGL(adam_transpose_kernel, grid, dim3(256), 0, st, p, g, m, v, R, C, a, dst, ldd, map, row_off);
     return hipGetLastError();
 }
 
-int sumsq_blocks(size_t n) { return (int)std::min<size_t>(1024, (n + 4095) / 4096); }
+int sumsq_blocks(size_t n) { return (int)std::min<size_t>(2048, (n + 8191) / 8192); }
 
 hipError_t launch_sumsq(const float* x, size_t n, float* part, hipStream_t st) {
+    if (n % 4 != 0 || n == 0) return hipErrorInvalidValue;
     const int nb = sumsq_blocks(n);
-    const size_t chunk = (n + nb - 1) / nb;
+    const size_t chunk = (n / 4 + nb - 1) / nb;
     hipLaunchKernelGGL(sumsq_kernel, dim3(nb), dim3(256), 0, st, x, n, chunk, part);
     return hipGetLastError();
 }
