@@ -190,6 +190,7 @@ def main():
 
     cpu = None if args.no_cpu else cpu_baseline(cfg, args)
     cpu_dec = None if (args.no_cpu or args.no_decode) else cpu_baseline_decode(cfg, args)
+    cpu_train = None if (args.no_cpu or not train_b) else cpu_baseline_train(cfg, args)
 
     line = {
         "metric": "prefill tok/s @7B seq512 fp16 (%MFMA); decode tok/s @7B b1 ctx2048 (%HBM)",
@@ -238,6 +239,8 @@ def main():
         line["cpu_baseline"] = cpu
     if cpu_dec:
         line["cpu_baseline_decode"] = cpu_dec
+    if cpu_train:
+        line["cpu_baseline_train"] = cpu_train
     print(json.dumps(line), flush=True)
 
 
@@ -448,6 +451,41 @@ def cpu_baseline(cfg, args):
             "sample": f"oracle fp32 forward at dim {D}/hidden {F}/vocab {V}/seq {S} with 1 and 2 layers "
                       f"({times[1]:.2f}s, {times[2]:.2f}s), extrapolated linearly to {cfg.nlayers} layers "
                       f"({t_total:.1f}s per forward)"}
+
+
+def cpu_baseline_train(cfg, args):
+    """Oracle forward + backward (fp32, all host cores) at the same shape over
+    a bounded sample: 1 and 2 layers at seq 512, extrapolated linearly."""
+    try:
+        import oracle
+    except Exception as e:  # pragma: no cover
+        log(f"[bench] no oracle: {e}")
+        return None
+    oracle.build()
+    D, F, V, S = cfg.dim, cfg.hidden, cfg.vocab, cfg.seq
+    rng = np.random.default_rng(6)
+
+    def mat(*s):
+        return (rng.standard_normal(s, dtype=np.float32) * np.float32(0.02))
+
+    lw = [mat(D, D), mat(D, D), mat(D, D), mat(D, D), mat(D, F), mat(D, F), mat(D, F),
+          np.ones(D, np.float32), np.ones(D, np.float32)]
+    embed = mat(V, D)
+    tok = rng.integers(0, V, size=(1, S + 1)).astype(np.uint32)
+    times = {}
+    for nl in (1, 2):
+        ocfg = oracle.make_config(D, F, cfg.heads, nl, V, head_dim=cfg.hd)
+        w = oracle.Weights(embed, np.ones(D, np.float32), [lw] * nl)
+        t = time.perf_counter()
+        oracle.forward_backward(ocfg, w, np.ascontiguousarray(tok[:, :-1]), np.ascontiguousarray(tok[:, 1:]))
+        times[nl] = time.perf_counter() - t
+    t_layer = max(times[2] - times[1], 1e-9)
+    t_total = times[1] + (cfg.nlayers - 1) * t_layer
+    return {"value": round(S / t_total, 2), "unit": "tok/s", "cores": int(oracle.lib().orc_num_threads()),
+            "kind": "port",
+            "sample": f"oracle fp32 forward + backward at dim {D}/hidden {F}/vocab {V}/seq {S} with 1 and 2 "
+                      f"layers ({times[1]:.2f}s, {times[2]:.2f}s), extrapolated linearly to {cfg.nlayers} "
+                      f"layers ({t_total:.1f}s per step)"}
 
 
 def cpu_baseline_decode(cfg, args, steps=4):

@@ -7,7 +7,9 @@
 //
 // Prefill: flash-style online softmax.  A block owns 64 queries of one
 // (sequence, head), 4 waves x 16 queries, and walks 64-key blocks up to the
-// causal limit with K and V^T resident in LDS.  The MFMAs compute the
+// causal limit with K and V resident in LDS (head dim 128: moved by DMA into
+// swizzled [key][hd] tiles, V^T fragments by the transposing LDS read; head
+// dim 64: staged through registers, V stored transposed).  The MFMAs compute the
 // transposed problem (S^T = K Q^T, O^T = V^T P^T) so that every lane owns one
 // query column throughout: the softmax row statistics, the rescaling of O and
 // the fp16 P operand all stay lane-local, and the row reductions are two
@@ -227,6 +229,231 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
     }
 }
 
+// Prefill attention for head dim 128 with K and V moved global -> LDS by DMA
+// (global_load_lds_dwordx4) through an NS-stage pipeline, so no VGPRs or LDS
+// store instructions stage them and NS - 1 key blocks are in flight while
+// one is computed.  The math, the MFMA arrangement (S^T = K Q^T, O^T = V^T P^T,
+// one query column per lane) and the lazy rescale are those of
+// attn_prefill_kernel; what changes is how the operands reach the MFMAs:
+//   * K and V sit in LDS in their natural [key][hd] order (256 B rows), as the
+//     DMA writes 1 KB per instruction (4 rows).  16-byte chunks are XOR
+//     swizzled per row by permuting each lane's global address, so the
+//     fragment reads below hit distinct banks: K chunk c of row k is stored at
+//     c ^ swz_k(k), V chunk c at c ^ swz_v(k).
+//   * V^T fragments come from the gfx950 transposing LDS read
+//     ds_read_b64_tr_b16: within each 16-lane group, result element e of lane
+//     m is element m % 4 of the 8 bytes read by lane 4e + m / 4.  Lane l of
+//     group g therefore reads hd 16j + 4(l % 4) .. +3 of key 32c + 8g + 4h +
+//     (l % 16) / 4, and gets V[32c + 8g + 4h + e][16j + l % 16] for e = 0..3:
+//     two reads (h = 0, 1) make the 8-key k slice of the O^T MFMA's A operand.
+__device__ __forceinline__ int swz_k(int row) { return (row & 3) | (((row >> 3) & 3) << 2); }
+__device__ __forceinline__ int swz_v(int row) { return ((row & 3) << 1) | (((row >> 3) & 1) << 3); }
+
+// s_waitcnt vmcnt(n), other counters left at their maximum
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+template <int NS>
+__global__ __launch_bounds__(256) void attn_prefill_dma_kernel(const f16* __restrict__ Q,
+                                                               const f16* __restrict__ Kc,
+                                                               const f16* __restrict__ Vc,
+                                                               f16* __restrict__ out, float* __restrict__ lse,
+                                                               int H, int S, int ctx, float scale_log2) {
+    constexpr int HD = 128, KB = 64, NKK = HD / 32, NHT = HD / 16;
+    constexpr int TILE = KB * HD;  // halves of one K or V block (16 KB)
+    static_assert(NS == 2 || NS == 3, "2 or 3 stages");
+    // one LDS array per stage and operand: the compiler's wait-count pass then
+    // knows a stage's reads do not alias the DMA filling another stage (one
+    // array would make it drain every DMA before the first read)
+    __shared__ __attribute__((aligned(1024))) f16 sK0[TILE], sV0[TILE], sK1[TILE], sV1[TILE], sK2[TILE], sV2[TILE];
+    auto kbuf = [&](auto I) -> f16* {
+        if constexpr (decltype(I)::value == 0) return sK0;
+        else if constexpr (decltype(I)::value == 1) return sK1;
+        else return sK2;
+    };
+    auto vbuf = [&](auto I) -> f16* {
+        if constexpr (decltype(I)::value == 0) return sV0;
+        else if constexpr (decltype(I)::value == 1) return sV1;
+        else return sV2;
+    };
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r = lane & 15;
+    const int nqt = (S + 63) / 64;
+    // 1-D grid: the query tiles of one (sequence, head) are consecutive
+    // logical tiles, which xcd_remap puts on one XCD, so that XCD's L2 serves
+    // their shared K and V (measured 13.1 -> 11.5 us at 7B, B 1, S 512; 144 ->
+    // 98 us at B 16); within a head the longest rows come first
+    const int t = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int bhi = t / nqt, qt = nqt - 1 - t % nqt;
+    const int h = bhi % H, b = bhi / H;
+    const int q0 = qt * 64;
+    const int qi = q0 + w * 16 + r;
+    const size_t bh = (size_t)b * H + h;
+    const f16* Kb = Kc + bh * ctx * HD;
+    const f16* Vb = Vc + bh * ctx * HD;
+
+    f16x8 qf[NKK];
+    {
+        const f16x8 z = {};
+        const f16* qp = Q + (bh * S + (qi < S ? qi : 0)) * HD + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) qf[kk] = qi < S ? *(const f16x8*)(qp + kk * 32) : z;
+    }
+    f32x4 o[NHT];
+#pragma unroll
+    for (int j = 0; j < NHT; ++j) o[j] = f32x4{};
+    float m_run = -INFINITY, l_run = 0.f;
+
+    const int kend = min(S, q0 + 64);
+    const int nkb = (kend + KB - 1) / KB;
+    // Wave w moves 1 KB units w, w + 4, w + 8, w + 12 of the K block and of the
+    // V block (8 DMA instructions per stage); unit i holds rows 4i..4i+3, lane L
+    // row 4i + L/16 and stored chunk L%16.  Keys past the sequence read the
+    // last row (masked below).
+    auto issue = [&](int kb, auto ST) {
+        const int k0 = kb * KB;
+        f16* dk = kbuf(ST);
+        f16* dv = vbuf(ST);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int i = w + 4 * t, row = 4 * i + (lane >> 4);
+            const size_t key = (size_t)min(k0 + row, S - 1);
+            __builtin_amdgcn_global_load_lds((const void*)(Kb + key * HD + 8 * ((lane & 15) ^ swz_k(row))),
+                                             (__attribute__((address_space(3))) void*)(dk + i * 512), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(Vb + key * HD + 8 * ((lane & 15) ^ swz_v(row))),
+                                             (__attribute__((address_space(3))) void*)(dv + i * 512), 16, 0, 0);
+        }
+    };
+    issue(0, std::integral_constant<int, 0>{});  // nkb >= 1
+    if constexpr (NS == 3)
+        if (nkb > 1) issue(1, std::integral_constant<int, 1>{});
+
+    // one key block on stage ST (a compile-time buffer choice)
+    auto step = [&](int kb, auto ST) {
+        constexpr int cur = decltype(ST)::value;
+        const int k0 = kb * KB;
+        // this wave's 8 DMAs of stage kb have landed when at most 8 per stage
+        // issued after it are outstanding; the barrier publishes every wave's
+        // and retires every wave's reads of stage kb - 1, whose buffer the
+        // next issue refills
+        const int ahead = min(NS - 2, nkb - 1 - kb);
+        if (ahead >= 2) wait_vm<16>();
+        else if (ahead == 1) wait_vm<8>();
+        else wait_vm<0>();
+        lds_barrier();
+        if (kb + NS - 1 < nkb) issue(kb + NS - 1, std::integral_constant<int, (cur + NS - 1) % NS>{});
+        const f16* sK = kbuf(ST);
+        const f16* sV = vbuf(ST);
+
+        f16x8 kf[2][2][NKK];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int krow = 32 * c + 8 * (r >> 2) + 4 * u + (r & 3);
+#pragma unroll
+                for (int kk = 0; kk < NKK; ++kk)
+                    kf[c][u][kk] = *(const f16x8*)&sK[krow * HD + 8 * ((4 * kk + g) ^ swz_k(krow))];
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 sc[2][2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) sc[c][u] = f32x4{};
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) sc[c][u] = mfma16(kf[c][u][kk], qf[kk], sc[c][u]);
+        __builtin_amdgcn_sched_barrier(0);
+        f16x8 vf[2][NHT];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int j = 0; j < NHT; ++j) {
+                const int ch = 2 * j + ((lane & 3) >> 1);
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int key = 32 * c + 8 * g + 4 * hh + (r >> 2);
+                    const f16* a = &sV[key * HD + 8 * (ch ^ swz_v(key)) + 4 * (lane & 1)];
+                    const s16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4*)a);
+                    const f16x4 tv = __builtin_bit_cast(f16x4, t);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) vf[c][j][4 * hh + e] = tv[e];
+                }
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        const int lim = min(qi, S - 1) - k0 - 8 * g;
+        auto block_max = [&](auto diag) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if constexpr (decltype(diag)::value)
+                            if (32 * c + 4 * u + i > lim) sc[c][u][i] = -INFINITY;
+                        mx = fmaxf(mx, sc[c][u][i]);
+                    }
+            return mx;
+        };
+        float mloc = (k0 + KB > q0 || k0 + KB > S) ? block_max(std::true_type{}) : block_max(std::false_type{});
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, RH_WAVE));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, RH_WAVE));
+        mloc *= scale_log2;
+        if (__any(mloc > m_run + 8.0f)) {
+            const float m_new = fmaxf(m_run, mloc);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int j = 0; j < NHT; ++j) o[j] *= alpha;
+            m_run = m_new;
+        }
+        float psum = 0.f;
+        f16x8 pf[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[c][u][i], scale_log2, -m_run));
+                    psum += p;
+                    pf[c][4 * u + i] = (f16)p;
+                }
+        l_run += psum;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int j = 0; j < NHT; ++j) o[j] = mfma16(vf[c][j], pf[c], o[j]);
+    };
+    for (int kb0 = 0; kb0 < nkb; kb0 += NS) {
+        step(kb0, std::integral_constant<int, 0>{});
+        if (kb0 + 1 < nkb) step(kb0 + 1, std::integral_constant<int, 1>{});
+        if constexpr (NS == 3)
+            if (kb0 + 2 < nkb) step(kb0 + 2, std::integral_constant<int, 2>{});
+    }
+    float lt = l_run + __shfl_xor(l_run, 16, RH_WAVE);
+    lt += __shfl_xor(lt, 32, RH_WAVE);
+    if (qi < S) {
+        if (lse && g == 0) lse[bh * S + qi] = m_run + log2f(lt);
+        const float inv = 1.0f / lt;
+        const int row = b * S + qi;
+#pragma unroll
+        for (int j = 0; j < NHT; ++j)
+            *(f16x4*)(out + frag_off(row, h * HD + 16 * j + 4 * g, H * HD)) =
+                f16x4{(f16)(o[j][0] * inv), (f16)(o[j][1] * inv), (f16)(o[j][2] * inv), (f16)(o[j][3] * inv)};
+    }
+}
+
 // Decode attention: one block per (chunk of DCH positions, head, sequence),
 // 4 waves.  Lane = LPP * slot + j: j owns dims 8j..8j+7 of one position
 // (16-byte K/V loads), so a wave covers 64 / LPP positions per pass.  Each
@@ -352,8 +579,11 @@ hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* ou
     const dim3 grid((S + 63) / 64, H, B);
     const float sl2 = (1.0f / sqrtf((float)hd)) * LOG2E;
     constexpr int PF = 1;  // deeper register prefetch measured no faster
+    // hd 128: DMA pipeline with 2 stages (64 KB of LDS, two blocks per CU; 3
+    // stages measured slower at every shape for the lost occupancy)
     if (hd == 128)
-        hipLaunchKernelGGL((attn_prefill_kernel<128, PF>), grid, dim3(256), 0, st, q, k, v, out, lse, H, S, ctx, sl2);
+        hipLaunchKernelGGL((attn_prefill_dma_kernel<2>), dim3((S + 63) / 64 * H * B), dim3(256), 0, st, q, k, v, out,
+                           lse, H, S, ctx, sl2);
     else if (hd == 64)
         hipLaunchKernelGGL((attn_prefill_kernel<64, PF>), grid, dim3(256), 0, st, q, k, v, out, lse, H, S, ctx, sl2);
     else

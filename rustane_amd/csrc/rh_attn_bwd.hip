@@ -71,8 +71,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const f16* __restrict_
     __shared__ __attribute__((aligned(16))) f16 sKt[HD * LT];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r = lane & 15;
     const int nqt = (S + 63) / 64;
-    const int qt = nqt - 1 - (int)blockIdx.x;  // longest rows first
-    const int h = blockIdx.y, b = blockIdx.z;
+    // 1-D grid: one (sequence, head)'s tiles are consecutive logical tiles on
+    // one XCD (xcd_remap), whose L2 then serves their shared K and V
+    const int t = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int qt = nqt - 1 - t % nqt;  // longest rows first
+    const int h = (t / nqt) % H, b = t / nqt / H;
     const int q0 = qt * 64, qi = q0 + w * 16 + r, qrow = min(qi, S - 1);
     const size_t bh = (size_t)b * H + h;
     const f16* Kb = K + bh * S * HD;
@@ -150,8 +153,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const f16* __restric
     __shared__ __attribute__((aligned(16))) f16 sdOt[HD * LT];
     __shared__ float sL[QB], sD[QB];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r = lane & 15;
-    const int kt = blockIdx.x;  // the first key blocks see the most queries: launched first
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int nkt = (S + 63) / 64;
+    const int t = xcd_remap((int)blockIdx.x, (int)gridDim.x);  // a head's tiles share an XCD's L2
+    const int kt = t % nkt;  // the first key blocks see the most queries: launched first
+    const int h = (t / nkt) % H, b = t / nkt / H;
     const int k0 = kt * 64, ki = k0 + w * 16 + r, krow = min(ki, S - 1);
     const size_t bh = (size_t)b * H + h;
     const f16* Qb = Q + bh * S * HD;
@@ -260,7 +265,7 @@ hipError_t launch_attn_backward(const f16* q, const f16* k, const f16* v, const 
                        B, H, S, hd);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 grid((S + 63) / 64, H, B);
+    const dim3 grid((S + 63) / 64 * H * B);
     const float scale = 1.0f / sqrtf((float)hd), sl2 = scale * 1.4426950408889634f;
     if (hd == 128) {
         hipLaunchKernelGGL((attn_bwd_dq_kernel<128>), grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S,
