@@ -67,6 +67,8 @@ def main():
                     help="time only the training step (forward + backward)")
     ap.add_argument("--train-steps", type=int, default=5)
     ap.add_argument("--train-batches", default="1,4", help="batches of the training-step timing")
+    ap.add_argument("--train-max-batch", type=int, default=10,
+                    help="context batch capacity in --train-only runs (>= 10 adds the accum-10 train step)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run three 256 MiB device-to-device copies (a known-size kernel "
                          "for scaling hardware byte counters)")
@@ -90,7 +92,8 @@ def main():
     extra = [int(x) for x in args.extra_batches.split(",") if x]
     extra_dec = [] if args.no_decode else [int(x) for x in args.extra_decode_batches.split(",") if x]
     train_b = [int(x) for x in args.train_batches.split(",") if x] if (args.train_only or not args.no_extra) else []
-    max_batch = max([args.batch, args.decode_batch] + extra + extra_dec + train_b)
+    max_batch = max([args.batch, args.decode_batch] + extra + extra_dec + train_b +
+                    ([args.train_max_batch] if args.train_only else []))
     max_ctx = 0 if args.no_decode else args.decode_ctx + args.decode_steps
     log(f"[bench] config={args.config} B={args.batch} S={cfg.seq} max_ctx={max_ctx}")
     t0 = time.time()
@@ -133,7 +136,10 @@ def main():
         return
     if args.train_only:
         tr = {f"B{b}": run_train_step(ctx, cfg, args, E, b) for b in train_b}
-        print(json.dumps({"train_step": tr, "optimizer": run_optimizer(ctx, cfg, hb)}), flush=True)
+        out = {"train_step": tr, "optimizer": run_optimizer(ctx, cfg, hb)}
+        if ctx.max_batch >= 10:
+            out["train_step_accum10"] = run_train_full(ctx, cfg, hb, E)
+        print(json.dumps(out), flush=True)
         return
 
     if args.copy_calibration:
@@ -175,6 +181,7 @@ def main():
 
     train = {f"B{b}": run_train_step(ctx, cfg, args, E, b) for b in train_b} if train_b else None
     optim = run_optimizer(ctx, cfg, hb) if train_b else None
+    train_full = run_train_full(ctx, cfg, hb, E) if (train_b and max_batch >= 10) else None
 
     decode = None
     decode_lines = {}
@@ -233,6 +240,8 @@ def main():
         line["train_step"] = train
     if optim:
         line["optimizer"] = optim
+    if train_full:
+        line["train_step_accum10"] = train_full
     if config_lines:
         line["prefill_configs"] = config_lines
     if cpu:
@@ -296,6 +305,33 @@ def run_optimizer(ctx, cfg, hb, steps=3):
            "grad_norm_ms": round(norm_ms, 3), "grad_norm_gb_s": round(4 * G / (norm_ms / 1e3) / 1e9, 1),
            "params": G}
     log(f"[bench] optimizer: {out}")
+    return out
+
+
+def run_train_full(ctx, cfg, hb, E, steps=3):
+    """rh_train_step with TrainConfig's defaults (accum_steps 10: ten
+    sequences per optimizer step, run as one batch, then the norm, clip and
+    AdamW) over a synthetic uint16 token file, timed by wall clock."""
+    import tempfile
+    tc = hb.train_config()
+    n = max(64 * cfg.seq, 200000)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "train.bin")
+        np.random.default_rng(8).integers(0, cfg.vocab, size=n).astype("<u2").tofile(path)
+        data = hb.TokenData(path)
+        ctx.train_step(data, 0, tc)  # warm-up (and state allocation)
+        t = time.perf_counter()
+        for s in range(1, steps + 1):
+            loss, norm = ctx.train_step(data, s, tc)
+        ms = (time.perf_counter() - t) * 1e3 / steps
+        data.close()
+    toks = tc.accum_steps * cfg.seq
+    flops = E.train_step_flops(cfg, cfg.seq, tc.accum_steps)
+    out = {"ms_per_step": round(ms, 2), "tok_s": round(toks / (ms / 1e3), 1), "accum_steps": tc.accum_steps,
+           "tokens_per_step": toks, "achieved_tflops": round(flops / (ms / 1e3) / 1e12, 1),
+           "mfma_frac": round(flops / (ms / 1e3) / 1e12 / PEAK_FP16_TFLOPS, 4), "loss": round(loss, 4),
+           "grad_norm": round(norm, 4)}
+    log(f"[bench] train_step (accum {tc.accum_steps}): {out}")
     return out
 
 
