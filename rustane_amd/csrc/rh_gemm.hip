@@ -13,7 +13,8 @@
 //
 // Tile policy: DTile (below) -- both operands in fragment order in HBM, moved
 // global -> LDS by DMA through a 4-stage pipeline of 32-wide k slices,
-// 32x32x16 MFMA on fragments double-buffered in registers.  Instantiated as
+// 32x32x16 MFMA (16x16x32 for the 192x256 tile) on fragments double-buffered
+// in registers.  Instantiated as
 // 256x256 (8 waves of 128x64, or 4 waves of 128x128 with AGPR accumulators),
 // 256x128, 192x256, 192x128 and 128x128; a cost model picks one per shape.
 // Out-of-range rows are clamped, not predicated (they only feed accumulator
@@ -27,6 +28,7 @@
 // kernel: on this multi-XCD part the per-XCD L2s are not coherent, and a
 // device-scope fence costs an L2 writeback + invalidate.
 #include <algorithm>
+#include <type_traits>
 
 #include "rh_device.h"
 #include "rh_kernels.h"
@@ -39,6 +41,11 @@ constexpr int SK_P = 256;  // stream-K blocks: one per CU
 template <int TN, int TM>
 struct Frag {
     f32x16 v[TN][TM];
+};
+// Accumulators of the 16x16x32 form: NA x NB tiles of 16 x 16.
+template <int NA, int NB>
+struct Frag16 {
+    f32x4 v[NA][NB];
 };
 
 // ---------------------------------------------------------------------------
@@ -55,8 +62,17 @@ struct Frag {
 // stages behind it stay in flight), then the barrier publishes every wave's.
 // The stages are separate LDS arrays so the compiler's own wait-count
 // tracking can tell them apart and adds no drain of its own.
-template <int WGN, int WGM, int TN, int TM>
+//
+// M16 selects the MFMA shape.  false: 32x32x16 (a 32x32 output tile per
+// instruction; operand lane 32h + r reads lane 16(2s + h) + r%16 of
+// fragment r/16 at k16-step s).  true: 16x16x32, whose operand layout is the
+// fragment itself (lane l: row l%16, k 8(l/16)..+7), so each operand is one
+// 1 KB fragment read as is; same tile sizes, operand bytes and accumulator
+// registers, a different output layout (epilogue16).
+template <int WGN, int WGM, int TN, int TM, bool M16 = false>
 struct DTile {
+    static constexpr bool kM16 = M16;
+    static constexpr int NA = 2 * TN, NB = 2 * TM;  // 16-wide A / B tiles per wave (M16)
     static constexpr int BN = 32 * TN * WGN, BM = 32 * TM * WGM, NT = 64 * WGN * WGM;
     static constexpr int FTN = TN, FTM = TM, KI = 32, NS = 4;
     static constexpr int NWF = BN / 16, NXF = BM / 16, NWAVE = WGN * WGM;
@@ -65,7 +81,7 @@ struct DTile {
     // same LDS place), so every wave issues the same count and vmcnt stays exact.
     static constexpr int LPS = (NWF + NXF + NWAVE - 1) / NWAVE;
     static constexpr int SH = (NWF + NXF) * 512;     // halves per stage
-    using Acc = Frag<TN, TM>;
+    using Acc = std::conditional_t<M16, Frag16<NA, NB>, Frag<TN, TM>>;
     struct Smem {};
     __device__ static int nw(int n0) { return n0 + ((threadIdx.x >> 6) % WGN) * 32 * TN; }
     __device__ static int mw(int m0) { return m0 + ((threadIdx.x >> 6) / WGN) * 32 * TM; }
@@ -97,12 +113,21 @@ struct DTile {
             }
         }
         const int r = lane & 31, h = lane >> 5;
-        int ao[TN], bo[TM];
+        constexpr int AO = M16 ? NA : TN, BO = M16 ? NB : TM;
+        int ao[AO], bo[BO];
+        if constexpr (M16) {
 #pragma unroll
-        for (int i = 0; i < TN; ++i) ao[i] = (((wn * 32 * TN + 32 * i) >> 4) + (r >> 4)) * 512 + 128 * h + 8 * (r & 15);
+            for (int i = 0; i < NA; ++i) ao[i] = (wn * NA + i) * 512 + 8 * lane;
 #pragma unroll
-        for (int j = 0; j < TM; ++j)
-            bo[j] = (NWF + ((wm * 32 * TM + 32 * j) >> 4) + (r >> 4)) * 512 + 128 * h + 8 * (r & 15);
+            for (int j = 0; j < NB; ++j) bo[j] = (NWF + wm * NB + j) * 512 + 8 * lane;
+        } else {
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+                ao[i] = (((wn * 32 * TN + 32 * i) >> 4) + (r >> 4)) * 512 + 128 * h + 8 * (r & 15);
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+                bo[j] = (NWF + ((wm * 32 * TM + 32 * j) >> 4) + (r >> 4)) * 512 + 128 * h + 8 * (r & 15);
+        }
         auto buf = [&](int s) -> f16* { return s == 0 ? st0 : s == 1 ? st1 : s == 2 ? st2 : st3; };
         auto issue = [&](int kt, f16* st) {
 #pragma unroll
@@ -110,29 +135,52 @@ struct DTile {
                 __builtin_amdgcn_global_load_lds((const void*)(gp[q] + (size_t)kt * gstep[q]),
                                                  (__attribute__((address_space(3))) void*)(st + loff[q]), 16, 0, 0);
         };
-        // fragments of one stage: [k16 step][tile]
-        struct Frags { f16x8 a[2][TN], b[2][TM]; };
+        // fragments of one stage: 32x32: [k16 step][tile]; 16x16: [tile] (one k32)
+        struct Frags32 { f16x8 a[2][TN], b[2][TM]; };
+        struct Frags16 { f16x8 a[NA], b[NB]; };
+        using Frags = std::conditional_t<M16, Frags16, Frags32>;
+        // operand m of a stage, in the order the interleaved step reads them
+        constexpr int NR = M16 ? NA + NB : 2 * (TN + TM);
+        auto read1 = [&](const f16* st, Frags& f, int m) {
+            if constexpr (M16) {
+                if (m < NA) f.a[m] = *(const f16x8*)&st[ao[m]];
+                else f.b[m - NA] = *(const f16x8*)&st[bo[m - NA]];
+            } else {
+                const int rks = m / (TN + TM), rr = m % (TN + TM);
+                if (rr < TN) f.a[rks][rr] = *(const f16x8*)&st[ao[rr] + 256 * rks];
+                else f.b[rks][rr - TN] = *(const f16x8*)&st[bo[rr - TN] + 256 * rks];
+            }
+        };
         auto readf = [&](const f16* st, Frags& f) {
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-                for (int i = 0; i < TN; ++i) f.a[ks][i] = *(const f16x8*)&st[ao[i] + 256 * ks];
-#pragma unroll
-                for (int j = 0; j < TM; ++j) f.b[ks][j] = *(const f16x8*)&st[bo[j] + 256 * ks];
+            for (int m = 0; m < NR; ++m) read1(st, f, m);
+        };
+        // MFMA m of a stage
+        constexpr int NM = M16 ? NA * NB : 2 * TN * TM;
+        auto mfma1 = [&](const Frags& f, int m) {
+            if constexpr (M16) {
+                const int i = m / NB, j = m % NB;
+                acc.v[i][j] = mfma16(f.a[i], f.b[j], acc.v[i][j]);
+            } else {
+                const int ks = m / (TN * TM), i = (m / TM) % TN, j = m % TM;
+                acc.v[i][j] = mfma32(f.a[ks][i], f.b[ks][j], acc.v[i][j]);
             }
         };
         auto mfmas = [&](const Frags& f) {
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int i = 0; i < TN; ++i)
-#pragma unroll
-                    for (int j = 0; j < TM; ++j) acc.v[i][j] = mfma32(f.a[ks][i], f.b[ks][j], acc.v[i][j]);
+            for (int m = 0; m < NM; ++m) mfma1(f, m);
         };
+        if constexpr (M16) {
 #pragma unroll
-        for (int i = 0; i < TN; ++i)
+            for (int i = 0; i < NA; ++i)
 #pragma unroll
-            for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
+                for (int j = 0; j < NB; ++j) acc.v[i][j] = f32x4{};
+        } else {
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
+        }
         // no wave may still read the stages from a previous call
         __builtin_amdgcn_s_waitcnt(vm_lgkm_wait(63));
         __builtin_amdgcn_s_barrier();
@@ -156,19 +204,11 @@ struct DTile {
             __builtin_amdgcn_s_waitcnt(vm_lgkm_wait((NS - 2) * LPS));
             __builtin_amdgcn_s_barrier();
             const int kt = kb + min(t + NS, n - 1);
-            constexpr int NM = 2 * TN * TM, NR = 2 * (TN + TM);
             constexpr int NG = NM > NR ? (NM > LPS ? NM : LPS) : (NR > LPS ? NR : LPS);
 #pragma unroll
             for (int m = 0; m < NG; ++m) {
-                if (m < NM) {
-                    const int ks = m / (TN * TM), i = (m / TM) % TN, j = m % TM;
-                    acc.v[i][j] = mfma32(cur.a[ks][i], cur.b[ks][j], acc.v[i][j]);
-                }
-                if (m < NR) {
-                    const int rks = m / (TN + TM), r = m % (TN + TM);
-                    if (r < TN) nxt.a[rks][r] = *(const f16x8*)&next[ao[r] + 256 * rks];
-                    else nxt.b[rks][r - TN] = *(const f16x8*)&next[bo[r - TN] + 256 * rks];
-                }
+                if (m < NM) mfma1(cur, m);
+                if (m < NR) read1(next, nxt, m);
                 if (m < LPS)
                     __builtin_amdgcn_global_load_lds((const void*)(gp[m] + (size_t)kt * gstep[m]),
                                                      (__attribute__((address_space(3))) void*)(refill + loff[m]),
@@ -206,12 +246,68 @@ struct DTile {
     }
 };
 
-// (nw, mw): the wave's first feature row and token.  Lane holds token
-// m = mw + j*32 + lane%32 and, per q4, the four consecutive features
+// Stores four consecutive output features n..n+3 of token m (every epilogue
+// but SwiGLU, whose lanes hold W1 and W3 rows and store gate features).
+template <int EPI>
+__device__ __forceinline__ void store4(const GemmArgs& a, int m, int n, float v0, float v1, float v2, float v3) {
+    if constexpr (EPI == EPI_F32) {
+        if (a.alpha != 0.f) {  // optional output scale (0 = none)
+            v0 *= a.alpha; v1 *= a.alpha; v2 *= a.alpha; v3 *= a.alpha;
+        }
+        if (a.softcap > 0.f) {
+            const float c = a.softcap, ic = 1.0f / c;
+            v0 = tanhf(v0 * ic) * c; v1 = tanhf(v1 * ic) * c;
+            v2 = tanhf(v2 * ic) * c; v3 = tanhf(v3 * ic) * c;
+        }
+        *(f32x4*)(a.out_f32 + (size_t)m * a.ldo + n) = f32x4{v0, v1, v2, v3};
+    } else if constexpr (EPI == EPI_RESID) {
+        f32x4* px = (f32x4*)(a.out_f32 + (size_t)m * a.ldo + n);
+        f32x4 x = *px;
+        x[0] = v0 * a.alpha + x[0]; x[1] = v1 * a.alpha + x[1];
+        x[2] = v2 * a.alpha + x[2]; x[3] = v3 * a.alpha + x[3];
+        *px = x;
+    } else if constexpr (EPI == EPI_QKV) {
+        const int sec = n / a.D, c = n - sec * a.D;
+        const int h = c / a.hd, d = c - h * a.hd;
+        const int b = m / a.S, s = m - b * a.S, pos = a.pos0 + s;
+        if (sec < 2) {
+            const float2 cs0 = a.rope[(size_t)pos * (a.hd / 2) + d / 2];
+            const float2 cs1 = a.rope[(size_t)pos * (a.hd / 2) + d / 2 + 1];
+            const float r0 = v0 * cs0.x + (-v1) * cs0.y, r1 = v1 * cs0.x + v0 * cs0.y;
+            const float r2 = v2 * cs1.x + (-v3) * cs1.y, r3 = v3 * cs1.x + v2 * cs1.y;
+            v0 = r0; v1 = r1; v2 = r2; v3 = r3;
+        }
+        f16* dst;
+        if (sec == 0)
+            dst = a.q + (((size_t)b * a.H + h) * a.S + s) * a.hd + d;
+        else
+            dst = (sec == 1 ? a.kc : a.vc) + (((size_t)b * a.H + h) * a.ctx + pos) * a.hd + d;
+        *(f16x4*)dst = f16x4{(f16)v0, (f16)v1, (f16)v2, (f16)v3};
+    }
+}
+
+// SwiGLU output of token m, gate features f..f+3 from h1 (W1 rows) and h3
+// (the matching W3 rows); EPI_SWIGLU_SAVE also keeps h1, h3 for the backward.
+template <int EPI>
+__device__ __forceinline__ void store_swiglu(const GemmArgs& a, int m, int f, const float (&h1)[4],
+                                             const float (&h3)[4]) {
+    f16x4 g;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) g[r] = (f16)(silu_f(h1[r]) * h3[r]);
+    *(f16x4*)(a.out_f16 + frag_off(m, f, a.ldo)) = g;
+    if constexpr (EPI == EPI_SWIGLU_SAVE) {
+        // the pre-activations for the backward pass: h1 | h3 planes [M][F]
+        const size_t o = (size_t)m * a.ldo + f, plane = (size_t)a.M * a.ldo;
+        *(f16x4*)(a.h13 + o) = f16x4{(f16)h1[0], (f16)h1[1], (f16)h1[2], (f16)h1[3]};
+        *(f16x4*)(a.h13 + plane + o) = f16x4{(f16)h3[0], (f16)h3[1], (f16)h3[2], (f16)h3[3]};
+    }
+}
+
+// 32x32 tiles.  (nw, mw): the wave's first feature row and token.  Lane holds
+// token m = mw + j*32 + lane%32 and, per q4, the four consecutive features
 // n = nw + i*32 + 8*q4 + 4*(lane/32) + (0..3).
 template <int TN, int TM, int EPI>
-__device__ __forceinline__ void epilogue(const GemmArgs& a, int nw, int mw,
-                                         const Frag<TN, TM>& acc) {
+__device__ __forceinline__ void epilogue(const GemmArgs& a, int nw, int mw, const Frag<TN, TM>& acc) {
     const int lane = threadIdx.x & 63;
     const int N = a.N, M = a.M;
 #pragma unroll
@@ -229,22 +325,13 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, int nw, int mw,
                 for (int q4 = 0; q4 < 2; ++q4) {
                     const int f = 16 * T + 8 * q4 + 4 * (lane >> 5);
                     if (f >= a.ldo) continue;
-                    f16x4 g;
+                    float h1[4], h3[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float h1 = acc.v[i][j][4 * q4 + r], h3 = acc.v[i][j][4 * q4 + 8 + r];
-                        g[r] = (f16)(silu_f(h1) * h3);
+                        h1[r] = acc.v[i][j][4 * q4 + r];
+                        h3[r] = acc.v[i][j][4 * q4 + 8 + r];
                     }
-                    *(f16x4*)(a.out_f16 + frag_off(m, f, a.ldo)) = g;
-                    if constexpr (EPI == EPI_SWIGLU_SAVE) {
-                        // the pre-activations for the backward pass: h1 | h3 planes [M][F]
-                        const size_t o = (size_t)m * a.ldo + f, plane = (size_t)M * a.ldo;
-                        *(f16x4*)(a.h13 + o) = f16x4{(f16)acc.v[i][j][4 * q4 + 0], (f16)acc.v[i][j][4 * q4 + 1],
-                                                     (f16)acc.v[i][j][4 * q4 + 2], (f16)acc.v[i][j][4 * q4 + 3]};
-                        *(f16x4*)(a.h13 + plane + o) =
-                            f16x4{(f16)acc.v[i][j][4 * q4 + 8], (f16)acc.v[i][j][4 * q4 + 9],
-                                  (f16)acc.v[i][j][4 * q4 + 10], (f16)acc.v[i][j][4 * q4 + 11]};
-                    }
+                    store_swiglu<EPI>(a, m, f, h1, h3);
                 }
             }
         } else {
@@ -254,45 +341,55 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, int nw, int mw,
                 for (int q4 = 0; q4 < 4; ++q4) {
                     const int n = nw + i * 32 + 8 * q4 + 4 * (lane >> 5);
                     if (n >= N) continue;
-                    float v0 = acc.v[i][j][4 * q4 + 0], v1 = acc.v[i][j][4 * q4 + 1];
-                    float v2 = acc.v[i][j][4 * q4 + 2], v3 = acc.v[i][j][4 * q4 + 3];
-                    if constexpr (EPI == EPI_F32) {
-                        if (a.alpha != 0.f) {  // optional output scale (0 = none)
-                            v0 *= a.alpha; v1 *= a.alpha; v2 *= a.alpha; v3 *= a.alpha;
-                        }
-                        if (a.softcap > 0.f) {
-                            const float c = a.softcap, ic = 1.0f / c;
-                            v0 = tanhf(v0 * ic) * c; v1 = tanhf(v1 * ic) * c;
-                            v2 = tanhf(v2 * ic) * c; v3 = tanhf(v3 * ic) * c;
-                        }
-                        *(f32x4*)(a.out_f32 + (size_t)m * a.ldo + n) = f32x4{v0, v1, v2, v3};
-                    } else if constexpr (EPI == EPI_RESID) {
-                        f32x4* px = (f32x4*)(a.out_f32 + (size_t)m * a.ldo + n);
-                        f32x4 x = *px;
-                        x[0] = v0 * a.alpha + x[0]; x[1] = v1 * a.alpha + x[1];
-                        x[2] = v2 * a.alpha + x[2]; x[3] = v3 * a.alpha + x[3];
-                        *px = x;
-                    } else {  // EPI_QKV
-                        const int sec = n / a.D, c = n - sec * a.D;
-                        const int h = c / a.hd, d = c - h * a.hd;
-                        const int b = m / a.S, s = m - b * a.S, pos = a.pos0 + s;
-                        if (sec < 2) {
-                            const float2 cs0 = a.rope[(size_t)pos * (a.hd / 2) + d / 2];
-                            const float2 cs1 = a.rope[(size_t)pos * (a.hd / 2) + d / 2 + 1];
-                            const float r0 = v0 * cs0.x + (-v1) * cs0.y, r1 = v1 * cs0.x + v0 * cs0.y;
-                            const float r2 = v2 * cs1.x + (-v3) * cs1.y, r3 = v3 * cs1.x + v2 * cs1.y;
-                            v0 = r0; v1 = r1; v2 = r2; v3 = r3;
-                        }
-                        f16* dst;
-                        if (sec == 0)
-                            dst = a.q + (((size_t)b * a.H + h) * a.S + s) * a.hd + d;
-                        else
-                            dst = (sec == 1 ? a.kc : a.vc) + (((size_t)b * a.H + h) * a.ctx + pos) * a.hd + d;
-                        *(f16x4*)dst = f16x4{(f16)v0, (f16)v1, (f16)v2, (f16)v3};
-                    }
+                    store4<EPI>(a, m, n, acc.v[i][j][4 * q4 + 0], acc.v[i][j][4 * q4 + 1], acc.v[i][j][4 * q4 + 2],
+                                acc.v[i][j][4 * q4 + 3]);
                 }
         }
     }
+}
+
+// 16x16 tiles: lane l holds token m = mw + 16j + l%16 and the four
+// consecutive features n = nw + 16i + 4(l/16) + (0..3) of A tile i, B tile j.
+template <int NA, int NB, int EPI>
+__device__ __forceinline__ void epilogue(const GemmArgs& a, int nw, int mw, const Frag16<NA, NB>& acc) {
+    const int lane = threadIdx.x & 63;
+    const int N = a.N, M = a.M;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int m = mw + 16 * j + (lane & 15);
+        if (m >= M) continue;
+        if constexpr (EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_SAVE) {
+            // A tiles 2p and 2p + 1 are the W1 rows of features 16T..16T+15 and
+            // the matching W3 rows (T = (nw + 32p) / 32; nw is a multiple of 32)
+#pragma unroll
+            for (int p = 0; p < NA / 2; ++p) {
+                const int f = 16 * ((nw + 32 * p) >> 5) + 4 * (lane >> 4);
+                if (f >= a.ldo) continue;
+                float h1[4], h3[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    h1[r] = acc.v[2 * p][j][r];
+                    h3[r] = acc.v[2 * p + 1][j][r];
+                }
+                store_swiglu<EPI>(a, m, f, h1, h3);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NA; ++i) {
+                const int n = nw + 16 * i + 4 * (lane >> 4);
+                if (n >= N) continue;
+                store4<EPI>(a, m, n, acc.v[i][j][0], acc.v[i][j][1], acc.v[i][j][2], acc.v[i][j][3]);
+            }
+        }
+    }
+}
+
+template <class Tl, int EPI>
+__device__ __forceinline__ void run_epilogue(const GemmArgs& a, int nw, int mw, const typename Tl::Acc& acc) {
+    if constexpr (Tl::kM16)
+        epilogue<Tl::NA, Tl::NB, EPI>(a, nw, mw, acc);
+    else
+        epilogue<Tl::FTN, Tl::FTM, EPI>(a, nw, mw, acc);
 }
 
 // MODE: MODE_DP one block per tile; MODE_SK stream-K over P blocks (T =
@@ -310,7 +407,7 @@ __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long lo
         const int t = xcd_remap(blockIdx.x, nbN * nbM);
         const int nb = t / nbM, mb = t - nb * nbM;
         Tl::run(a, nb * Tl::BN, mb * Tl::BM, 0, KT, acc, sm);
-        epilogue<Tl::FTN, Tl::FTM, EPI>(a, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
+        run_epilogue<Tl, EPI>(a, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
     } else if constexpr (MODE == MODE_SPLIT) {
         // the splits of one tile and the tiles of one weight panel land on the
         // same XCD
@@ -324,7 +421,7 @@ __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long lo
         b.ldo = a.N;
         b.softcap = 0.f;
         b.alpha = 0.f;  // raw partials: the row kernel applies alpha once to their sum
-        epilogue<Tl::FTN, Tl::FTM, EPI_F32>(b, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
+        run_epilogue<Tl, EPI_F32>(b, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
     } else {
         constexpr int TN = Tl::FTN, TM = Tl::FTM, NT = Tl::NT;
         constexpr int NV = TN * TM * 4;  // f32x4 per thread per partial tile
@@ -409,11 +506,15 @@ hipError_t launch_tile(const GemmArgs& a, bool sk, hipStream_t st) {
     const int tiles = nbN * nbM;
     const long long T = (long long)tiles * (a.K / Tl::KI);
     if (sk) {
-        if (!a.sk_part || (size_t)SK_P * 2 * Tl::BN * Tl::BM > a.sk_part_floats) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((gemm_kernel<Tl, EPI, MODE_SK>), dim3(SK_P), dim3(Tl::NT), 0, st, a, SK_P, T);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((gemm_fixup_kernel<Tl, EPI>), dim3(tiles, Tl::FTN), dim3(Tl::NT), 0, st, a, SK_P, T);
+        if constexpr (Tl::kM16) {
+            return hipErrorInvalidValue;  // stream-K partials use the 32x32 layout
+        } else {
+            if (!a.sk_part || (size_t)SK_P * 2 * Tl::BN * Tl::BM > a.sk_part_floats) return hipErrorInvalidValue;
+            hipLaunchKernelGGL((gemm_kernel<Tl, EPI, MODE_SK>), dim3(SK_P), dim3(Tl::NT), 0, st, a, SK_P, T);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL((gemm_fixup_kernel<Tl, EPI>), dim3(tiles, Tl::FTN), dim3(Tl::NT), 0, st, a, SK_P, T);
+        }
     } else {
         hipLaunchKernelGGL((gemm_kernel<Tl, EPI, MODE_DP>), dim3(tiles), dim3(Tl::NT), 0, st, a, 1, T);
     }
@@ -462,6 +563,10 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
             }
         }
     }
+    // 192x256 runs the 16x16x32 form: measured on MI355X at M = 512 (W1|W3 of
+    // the 7B shape) 85 vs 89 us; the other shapes are faster as 32x32x16
+    // (192x128 loses its second wave per SIMD to the extra registers, the
+    // 8-wave tiles spill).
     switch (cfg) {
         case GCFG_D8_256x256: return launch_tile<DTile<2, 4, 4, 2>, EPI>(a, false, st);
         case GCFG_D8_256x256_SK: return launch_tile<DTile<2, 4, 4, 2>, EPI>(a, true, st);
@@ -477,7 +582,7 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         case GCFG_D4_192x128_SK: return launch_tile<DTile<2, 2, 3, 2>, EPI>(a, true, st);
         case GCFG_D8_192x256: return launch_tile<DTile<2, 4, 3, 2>, EPI>(a, false, st);
         case GCFG_D8_192x256_SK: return launch_tile<DTile<2, 4, 3, 2>, EPI>(a, true, st);
-        case GCFG_D4_192x256: return launch_tile<DTile<2, 2, 3, 4>, EPI>(a, false, st);
+        case GCFG_D4_192x256: return launch_tile<DTile<2, 2, 3, 4, true>, EPI>(a, false, st);
         case GCFG_D4_192x256_SK: return launch_tile<DTile<2, 2, 3, 4>, EPI>(a, true, st);
     }
     return hipErrorInvalidValue;
