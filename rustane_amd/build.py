@@ -1,8 +1,10 @@
 """Builds librustane_hip.so (gfx950) in-tree with hipcc.
 
 Every HIP translation unit is compiled for gfx950 only, with packed-fp32
-VALU ops disabled, and linked into rustane_amd/librustane_hip.so.  Object
-files go to rustane_amd/_build/.  Run as `python -m rustane_amd.build`.
+VALU ops disabled, and linked into rustane_amd/librustane_hip.so.  The GEMM
+test harness (rh_gemm_harness.cpp, used only by the tests) is linked with the
+GEMM objects into rustane_amd/librustane_gemm_harness.so.  Object files go to
+rustane_amd/_build/.  Run as `python -m rustane_amd.build`.
 """
 from __future__ import annotations
 
@@ -17,6 +19,9 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librustane_hip.so")
+HARNESS = os.path.join(HERE, "librustane_gemm_harness.so")
+HARNESS_SOURCES = ["rh_gemm_harness.cpp"]
+HARNESS_DEPS = ["rh_gemm.hip", "rh_rowops.hip"]  # objects of SOURCES it links
 
 SOURCES = ["rh_gemm.hip", "rh_attn.hip", "rh_attn_bwd.hip", "rh_gemv.hip", "rh_rowops.hip", "rh_trainops.hip", "rh_optim.hip",
            "rh_runtime.cpp", "rh_train.cpp", "rh_data.cpp", "rh_sched.cpp"]
@@ -49,18 +54,24 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
+def _link(out: str, objs: list) -> None:
+    tmp = out + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout)
-    shutil.move(tmp, LIB)
+    shutil.move(tmp, out)
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    srcs = SOURCES + HARNESS_SOURCES
+    with cf.ThreadPoolExecutor(max_workers=min(len(srcs), os.cpu_count() or 4)) as ex:
+        objs = dict(zip(srcs, ex.map(_compile, srcs)))
+    _link(LIB, [objs[s] for s in SOURCES])
+    _link(HARNESS, [objs[s] for s in HARNESS_SOURCES + HARNESS_DEPS])
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {HARNESS}")
     return LIB
 
 
