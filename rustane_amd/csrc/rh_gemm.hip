@@ -283,6 +283,23 @@ __device__ __forceinline__ void store4(const GemmArgs& a, int m, int n, float v0
         else
             dst = (sec == 1 ? a.kc : a.vc) + (((size_t)b * a.H + h) * a.ctx + pos) * a.hd + d;
         *(f16x4*)dst = f16x4{(f16)v0, (f16)v1, (f16)v2, (f16)v3};
+    } else if constexpr (EPI == EPI_SILU_BWD) {
+        // SiLU-gate backward (layer.rs:7083-7104) of the gate gradient g = acc
+        // and the saved h1, h3: dh3 = g silu(h1), dh1 = g h3 silu'(h1), fp16
+        // in fragment order [M][2N] (dh1 in columns 0..N-1, dh3 in N..2N-1)
+        const size_t o = (size_t)m * a.ldo + n, plane = (size_t)a.M * a.ldo;
+        const f16x4 a1 = *(const f16x4*)(a.h13 + o), a3 = *(const f16x4*)(a.h13 + plane + o);
+        const float g[4] = {v0, v1, v2, v3};
+        f16x4 o1, o3;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float h1 = (float)a1[e], h3 = (float)a3[e];
+            const float sig = 1.0f / (1.0f + __expf(-h1));
+            o3[e] = (f16)(g[e] * (h1 * sig));
+            o1[e] = (f16)(g[e] * h3 * (sig * (1.0f + h1 * (1.0f - sig))));
+        }
+        *(f16x4*)(a.out_f16 + frag_off(m, n, 2 * a.ldo)) = o1;
+        *(f16x4*)(a.out_f16 + frag_off(m, a.ldo + n, 2 * a.ldo)) = o3;
     }
 }
 
@@ -628,6 +645,9 @@ hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
         case EPI_SWIGLU_SAVE:
             if (a.N % 32 != 0 || !a.h13) return hipErrorInvalidValue;
             return launch_epi<EPI_SWIGLU_SAVE>(a, st);
+        case EPI_SILU_BWD:
+            if (a.N % 128 != 0 || a.ldo != a.N || !a.h13 || !a.out_f16) return hipErrorInvalidValue;
+            return launch_epi<EPI_SILU_BWD>(a, st);
     }
     return hipErrorInvalidValue;
 }

@@ -41,10 +41,12 @@ extern "C" {
 
 // epi: 0 fp32 store (alpha scale when nonzero, softcap when > 0), 1 residual
 // (io_f32 += alpha * acc), 2 SwiGLU (out_f16 = gate [M][N/2] in fragment
-// order), 4 SwiGLU + saved pre-activations (h13 = [2][M][N/2] row-major), 3
-// QKV + RoPE (q16 [B][H][S][hd], k16 / v16 [B][H][ctx][hd], rope [ctx][hd/2]
-// cos/sin pairs; M = B*S, N = 3*H*hd, positions pos0 .. pos0+S-1).  cfg is a
-// GemmCfg value (0 = the shape heuristic).  Returns 0 or a hipError_t / -1.
+// order), 3 QKV + RoPE (q16 [B][H][S][hd], k16 / v16 [B][H][ctx][hd], rope
+// [ctx][hd/2] cos/sin pairs; M = B*S, N = 3*H*hd, positions pos0 .. pos0+S-1),
+// 4 SwiGLU + saved pre-activations (h13 = [2][M][N/2] row-major), 5 SiLU-gate
+// backward (h13 = [2][M][N] input, out_f16 = dh1 | dh3 [M][2N] in fragment
+// order).  cfg is a GemmCfg value (0 = the shape heuristic).  Returns 0 or a
+// hipError_t / -1.
 int rhh_gemm(int epi, int cfg, const uint16_t* wf, const uint16_t* xf, int M, int N, int K, float alpha,
              float softcap, float* io_f32, uint16_t* out_f16, uint16_t* h13, int B, int S, int H, int hd, int ctx,
              int pos0, const float* rope, uint16_t* q16, uint16_t* k16, uint16_t* v16) {
@@ -85,6 +87,16 @@ int rhh_gemm(int epi, int cfg, const uint16_t* wf, const uint16_t* xf, int M, in
             if (!hh) return -1;
             a.h13 = hh;
         }
+    } else if (epi == rh::EPI_SILU_BWD) {
+        if (!out_f16 || !h13) return -1;
+        a.ldo = N;
+        o16n = (size_t)up16(M) * 2 * N;
+        o16 = d.alloc<f16>(o16n);
+        f16* hin = d.alloc<f16>((size_t)2 * M * N);
+        if (!o16 || !hin || hipMemset(o16, 0, o16n * 2) != hipSuccess) return -1;
+        if (hipMemcpy(hin, h13, (size_t)2 * M * N * 2, hipMemcpyHostToDevice) != hipSuccess) return -1;
+        a.out_f16 = o16;
+        a.h13 = hin;
     } else if (epi == rh::EPI_QKV) {
         if (!rope || !q16 || !k16 || !v16 || B * S != M || N != 3 * H * hd || pos0 + S > ctx) return -1;
         qn = (size_t)B * H * S * hd;

@@ -11,7 +11,7 @@ namespace rh {
 // ---------------- prefill GEMM:  Y[m][n] = sum_k X[m][k] * W[n][k] -------------
 // EPI_SWIGLU_SAVE is EPI_SWIGLU that also stores the fp16 pre-activations
 // h1, h3 (planes [M][F] at h13 and h13 + M*F) for the backward pass.
-enum GemmEpi { EPI_F32 = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3, EPI_SWIGLU_SAVE = 4 };
+enum GemmEpi { EPI_F32 = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3, EPI_SWIGLU_SAVE = 4, EPI_SILU_BWD = 5 };
 
 struct GemmArgs {
     const f16* W;  // [N, K] weights ("out x in"), fragment order (frag_off), rows padded to 16
@@ -28,7 +28,9 @@ struct GemmArgs {
     f16* vc;         // [B][H][ctx][hd]
     const float2* rope;  // [pos][hd/2] (cos, sin)
     int S, D, H, hd, ctx, pos0;
-    f16* h13;        // EPI_SWIGLU_SAVE: h1 | h3 planes, [2][M][ldo] fp16 row-major
+    f16* h13;        // EPI_SWIGLU_SAVE (written) / EPI_SILU_BWD (read): h1 | h3 planes, [2][M][ldo] fp16
+                     // row-major.  EPI_SILU_BWD: acc is the gate gradient [M][ldo = N]; out_f16 gets
+                     // dh1 | dh3 in fragment order [M][2N]
     // Stream-K workspace (optional): fp32 partial tiles.
     float* sk_part;
     size_t sk_part_floats;
@@ -163,8 +165,6 @@ hipError_t launch_rms_backward(const float* dy, const float* x, const float* gam
 // dgamma[d] += kappa * sum_b part[b][d]  (= instead of += when store is set)
 hipError_t launch_dgamma_reduce(const float* part, int nblk, int D, float kappa, float* dgamma, bool store,
                                 hipStream_t st);
-// dh [M][2F] fp16 fragment order (dh1 | dh3) from dgate [M][F] fp32 and h13.
-hipError_t launch_silu_backward(const float* dg, const f16* h13, f16* dh, int M, int F, hipStream_t st);
 // RoPE backward on the q, k sections of dqkv [M][3D] fp32, out fp16 fragment order.
 hipError_t launch_rope_backward_pack(const float* dqkv, const float2* rope, f16* out, int M, int S, int D, int hd,
                                      hipStream_t st);

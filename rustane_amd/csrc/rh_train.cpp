@@ -305,8 +305,13 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         LCK(rh::launch_transpose_frag(T->H1, T->T1, M, D, Mp, 0, st));
         LCK(rh::launch_transpose_frag(cc.gate, T->T2, M, F, Mp, 0, st));
         RCK(grad_gemm(ctx, T->T1, T->T2, D, F, kappa, G[6]));
-        RCK(data_gemm(ctx, T->H1, wt.w2t, M, F, D, T->gout));
-        LCK(rh::launch_silu_backward(T->gout, cc.h13, T->H2, M, F, st));
+        {  // dgate = dffn W2 with the SiLU-gate backward in the epilogue -> [dh1 | dh3]
+            rh::GemmArgs g{};
+            g.X = T->H1; g.W = wt.w2t; g.M = M; g.N = F; g.K = D;
+            g.h13 = cc.h13; g.out_f16 = T->H2; g.ldo = F;
+            set_sk(ctx, g);
+            LCK(rh::launch_gemm(rh::EPI_SILU_BWD, g, st));
+        }
         // dx_ffn = [dh1 | dh3] [W1 | W3]^T; dW1, dW3 += x2n^T dh
         RCK(data_gemm(ctx, T->H2, wt.w13t, M, D, 2 * F, T->gout));
         LCK(rh::launch_transpose_frag(T->H2, T->T3, M, 2 * F, Mp, 0, st));

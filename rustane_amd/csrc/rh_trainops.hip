@@ -224,31 +224,6 @@ __global__ __launch_bounds__(256) void dgamma_reduce_kernel(const float* __restr
     }
 }
 
-// SiLU-gate backward (layer.rs:7083-7104) from the GEMM's dgate [M, F] fp32
-// and the saved fp16 pre-activations h1 | h3 ([2][M][F]): dh1, dh3 as fp16
-// in fragment order [M][2F] (dh1 in columns 0..F-1, dh3 in F..2F-1).
-__global__ __launch_bounds__(256) void silu_backward_kernel(const float* __restrict__ dg, const f16* __restrict__ h13,
-                                                            f16* __restrict__ dh, int M, int F) {
-    const size_t n8 = (size_t)M * F / 8;
-    for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n8; t += (size_t)gridDim.x * blockDim.x) {
-        const size_t base = t * 8;
-        const int m = (int)(base / F), f = (int)(base % F);
-        const f32x4 g0 = *(const f32x4*)(dg + base), g1 = *(const f32x4*)(dg + base + 4);
-        const f16x8 a = *(const f16x8*)(h13 + base), c = *(const f16x8*)(h13 + (size_t)M * F + base);
-        f16x8 o1, o3;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float g = e < 4 ? g0[e] : g1[e - 4];
-            const float h1 = (float)a[e], h3 = (float)c[e];
-            const float sig = 1.0f / (1.0f + __expf(-h1));
-            o3[e] = (f16)(g * (h1 * sig));
-            o1[e] = (f16)(g * h3 * (sig * (1.0f + h1 * (1.0f - sig))));
-        }
-        *(f16x8*)(dh + frag_off(m, f, 2 * F)) = o1;
-        *(f16x8*)(dh + frag_off(m, F + f, 2 * F)) = o3;
-    }
-}
-
 // RoPE backward (rope_backward_inplace, layer.rs:7389-7407) on the q and k
 // sections of dqkv [M][3D] fp32 (token m at position m % S), then fp16 in
 // fragment order [M][3D] for the dX GEMM.
@@ -327,13 +302,6 @@ hipError_t launch_dgamma_reduce(const float* part, int nblk, int D, float kappa,
                                 hipStream_t st) {
     hipLaunchKernelGGL(dgamma_reduce_kernel, dim3((D + 15) / 16), dim3(256), 0, st, part, nblk, D, kappa, dgamma,
                        (int)store);
-    return hipGetLastError();
-}
-
-hipError_t launch_silu_backward(const float* dg, const f16* h13, f16* dh, int M, int F, hipStream_t st) {
-    if (F % 8 != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(silu_backward_kernel, dim3(grid_for((size_t)M * F / 8, 256)), dim3(256), 0, st, dg, h13, dh,
-                       M, F);
     return hipGetLastError();
 }
 

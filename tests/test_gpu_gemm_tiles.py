@@ -26,7 +26,7 @@ pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(os.path.dirname(HERE), "rustane_amd", "librustane_gemm_harness.so")
 
-EPI_F32, EPI_RESID, EPI_SWIGLU, EPI_QKV, EPI_SWIGLU_SAVE = 0, 1, 2, 3, 4
+EPI_F32, EPI_RESID, EPI_SWIGLU, EPI_QKV, EPI_SWIGLU_SAVE, EPI_SILU_BWD = 0, 1, 2, 3, 4, 5
 # GemmCfg values (rh_kernels.h): one block per tile, and their stream-K twins
 DP = {"D8_256x256": 6, "D4_128x128": 8, "D8_256x128": 10, "D4_256x256": 12, "D4_256x128": 14,
       "D4_192x128": 16, "D8_192x256": 18, "D4_192x256": 20}
@@ -153,6 +153,26 @@ def test_swiglu_and_saved_preactivations(lib, name):
     close(frag_unpack(out16, M, F), g_ref, 2e-3, f"{name} swiglu_save gate")
     close(h13[:M * F].reshape(M, F), h1, 2e-3, f"{name} saved h1")
     close(h13[M * F:].reshape(M, F), h3, 2e-3, f"{name} saved h3")
+
+
+@pytest.mark.parametrize("name", list(CFGS))
+def test_silu_gate_backward(lib, name):
+    """The gate gradient g = X W^T with the SiLU-gate backward in the
+    epilogue (crates/engine/src/layer.rs:7083-7104, cpu/silu.rs:68-90):
+    dh3 = g silu(h1), dh1 = g h3 silu'(h1), written as [dh1 | dh3] in
+    fragment order."""
+    M, F, K = 300, 640, 384
+    x, w, g = operands(9, M, F, K)
+    rng = np.random.default_rng(10)
+    h13 = (rng.standard_normal(2 * M * F) * 2).astype(np.float16)
+    out16 = np.zeros(up16(M) * 2 * F, np.float16)
+    run(lib, EPI_SILU_BWD, CFGS[name], x, w, out16=out16, h13=h13)
+    h1 = h13[:M * F].reshape(M, F).astype(np.float64)
+    h3 = h13[M * F:].reshape(M, F).astype(np.float64)
+    sig = 1.0 / (1.0 + np.exp(-h1))
+    dh = frag_unpack(out16, M, 2 * F)
+    close(dh[:, :F], g * h3 * sig * (1.0 + h1 * (1.0 - sig)), 2e-3, f"{name} dh1")
+    close(dh[:, F:], g * h1 * sig, 2e-3, f"{name} dh3")
 
 
 @pytest.mark.parametrize("name", ["auto", "D4_192x128", "D4_192x256", "D8_256x256", "D4_128x128_SK"])
