@@ -13,8 +13,8 @@
 //
 // Tile policy: DTile (below) -- both operands in fragment order in HBM, moved
 // global -> LDS by DMA through a 4-stage pipeline of 32-wide k slices,
-// 32x32x16 MFMA (16x16x32 for the 192x256 tile) on fragments double-buffered
-// in registers.  Instantiated as
+// 32x32x16 MFMA (16x16x32 for the 8-wave 192x256 tile) on fragments
+// double-buffered in registers.  Instantiated as
 // 256x256 (8 waves of 128x64, or 4 waves of 128x128 with AGPR accumulators),
 // 256x128, 192x256, 192x128 and 128x128; a cost model picks one per shape.
 // Out-of-range rows are clamped, not predicated (they only feed accumulator
@@ -553,16 +553,17 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
     int cfg = a.force_cfg;
     if (cfg == GCFG_AUTO) {
         // Data-parallel tiles: estimated time = rounds of one block per CU x
-        // tile FLOPs / that tile's sustained per-CU rate.  The rates are
-        // measured on MI355X with random fp16 operands (TFLOP/s per CU at full
-        // occupancy); the estimate trades wave quantization (e.g. 172 vs 230
-        // tiles at M = 512) against per-tile efficiency.  Narrow outputs (Wo)
-        // and long K (W2) use stream-K instead, when every block gets at least
-        // two 32-wide k-iterations.
+        // tile FLOPs / that tile's per-CU rate.  The rates are fitted to MI355X
+        // timings of every tile on 27 GEMM shapes of the 7B forward and
+        // training step (M 512 - 8192, random fp16 operands; the picks land
+        // within 0.5% of the per-shape best in total); the estimate trades wave
+        // quantization (e.g. 172 vs 230 tiles at M = 512) against per-tile
+        // efficiency.  Narrow outputs (Wo) and long K (W2) use stream-K
+        // instead, when every block gets at least two 32-wide k-iterations.
         struct Cand { int cfg, bn, bm; float rate; };
-        constexpr Cand dp[] = {{GCFG_D8_256x256, 256, 256, 4.4f}, {GCFG_D4_192x256, 192, 256, 4.18f},
-                               {GCFG_D8_256x128, 256, 128, 4.0f}, {GCFG_D4_192x128, 192, 128, 3.95f},
-                               {GCFG_D4_128x128, 128, 128, 3.7f}};
+        constexpr Cand dp[] = {{GCFG_D8_256x256, 256, 256, 4.4f}, {GCFG_D8_192x256, 192, 256, 4.35f},
+                               {GCFG_D8_256x128, 256, 128, 3.6f}, {GCFG_D4_192x128, 192, 128, 3.7f},
+                               {GCFG_D4_128x128, 128, 128, 3.0f}};
         const long long KT = a.K / 32;
         const int t256x128 = ((a.N + 255) / 256) * ((a.M + 127) / 128);
         const int t128 = ((a.N + 127) / 128) * ((a.M + 127) / 128);
@@ -580,10 +581,11 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
             }
         }
     }
-    // 192x256 runs the 16x16x32 form: measured on MI355X at M = 512 (W1|W3 of
-    // the 7B shape) 85 vs 89 us; the other shapes are faster as 32x32x16
-    // (192x128 loses its second wave per SIMD to the extra registers, the
-    // 8-wave tiles spill).
+    // The 8-wave 192x256 tile runs the 16x16x32 form: W1|W3 of the 7B shape at
+    // M = 512 takes 84.5 us, against 87.8 as the 4-wave 16x16x32 tile and
+    // 91.4 as 8-wave 32x32x16.  The other tiles are faster as 32x32x16
+    // (192x128 loses its second block per CU to the extra registers, the
+    // 8-wave 256-wide tiles spill).
     switch (cfg) {
         case GCFG_D8_256x256: return launch_tile<DTile<2, 4, 4, 2>, EPI>(a, false, st);
         case GCFG_D8_256x256_SK: return launch_tile<DTile<2, 4, 4, 2>, EPI>(a, true, st);
@@ -597,9 +599,9 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         case GCFG_D4_256x128_SK: return launch_tile<DTile<2, 2, 4, 2>, EPI>(a, true, st);
         case GCFG_D4_192x128: return launch_tile<DTile<2, 2, 3, 2>, EPI>(a, false, st);
         case GCFG_D4_192x128_SK: return launch_tile<DTile<2, 2, 3, 2>, EPI>(a, true, st);
-        case GCFG_D8_192x256: return launch_tile<DTile<2, 4, 3, 2>, EPI>(a, false, st);
+        case GCFG_D8_192x256: return launch_tile<DTile<2, 4, 3, 2, true>, EPI>(a, false, st);
         case GCFG_D8_192x256_SK: return launch_tile<DTile<2, 4, 3, 2>, EPI>(a, true, st);
-        case GCFG_D4_192x256: return launch_tile<DTile<2, 2, 3, 4, true>, EPI>(a, false, st);
+        case GCFG_D4_192x256: return launch_tile<DTile<2, 2, 3, 4>, EPI>(a, false, st);
         case GCFG_D4_192x256_SK: return launch_tile<DTile<2, 2, 3, 4>, EPI>(a, true, st);
     }
     return hipErrorInvalidValue;

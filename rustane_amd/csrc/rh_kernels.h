@@ -52,7 +52,7 @@ enum GemmCfg {
     GCFG_D4_256x128_SK = 15,
     GCFG_D4_192x128 = 16,    // 4 waves (96x64 each)
     GCFG_D4_192x128_SK = 17,
-    GCFG_D8_192x256 = 18,    // 8 waves (96x64 each)
+    GCFG_D8_192x256 = 18,    // 8 waves (96x64 each), 16x16x32 MFMA
     GCFG_D8_192x256_SK = 19,
     GCFG_D4_192x256 = 20,    // 4 waves (96x128 each, accumulators in AGPRs)
     GCFG_D4_192x256_SK = 21,

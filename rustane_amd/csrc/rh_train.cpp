@@ -253,15 +253,17 @@ int gamma_grad(rh_ctx* ctx, int nblk, int D, float kappa, float* dgamma) {
 // C[rows][cols] += kappa * X W^T with X [rows][Mp], W [cols][Mp] (token-inner).
 // When every gradient is still zero the epilogue stores kappa * acc instead
 // (the same values; it skips reading the fp32 gradient back).  K is the
-// token count, short next to the fp32 output these GEMMs write, so they use
-// 192x128 tiles, whose 80 KB of LDS lets two blocks share a CU and one's
-// epilogue stores overlap the other's MFMAs (measured at 7B: 40.4 vs 44.1 ms
-// per B1 step with the 256x256 tiles the FLOP-rate heuristic picks).
+// token count.  Below 2048 tokens it is short next to the fp32 output these
+// GEMMs write, so they use 192x128 tiles, whose 80 KB of LDS lets two blocks
+// share a CU and one's epilogue stores overlap the other's MFMAs (measured at
+// 7B: 40.4 vs 44.1 ms per B1 step with the 256x256 tiles the FLOP model
+// picks); from 2048 tokens on the model's larger tiles are faster (4096 x
+// 11008 at K 2048: 198 vs 235 us).
 int grad_gemm(rh_ctx* ctx, const f16* X, const f16* W, int rows, int cols, float kappa, float* out) {
     rh::GemmArgs g{};
     g.X = X; g.W = W; g.M = rows; g.N = cols; g.K = ctx->train->Mp;
     g.out_f32 = out; g.ldo = cols; g.alpha = kappa;
-    g.force_cfg = rh::GCFG_D4_192x128;
+    g.force_cfg = g.K < 2048 ? rh::GCFG_D4_192x128 : rh::GCFG_AUTO;
     set_sk(ctx, g);
     LCK(rh::launch_gemm(ctx->train->zero ? rh::EPI_F32 : rh::EPI_RESID, g, ctx->stream));
     return RH_OK;
