@@ -13,8 +13,8 @@
 //
 // Tile policy: DTile (below) -- both operands in fragment order in HBM, moved
 // global -> LDS by DMA through a 4-stage pipeline of 32-wide k slices,
-// 32x32x16 MFMA (16x16x32 for the 8-wave 192x256 tile) on fragments
-// double-buffered in registers.  Instantiated as
+// 32x32x16 MFMA (16x16x32 for the 8-wave 192-row tiles and the W2 split)
+// on fragments double-buffered in registers.  Instantiated as
 // 256x256 (8 waves of 128x64, or 4 waves of 128x128 with AGPR accumulators),
 // 256x128, 192x256, 192x128 and 128x128; a cost model picks one per shape.
 // Out-of-range rows are clamped, not predicated (they only feed accumulator
@@ -562,7 +562,7 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         // instead, when every block gets at least two 32-wide k-iterations.
         struct Cand { int cfg, bn, bm; float rate; };
         constexpr Cand dp[] = {{GCFG_D8_256x256, 256, 256, 4.4f}, {GCFG_D8_192x256, 192, 256, 4.35f},
-                               {GCFG_D8_256x128, 256, 128, 3.6f}, {GCFG_D4_192x128, 192, 128, 3.7f},
+                               {GCFG_D8_256x128, 256, 128, 3.6f}, {GCFG_D8_192x128, 192, 128, 3.7f},
                                {GCFG_D4_128x128, 128, 128, 3.0f}};
         const long long KT = a.K / 32;
         const int t256x128 = ((a.N + 255) / 256) * ((a.M + 127) / 128);
@@ -581,11 +581,13 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
             }
         }
     }
-    // The 8-wave 192x256 tile runs the 16x16x32 form: W1|W3 of the 7B shape at
-    // M = 512 takes 84.5 us, against 87.8 as the 4-wave 16x16x32 tile and
-    // 91.4 as 8-wave 32x32x16.  The other tiles are faster as 32x32x16
-    // (192x128 loses its second block per CU to the extra registers, the
-    // 8-wave 256-wide tiles spill).
+    // The 8-wave 192-row tiles run the 16x16x32 form: at M = 512 (7B) W1|W3
+    // takes 84.5 us as 8-wave 16x16x32 192x256, against 87.8 as a 4-wave
+    // 16x16x32 tile and 91.4 as 8-wave 32x32x16; QKV 60.4 us as 8-wave
+    // 16x16x32 192x128 against 64.7 as 4-wave 32x32x16.  The 4-wave 192x128
+    // tile stays 32x32x16: the weight-gradient GEMMs need its two blocks per
+    // CU, which the 16x16x32 form's extra registers would cost; the 8-wave
+    // 256-wide tiles spill in that form.
     switch (cfg) {
         case GCFG_D8_256x256: return launch_tile<DTile<2, 4, 4, 2>, EPI>(a, false, st);
         case GCFG_D8_256x256_SK: return launch_tile<DTile<2, 4, 4, 2>, EPI>(a, true, st);
@@ -598,6 +600,7 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         case GCFG_D4_256x128: return launch_tile<DTile<2, 2, 4, 2>, EPI>(a, false, st);
         case GCFG_D4_256x128_SK: return launch_tile<DTile<2, 2, 4, 2>, EPI>(a, true, st);
         case GCFG_D4_192x128: return launch_tile<DTile<2, 2, 3, 2>, EPI>(a, false, st);
+        case GCFG_D8_192x128: return launch_tile<DTile<2, 4, 3, 1, true>, EPI>(a, false, st);
         case GCFG_D4_192x128_SK: return launch_tile<DTile<2, 2, 3, 2>, EPI>(a, true, st);
         case GCFG_D8_192x256: return launch_tile<DTile<2, 4, 3, 2, true>, EPI>(a, false, st);
         case GCFG_D8_192x256_SK: return launch_tile<DTile<2, 4, 3, 2>, EPI>(a, true, st);
@@ -624,7 +627,10 @@ hipError_t launch_gemm_resid_norm(const GemmArgs& a, const float* gamma, float e
         while (S > 1 && (size_t)S * a.M * a.N > a.sk_part_floats) --S;
     }
     if (S >= 2) {
-        const hipError_t e = wide_k ? launch_split<DTile<2, 2, 4, 2>>(a, S, st)
+        // K >= 8192 (W2): 256x128 tiles as 8 waves of 16x16x32 (50.3 vs 52.9 us
+        // as 4 waves of 32x32x16 at 7B, M = 512); otherwise 128x128 (the two
+        // forms measure the same there)
+        const hipError_t e = wide_k ? launch_split<DTile<4, 2, 2, 2, true>>(a, S, st)
                                     : launch_split<DTile<2, 2, 2, 2>>(a, S, st);
         if (e != hipSuccess) return e;
         return launch_resid_norm(a.out_f32, a.sk_part, S, (size_t)a.M * a.N, a.alpha, gamma, eps, xn, a.M,

@@ -56,6 +56,7 @@ enum GemmCfg {
     GCFG_D8_192x256_SK = 19,
     GCFG_D4_192x256 = 20,    // 4 waves (96x128 each, accumulators in AGPRs)
     GCFG_D4_192x256_SK = 21,
+    GCFG_D8_192x128 = 24,    // 8 waves (96x32 each), 16x16x32 MFMA (no stream-K twin)
 };
 // Floats of stream-K workspace any prefill GEMM needs.
 size_t gemm_sk_part_floats();

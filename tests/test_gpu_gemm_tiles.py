@@ -3,7 +3,7 @@
 The forward only reaches the tile configurations its shape heuristic picks
 for the model widths under test.  Through the GEMM test harness
 (rustane_amd/librustane_gemm_harness.so) each configuration -- one block per
-tile (including the 16x16x32 192x256 tile), stream-K with its fix-up kernel,
+tile (including the 16x16x32 8-wave 192-row tiles), stream-K with its fix-up kernel,
 split-K with the summing residual + RMSNorm row kernel -- runs every epilogue
 on ragged shapes (M, N not multiples of any tile) and is checked against a
 float64 numpy product of the same fp16 operands:
@@ -31,7 +31,7 @@ EPI_F32, EPI_RESID, EPI_SWIGLU, EPI_QKV, EPI_SWIGLU_SAVE, EPI_SILU_BWD = 0, 1, 2
 DP = {"D8_256x256": 6, "D4_128x128": 8, "D8_256x128": 10, "D4_256x256": 12, "D4_256x128": 14,
       "D4_192x128": 16, "D8_192x256": 18, "D4_192x256": 20}
 SK = {k + "_SK": v + 1 for k, v in DP.items()}
-CFGS = {"auto": 0, **DP, **SK}
+CFGS = {"auto": 0, **DP, **SK, "D8_192x128": 24}
 
 
 @pytest.fixture(scope="module")
@@ -175,7 +175,7 @@ def test_silu_gate_backward(lib, name):
     close(dh[:, F:], g * h1 * sig, 2e-3, f"{name} dh3")
 
 
-@pytest.mark.parametrize("name", ["auto", "D4_192x128", "D4_192x256", "D8_256x256", "D4_128x128_SK"])
+@pytest.mark.parametrize("name", ["auto", "D4_192x128", "D8_192x128", "D8_192x256", "D8_256x256", "D4_128x128_SK"])
 def test_qkv_rope_scatter(lib, name):
     B, S, H, hd, ctx, pos0, K = 2, 150, 2, 128, 200, 10, 384
     D = H * hd
