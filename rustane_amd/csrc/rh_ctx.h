@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <string>
 #include <utility>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/rustane_hip.h"
@@ -127,21 +128,29 @@ int dalloc(rh_ctx* ctx, T** p, size_t elems) {
 void dfree(rh_ctx* ctx, void* p);
 
 // Launches fn(); when profiling class cls is on (and no graph is being
-// captured) brackets it with events.
+// captured) times it with an event pair.  A launcher that takes the two
+// events (fn(start, stop); both null when off) stamps them at its kernel's
+// own start and end, so the time excludes the dispatch; otherwise the events
+// are recorded around fn().
 template <typename Fn>
 int timed(rh_ctx* ctx, int cls, Fn&& fn) {
     Prof& p = ctx->prof[cls];
     const bool on = p.on && !ctx->capturing;
+    constexpr bool attached = std::is_invocable_v<Fn, hipEvent_t, hipEvent_t>;
     hipEvent_t a = nullptr, b = nullptr;
     if (on) {
         HCK(hipEventCreate(&a));
         HCK(hipEventCreate(&b));
-        HCK(hipEventRecord(a, ctx->stream));
+        if constexpr (!attached) HCK(hipEventRecord(a, ctx->stream));
     }
-    hipError_t e = fn();
+    hipError_t e;
+    if constexpr (attached)
+        e = fn(a, b);
+    else
+        e = fn();
     if (e != hipSuccess) return fail(ctx, RH_EDEVICE, std::string("kernel launch: ") + hipGetErrorString(e));
     if (on) {
-        HCK(hipEventRecord(b, ctx->stream));
+        if constexpr (!attached) HCK(hipEventRecord(b, ctx->stream));
         p.ev.emplace_back(a, b);
     }
     return RH_OK;

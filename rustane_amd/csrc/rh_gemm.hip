@@ -30,6 +30,8 @@
 #include <algorithm>
 #include <type_traits>
 
+#include <hip/hip_ext.h>
+
 #include "rh_device.h"
 #include "rh_kernels.h"
 
@@ -527,11 +529,16 @@ hipError_t launch_tile(const GemmArgs& a, bool sk, hipStream_t st) {
             return hipErrorInvalidValue;  // stream-K partials use the 32x32 layout
         } else {
             if (!a.sk_part || (size_t)SK_P * 2 * Tl::BN * Tl::BM > a.sk_part_floats) return hipErrorInvalidValue;
+            if (a.prof_start && hipEventRecord(a.prof_start, st) != hipSuccess) return hipErrorInvalidValue;
             hipLaunchKernelGGL((gemm_kernel<Tl, EPI, MODE_SK>), dim3(SK_P), dim3(Tl::NT), 0, st, a, SK_P, T);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL((gemm_fixup_kernel<Tl, EPI>), dim3(tiles, Tl::FTN), dim3(Tl::NT), 0, st, a, SK_P, T);
+            if (a.prof_stop && hipEventRecord(a.prof_stop, st) != hipSuccess) return hipErrorInvalidValue;
         }
+    } else if (a.prof_start) {
+        hipExtLaunchKernelGGL((gemm_kernel<Tl, EPI, MODE_DP>), dim3(tiles), dim3(Tl::NT), 0, st, a.prof_start,
+                              a.prof_stop, 0u, a, 1, T);
     } else {
         hipLaunchKernelGGL((gemm_kernel<Tl, EPI, MODE_DP>), dim3(tiles), dim3(Tl::NT), 0, st, a, 1, T);
     }
@@ -544,7 +551,9 @@ hipError_t launch_split(const GemmArgs& a, int S, hipStream_t st) {
     const int tiles = ((a.N + Tl::BN - 1) / Tl::BN) * ((a.M + Tl::BM - 1) / Tl::BM);
     if (S < 1 || S > a.K / Tl::KI || !a.sk_part || (size_t)S * a.M * a.N > a.sk_part_floats)
         return hipErrorInvalidValue;
+    if (a.prof_start && hipEventRecord(a.prof_start, st) != hipSuccess) return hipErrorInvalidValue;
     hipLaunchKernelGGL((gemm_kernel<Tl, EPI_F32, MODE_SPLIT>), dim3(tiles * S), dim3(Tl::NT), 0, st, a, S, 0LL);
+    if (a.prof_stop && hipEventRecord(a.prof_stop, st) != hipSuccess) return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

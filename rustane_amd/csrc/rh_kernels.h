@@ -35,6 +35,10 @@ struct GemmArgs {
     float* sk_part;
     size_t sk_part_floats;
     int force_cfg;  // 0 = heuristic; otherwise a GemmCfg value (tuning)
+    // Optional timing: stamped at the kernel's own start and end by the
+    // one-block-per-tile launch (hipExtLaunchKernelGGL), recorded around the
+    // launches otherwise.
+    hipEvent_t prof_start, prof_stop;
 };
 // Tile configurations of the prefill GEMM (all: direct-to-LDS 4-stage
 // pipeline; waves x per-wave tile).

@@ -150,7 +150,10 @@ int enqueue_body(rh_ctx* ctx, int B, int S, bool to_cache, bool final_norm) {
         g.W = W.w13; g.X = ctx->xn; g.M = M; g.N = 2 * F; g.K = D;
         g.out_f16 = ctx->gate; g.ldo = F;
         set_sk(ctx, g);
-        RCK(timed(ctx, RH_K_GEMM_W13, [&] { return rh::launch_gemm(rh::EPI_SWIGLU, g, st); }));
+        RCK(timed(ctx, RH_K_GEMM_W13, [&](hipEvent_t t0, hipEvent_t t1) {
+            g.prof_start = t0; g.prof_stop = t1;
+            return rh::launch_gemm(rh::EPI_SWIGLU, g, st);
+        }));
         g = rh::GemmArgs{};
         g.W = W.w2; g.X = ctx->gate; g.M = M; g.N = D; g.K = F;
         g.out_f32 = ctx->x; g.ldo = D; g.alpha = alpha;

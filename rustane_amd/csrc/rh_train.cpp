@@ -229,7 +229,10 @@ int enqueue_forward_train(rh_ctx* ctx, int B, int S) {
         g.W = W.w13; g.X = cc.x2n; g.M = M; g.N = 2 * F; g.K = D;
         g.out_f16 = cc.gate; g.ldo = F; g.h13 = cc.h13;
         set_sk(ctx, g);
-        RCK(timed(ctx, RH_K_GEMM_W13, [&] { return rh::launch_gemm(rh::EPI_SWIGLU_SAVE, g, st); }));
+        RCK(timed(ctx, RH_K_GEMM_W13, [&](hipEvent_t t0, hipEvent_t t1) {
+            g.prof_start = t0; g.prof_stop = t1;
+            return rh::launch_gemm(rh::EPI_SWIGLU_SAVE, g, st);
+        }));
         const bool last = l + 1 == c.nlayers;
         g = rh::GemmArgs{};
         g.W = W.w2; g.X = cc.gate; g.M = M; g.N = D; g.K = F;
