@@ -13,8 +13,8 @@
 //
 // Tile policy: DTile (below) -- both operands in fragment order in HBM, moved
 // global -> LDS by DMA through a 4-stage pipeline of 32-wide k slices,
-// 32x32x16 MFMA (16x16x32 for the 8-wave 192-row tiles and the W2 split)
-// on fragments double-buffered in registers.  Instantiated as
+// 32x32x16 MFMA (16x16x32 for the 8-wave 192x256, 192x128 and 256x128
+// tiles) on fragments double-buffered in registers.  Instantiated as
 // 256x256 (8 waves of 128x64, or 4 waves of 128x128 with AGPR accumulators),
 // 256x128, 192x256, 192x128 and 128x128; a cost model picks one per shape.
 // Out-of-range rows are clamped, not predicated (they only feed accumulator
@@ -590,19 +590,20 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
             }
         }
     }
-    // The 8-wave 192-row tiles run the 16x16x32 form: at M = 512 (7B) W1|W3
-    // takes 84.5 us as 8-wave 16x16x32 192x256, against 87.8 as a 4-wave
-    // 16x16x32 tile and 91.4 as 8-wave 32x32x16; QKV 60.4 us as 8-wave
-    // 16x16x32 192x128 against 64.7 as 4-wave 32x32x16.  The 4-wave 192x128
-    // tile stays 32x32x16: the weight-gradient GEMMs need its two blocks per
-    // CU, which the 16x16x32 form's extra registers would cost; the 8-wave
-    // 256-wide tiles spill in that form.
+    // The 8-wave 192x256, 192x128 and 256x128 tiles run the 16x16x32 form: at
+    // M = 512 (7B) W1|W3 takes 84.5 us as 8-wave 16x16x32 192x256, against
+    // 87.8 as a 4-wave 16x16x32 tile and 91.4 as 8-wave 32x32x16; QKV 60.4 us
+    // as 8-wave 16x16x32 192x128 against 64.7 as 4-wave 32x32x16; the 8-wave
+    // 256x128 tile is 0-12% faster in that form on every shape timed.  The
+    // 4-wave 192x128 tile stays 32x32x16: the weight-gradient GEMMs need its
+    // two blocks per CU, which the 16x16x32 form's extra registers would
+    // cost; the 8-wave 256x256 tile spills in that form.
     switch (cfg) {
         case GCFG_D8_256x256: return launch_tile<DTile<2, 4, 4, 2>, EPI>(a, false, st);
         case GCFG_D8_256x256_SK: return launch_tile<DTile<2, 4, 4, 2>, EPI>(a, true, st);
         case GCFG_D4_128x128: return launch_tile<DTile<2, 2, 2, 2>, EPI>(a, false, st);
         case GCFG_D4_128x128_SK: return launch_tile<DTile<2, 2, 2, 2>, EPI>(a, true, st);
-        case GCFG_D8_256x128: return launch_tile<DTile<4, 2, 2, 2>, EPI>(a, false, st);
+        case GCFG_D8_256x128: return launch_tile<DTile<4, 2, 2, 2, true>, EPI>(a, false, st);
         case GCFG_D8_256x128_SK: return launch_tile<DTile<4, 2, 2, 2>, EPI>(a, true, st);
         case GCFG_D4_256x256: return launch_tile<DTile<2, 2, 4, 4>, EPI>(a, false, st);
         case GCFG_D4_256x256_SK: return launch_tile<DTile<2, 2, 4, 4>, EPI>(a, true, st);

@@ -48,7 +48,7 @@ enum GemmCfg {
     GCFG_D8_256x256_SK = 7,  // ... stream-K
     GCFG_D4_128x128 = 8,     // 4 waves (64x64 each)
     GCFG_D4_128x128_SK = 9,
-    GCFG_D8_256x128 = 10,    // 8 waves (64x64 each)
+    GCFG_D8_256x128 = 10,    // 8 waves (64x64 each), 16x16x32 MFMA
     GCFG_D8_256x128_SK = 11,
     GCFG_D4_256x256 = 12,    // 4 waves (128x128 each, accumulators in AGPRs)
     GCFG_D4_256x256_SK = 13,
