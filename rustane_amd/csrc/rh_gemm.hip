@@ -24,7 +24,9 @@
 // Stream-K: P blocks split the tiles x k-iterations space evenly.  A
 // block whose range covers only part of a tile stores its fp32 partial; a
 // second kernel sums each split tile's partials in block order
-// (deterministic) and runs the epilogue.  Blocks never communicate inside a
+// (deterministic) and runs the epilogue.  Partials are each thread's own
+// accumulator quads, so both MFMA forms use the same format (the long-K
+// narrow outputs take the 8-wave 16x16x32 256x128 tile).  Blocks never communicate inside a
 // kernel: on this multi-XCD part the per-XCD L2s are not coherent, and a
 // device-scope fence costs an L2 writeback + invalidate.
 #include <algorithm>
@@ -411,6 +413,34 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs& a, int nw, int mw, 
         epilogue<Tl::FTN, Tl::FTM, EPI>(a, nw, mw, acc);
 }
 
+// The accumulators of a thread as TN*TM*4 quads of 4 floats (the stream-K
+// partial format; the same thread stores and reloads them).  32x32: quad
+// (i*TM + j)*4 + q = acc.v[i][j][4q..4q+3]; 16x16: quad a*NB + b = acc.v[a][b].
+template <int TN, int TM>
+__device__ __forceinline__ f32x4 get_quad(const Frag<TN, TM>& f, int x) {
+    const f32x16& v = f.v[x / (TM * 4)][(x / 4) % TM];
+    const int e = 4 * (x % 4);
+    return f32x4{v[e], v[e + 1], v[e + 2], v[e + 3]};
+}
+template <int TN, int TM>
+__device__ __forceinline__ void set_quad(Frag<TN, TM>& f, int x, f32x4 q) {
+    f32x16& v = f.v[x / (TM * 4)][(x / 4) % TM];
+    const int e = 4 * (x % 4);
+    v[e] = q[0]; v[e + 1] = q[1]; v[e + 2] = q[2]; v[e + 3] = q[3];
+}
+template <int NA, int NB>
+__device__ __forceinline__ f32x4 get_quad(const Frag16<NA, NB>& f, int x) { return f.v[x / NB][x % NB]; }
+template <int NA, int NB>
+__device__ __forceinline__ void set_quad(Frag16<NA, NB>& f, int x, f32x4 q) { f.v[x / NB][x % NB] = q; }
+// The quads of 32-row slice s of a wave's tile and the type holding them:
+// 32x32: row tile s (TM tiles x 4 quads); 16x16: A tiles 2s, 2s+1 (2 x NB).
+template <class Tl>
+struct Slice {
+    static constexpr int NQ = Tl::FTM * 4;
+    using Acc = std::conditional_t<Tl::kM16, Frag16<2, Tl::NB>, Frag<1, Tl::FTM>>;
+    __device__ static int quad_of(int s, int x) { return s * NQ + x; }  // both layouts: slice-major
+};
+
 // MODE: MODE_DP one block per tile; MODE_SK stream-K over P blocks (T =
 // tiles x k-iterations); MODE_SPLIT P even k-splits per tile, each storing its
 // fp32 partial [M][N] at sk_part + split * M * N.
@@ -442,8 +472,8 @@ __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long lo
         b.alpha = 0.f;  // raw partials: the row kernel applies alpha once to their sum
         run_epilogue<Tl, EPI_F32>(b, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
     } else {
-        constexpr int TN = Tl::FTN, TM = Tl::FTM, NT = Tl::NT;
-        constexpr int NV = TN * TM * 4;  // f32x4 per thread per partial tile
+        constexpr int NT = Tl::NT;
+        constexpr int NV = Tl::FTN * Tl::FTM * 4;  // f32x4 per thread per partial tile
         const int tid = threadIdx.x;
         const int lp = xcd_remap(blockIdx.x, P);
         const long long it0 = (long long)lp * T / P, it1 = (long long)(lp + 1) * T / P;
@@ -456,21 +486,14 @@ __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long lo
             const int n0 = nb * Tl::BN, m0 = mb * Tl::BM;
             Tl::run(a, n0, m0, kb, ke, acc, sm);
             if (kb == 0 && ke == KT) {
-                epilogue<TN, TM, EPI>(a, Tl::nw(n0), Tl::mw(m0), acc);
+                run_epilogue<Tl, EPI>(a, Tl::nw(n0), Tl::mw(m0), acc);
             } else {
                 // A block's first segment goes to slot 0, its last to slot 1;
                 // the fixup kernel merges them once this kernel has finished.
                 const int slot = (it == it0) ? 0 : 1;
                 f32x4* mine = (f32x4*)a.sk_part + ((size_t)(lp * 2 + slot) * NV) * NT + tid;
 #pragma unroll
-                for (int i = 0; i < TN; ++i)
-#pragma unroll
-                    for (int j = 0; j < TM; ++j)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            mine[(size_t)((i * TM + j) * 4 + q) * NT] =
-                                f32x4{acc.v[i][j][4 * q], acc.v[i][j][4 * q + 1], acc.v[i][j][4 * q + 2],
-                                      acc.v[i][j][4 * q + 3]};
+                for (int x = 0; x < NV; ++x) mine[(size_t)x * NT] = get_quad(acc, x);
             }
             it = (long long)tile * KT + ke;
         }
@@ -483,40 +506,31 @@ __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long lo
 // the epilogue on the slice.
 template <class Tl, int EPI>
 __global__ __launch_bounds__(Tl::NT) void gemm_fixup_kernel(GemmArgs a, int P, long long T) {
-    constexpr int TN = Tl::FTN, TM = Tl::FTM, NT = Tl::NT;
-    constexpr int NV = TN * TM * 4;
-    constexpr int SL = 1;
+    using Sl = Slice<Tl>;
+    constexpr int NT = Tl::NT, NV = Tl::FTN * Tl::FTM * 4, NQ = Sl::NQ;
     const int nbM = (a.M + Tl::BM - 1) / Tl::BM;
     const int KT = a.K / Tl::KI;
-    const int tile = blockIdx.x, i0 = blockIdx.y * SL, tid = threadIdx.x;
+    const int tile = blockIdx.x, i0 = blockIdx.y, tid = threadIdx.x;
     const long long tb = (long long)tile * KT, te = tb + KT;
     const int pf = (int)(((tb + 1) * P - 1) / T), pl = (int)((te * P - 1) / T);
     if (pf == pl) return;
-    Frag<SL, TM> acc;
+    typename Sl::Acc acc;
 #pragma unroll
-    for (int i = 0; i < SL; ++i)
-#pragma unroll
-        for (int j = 0; j < TM; ++j) acc.v[i][j] = f32x16{};
+    for (int x = 0; x < NQ; ++x) set_quad(acc, x, f32x4{});
     for (int c = pf; c <= pl; ++c) {
         // with fewer iterations than blocks some blocks own none and wrote nothing
         if ((long long)c * T / P == (long long)(c + 1) * T / P) continue;
         const int cslot = ((long long)c * T / P >= tb) ? 0 : 1;
         const f32x4* part = (const f32x4*)a.sk_part + ((size_t)(c * 2 + cslot) * NV) * NT + tid;
 #pragma unroll
-        for (int i = 0; i < SL; ++i)
-#pragma unroll
-            for (int j = 0; j < TM; ++j)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const f32x4 o = part[(size_t)(((i0 + i) * TM + j) * 4 + q) * NT];
-                    acc.v[i][j][4 * q] += o[0];
-                    acc.v[i][j][4 * q + 1] += o[1];
-                    acc.v[i][j][4 * q + 2] += o[2];
-                    acc.v[i][j][4 * q + 3] += o[3];
-                }
+        for (int x = 0; x < NQ; ++x) set_quad(acc, x, get_quad(acc, x) + part[(size_t)Sl::quad_of(i0, x) * NT]);
     }
     const int nb = tile / nbM, mb = tile - nb * nbM;
-    epilogue<SL, TM, EPI>(a, Tl::nw(nb * Tl::BN) + 32 * i0, Tl::mw(mb * Tl::BM), acc);
+    const int nw = Tl::nw(nb * Tl::BN) + 32 * i0, mw = Tl::mw(mb * Tl::BM);
+    if constexpr (Tl::kM16)
+        epilogue<2, Tl::NB, EPI>(a, nw, mw, acc);
+    else
+        epilogue<1, Tl::FTM, EPI>(a, nw, mw, acc);
 }
 
 template <class Tl, int EPI>
@@ -525,17 +539,13 @@ hipError_t launch_tile(const GemmArgs& a, bool sk, hipStream_t st) {
     const int tiles = nbN * nbM;
     const long long T = (long long)tiles * (a.K / Tl::KI);
     if (sk) {
-        if constexpr (Tl::kM16) {
-            return hipErrorInvalidValue;  // stream-K partials use the 32x32 layout
-        } else {
-            if (!a.sk_part || (size_t)SK_P * 2 * Tl::BN * Tl::BM > a.sk_part_floats) return hipErrorInvalidValue;
-            if (a.prof_start && hipEventRecord(a.prof_start, st) != hipSuccess) return hipErrorInvalidValue;
-            hipLaunchKernelGGL((gemm_kernel<Tl, EPI, MODE_SK>), dim3(SK_P), dim3(Tl::NT), 0, st, a, SK_P, T);
-            const hipError_t e = hipGetLastError();
-            if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((gemm_fixup_kernel<Tl, EPI>), dim3(tiles, Tl::FTN), dim3(Tl::NT), 0, st, a, SK_P, T);
-            if (a.prof_stop && hipEventRecord(a.prof_stop, st) != hipSuccess) return hipErrorInvalidValue;
-        }
+        if (!a.sk_part || (size_t)SK_P * 2 * Tl::BN * Tl::BM > a.sk_part_floats) return hipErrorInvalidValue;
+        if (a.prof_start && hipEventRecord(a.prof_start, st) != hipSuccess) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((gemm_kernel<Tl, EPI, MODE_SK>), dim3(SK_P), dim3(Tl::NT), 0, st, a, SK_P, T);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((gemm_fixup_kernel<Tl, EPI>), dim3(tiles, Tl::FTN), dim3(Tl::NT), 0, st, a, SK_P, T);
+        if (a.prof_stop && hipEventRecord(a.prof_stop, st) != hipSuccess) return hipErrorInvalidValue;
     } else if (a.prof_start) {
         hipExtLaunchKernelGGL((gemm_kernel<Tl, EPI, MODE_DP>), dim3(tiles), dim3(Tl::NT), 0, st, a.prof_start,
                               a.prof_stop, 0u, a, 1, T);
@@ -578,7 +588,7 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         const int t128 = ((a.N + 127) / 128) * ((a.M + 127) / 128);
         const bool sk_ok = a.sk_part && (size_t)SK_P * 2 * 256 * 256 <= a.sk_part_floats;
         if (sk_ok && a.K >= 8192 && t256x128 < 160 && t256x128 * KT >= 2 * SK_P) {
-            cfg = GCFG_D4_256x128_SK;
+            cfg = GCFG_D8_256x128_SK;
         } else if (sk_ok && t128 < 160 && t128 * KT >= 2 * SK_P) {
             cfg = GCFG_D4_128x128_SK;
         } else {
@@ -604,7 +614,7 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         case GCFG_D4_128x128: return launch_tile<DTile<2, 2, 2, 2>, EPI>(a, false, st);
         case GCFG_D4_128x128_SK: return launch_tile<DTile<2, 2, 2, 2>, EPI>(a, true, st);
         case GCFG_D8_256x128: return launch_tile<DTile<4, 2, 2, 2, true>, EPI>(a, false, st);
-        case GCFG_D8_256x128_SK: return launch_tile<DTile<4, 2, 2, 2>, EPI>(a, true, st);
+        case GCFG_D8_256x128_SK: return launch_tile<DTile<4, 2, 2, 2, true>, EPI>(a, true, st);
         case GCFG_D4_256x256: return launch_tile<DTile<2, 2, 4, 4>, EPI>(a, false, st);
         case GCFG_D4_256x256_SK: return launch_tile<DTile<2, 2, 4, 4>, EPI>(a, true, st);
         case GCFG_D4_256x128: return launch_tile<DTile<2, 2, 4, 2>, EPI>(a, false, st);
@@ -613,7 +623,7 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         case GCFG_D8_192x128: return launch_tile<DTile<2, 4, 3, 1, true>, EPI>(a, false, st);
         case GCFG_D4_192x128_SK: return launch_tile<DTile<2, 2, 3, 2>, EPI>(a, true, st);
         case GCFG_D8_192x256: return launch_tile<DTile<2, 4, 3, 2, true>, EPI>(a, false, st);
-        case GCFG_D8_192x256_SK: return launch_tile<DTile<2, 4, 3, 2>, EPI>(a, true, st);
+        case GCFG_D8_192x256_SK: return launch_tile<DTile<2, 4, 3, 2, true>, EPI>(a, true, st);
         case GCFG_D4_192x256: return launch_tile<DTile<2, 2, 3, 4>, EPI>(a, false, st);
         case GCFG_D4_192x256_SK: return launch_tile<DTile<2, 2, 3, 4>, EPI>(a, true, st);
     }
