@@ -13,8 +13,8 @@
 //
 // Tile policy: DTile (below) -- both operands in fragment order in HBM, moved
 // global -> LDS by DMA through a 4-stage pipeline of 32-wide k slices,
-// 32x32x16 MFMA (16x16x32 for the 8-wave 192x256, 192x128 and 256x128
-// tiles) on fragments double-buffered in registers.  Instantiated as
+// 32x32x16 MFMA (16x16x32 for the 8-wave tiles but 256x256) on fragments
+// double-buffered in registers.  Instantiated as
 // 256x256 (8 waves of 128x64, or 4 waves of 128x128 with AGPR accumulators),
 // 256x128, 192x256, 192x128 and 128x128; a cost model picks one per shape.
 // Out-of-range rows are clamped, not predicated (they only feed accumulator
@@ -582,7 +582,7 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         struct Cand { int cfg, bn, bm; float rate; };
         constexpr Cand dp[] = {{GCFG_D8_256x256, 256, 256, 4.4f}, {GCFG_D8_192x256, 192, 256, 4.35f},
                                {GCFG_D8_256x128, 256, 128, 3.6f}, {GCFG_D8_192x128, 192, 128, 3.7f},
-                               {GCFG_D4_128x128, 128, 128, 3.0f}};
+                               {GCFG_D8_128x128, 128, 128, 3.0f}};
         const long long KT = a.K / 32;
         const int t256x128 = ((a.N + 255) / 256) * ((a.M + 127) / 128);
         const int t128 = ((a.N + 127) / 128) * ((a.M + 127) / 128);
@@ -590,7 +590,7 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         if (sk_ok && a.K >= 8192 && t256x128 < 160 && t256x128 * KT >= 2 * SK_P) {
             cfg = GCFG_D8_256x128_SK;
         } else if (sk_ok && t128 < 160 && t128 * KT >= 2 * SK_P) {
-            cfg = GCFG_D4_128x128_SK;
+            cfg = GCFG_D8_128x128_SK;
         } else {
             float best = 3.0e38f;
             for (const Cand& c : dp) {
@@ -600,11 +600,12 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
             }
         }
     }
-    // The 8-wave 192x256, 192x128 and 256x128 tiles run the 16x16x32 form: at
-    // M = 512 (7B) W1|W3 takes 84.5 us as 8-wave 16x16x32 192x256, against
-    // 87.8 as a 4-wave 16x16x32 tile and 91.4 as 8-wave 32x32x16; QKV 60.4 us
-    // as 8-wave 16x16x32 192x128 against 64.7 as 4-wave 32x32x16; the 8-wave
-    // 256x128 tile is 0-12% faster in that form on every shape timed.  The
+    // The 8-wave 192x256, 192x128, 256x128 and 128x128 tiles run the
+    // 16x16x32 form: at M = 512 (7B) W1|W3 takes 84.5 us as 8-wave 16x16x32
+    // 192x256, against 87.8 as a 4-wave 16x16x32 tile and 91.4 as 8-wave
+    // 32x32x16; QKV 60.4 us as 8-wave 16x16x32 192x128 against 64.7 as 4-wave
+    // 32x32x16; the 8-wave 256x128 and 128x128 tiles are 0-12% and 1-6%
+    // faster in that form than their 32x32x16 twins on every shape timed.  The
     // 4-wave 192x128 tile stays 32x32x16: the weight-gradient GEMMs need its
     // two blocks per CU, which the 16x16x32 form's extra registers would
     // cost; the 8-wave 256x256 tile spills in that form.
@@ -621,6 +622,9 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         case GCFG_D4_256x128_SK: return launch_tile<DTile<2, 2, 4, 2>, EPI>(a, true, st);
         case GCFG_D4_192x128: return launch_tile<DTile<2, 2, 3, 2>, EPI>(a, false, st);
         case GCFG_D8_192x128: return launch_tile<DTile<2, 4, 3, 1, true>, EPI>(a, false, st);
+        case GCFG_D8_192x128_SK: return launch_tile<DTile<2, 4, 3, 1, true>, EPI>(a, true, st);
+        case GCFG_D8_128x128: return launch_tile<DTile<2, 4, 2, 1, true>, EPI>(a, false, st);
+        case GCFG_D8_128x128_SK: return launch_tile<DTile<2, 4, 2, 1, true>, EPI>(a, true, st);
         case GCFG_D4_192x128_SK: return launch_tile<DTile<2, 2, 3, 2>, EPI>(a, true, st);
         case GCFG_D8_192x256: return launch_tile<DTile<2, 4, 3, 2, true>, EPI>(a, false, st);
         case GCFG_D8_192x256_SK: return launch_tile<DTile<2, 4, 3, 2, true>, EPI>(a, true, st);

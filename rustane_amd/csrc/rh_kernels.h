@@ -60,7 +60,10 @@ enum GemmCfg {
     GCFG_D8_192x256_SK = 19,
     GCFG_D4_192x256 = 20,    // 4 waves (96x128 each, accumulators in AGPRs)
     GCFG_D4_192x256_SK = 21,
-    GCFG_D8_192x128 = 24,    // 8 waves (96x32 each), 16x16x32 MFMA (no stream-K twin)
+    GCFG_D8_192x128 = 24,    // 8 waves (96x32 each), 16x16x32 MFMA
+    GCFG_D8_192x128_SK = 25,
+    GCFG_D8_128x128 = 26,    // 8 waves (64x32 each), 16x16x32 MFMA
+    GCFG_D8_128x128_SK = 27,
 };
 // Floats of stream-K workspace any prefill GEMM needs.
 size_t gemm_sk_part_floats();

@@ -3,7 +3,7 @@
 The forward only reaches the tile configurations its shape heuristic picks
 for the model widths under test.  Through the GEMM test harness
 (rustane_amd/librustane_gemm_harness.so) each configuration -- one block per
-tile (including the 16x16x32 8-wave 192-row tiles), stream-K with its fix-up kernel,
+tile (including the 16x16x32 8-wave tiles), stream-K with its fix-up kernel,
 split-K with the summing residual + RMSNorm row kernel -- runs every epilogue
 on ragged shapes (M, N not multiples of any tile) and is checked against a
 float64 numpy product of the same fp16 operands:
@@ -29,9 +29,9 @@ LIB = os.path.join(os.path.dirname(HERE), "rustane_amd", "librustane_gemm_harnes
 EPI_F32, EPI_RESID, EPI_SWIGLU, EPI_QKV, EPI_SWIGLU_SAVE, EPI_SILU_BWD = 0, 1, 2, 3, 4, 5
 # GemmCfg values (rh_kernels.h): one block per tile, and their stream-K twins
 DP = {"D8_256x256": 6, "D4_128x128": 8, "D8_256x128": 10, "D4_256x256": 12, "D4_256x128": 14,
-      "D4_192x128": 16, "D8_192x256": 18, "D4_192x256": 20}
+      "D4_192x128": 16, "D8_192x256": 18, "D4_192x256": 20, "D8_192x128": 24, "D8_128x128": 26}
 SK = {k + "_SK": v + 1 for k, v in DP.items()}
-CFGS = {"auto": 0, **DP, **SK, "D8_192x128": 24}
+CFGS = {"auto": 0, **DP, **SK}
 
 
 @pytest.fixture(scope="module")
