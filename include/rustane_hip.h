@@ -154,8 +154,10 @@ void* rh_stream(rh_ctx* ctx);
 
 /* Per-kernel-class timing with HIP events on the context stream: while
  * enabled, every launch of `kernel_class` in the forward, prefill and decode calls is
- * bracketed by an event pair; rh_profile_read returns the summed time and
- * the launch count since rh_profile_enable.  Classes: */
+ * timed by an event pair (bracketing the launch; for RH_K_GEMM_W13 stamped at
+ * the GEMM kernel's own start and end); rh_profile_read returns the summed
+ * time and the launch count since rh_profile_enable.  Not a reference
+ * interface: it serves the benchmark's per-kernel roofline figure.  Classes: */
 #define RH_K_GEMM_QKV 0
 #define RH_K_GEMM_WO 1
 #define RH_K_GEMM_W13 2

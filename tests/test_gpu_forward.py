@@ -156,3 +156,30 @@ def test_weights_roundtrip():
     for lw, got in zip(w.layers, layers):
         for a, b in zip(lw.tensors(), got):
             np.testing.assert_array_equal(a, b)
+
+
+def test_profile_counts_and_times_launches(orc):
+    """rh_profile_*: one W1|W3 GEMM and one QKV GEMM per layer and forward,
+    positive times (the W1|W3 events are stamped at the kernel's own start
+    and end), the profiled forward still equal to an unprofiled one, and
+    nothing counted once profiling is off."""
+    import time
+    cfg = small_cfg()
+    w = ModelWeights.normal(cfg, seed=21)
+    tok, tgt = tokens_uniform(22, cfg.vocab, 1, cfg.seq)
+    with _ctx(cfg, w) as c:
+        ref = c.forward(tok, tgt)
+        c.profile_enable(hb.K_GEMM_W13, True)
+        c.profile_enable(hb.K_GEMM_QKV, True)
+        t0 = time.perf_counter()
+        outs = [c.forward(tok, tgt) for _ in range(3)]
+        wall_ms = (time.perf_counter() - t0) * 1e3
+        w13_ms, w13_n = c.profile_read(hb.K_GEMM_W13)
+        qkv_ms, qkv_n = c.profile_read(hb.K_GEMM_QKV)
+        assert w13_n == 3 * cfg.nlayers and qkv_n == 3 * cfg.nlayers, (w13_n, qkv_n)
+        assert 0.0 < w13_ms < wall_ms and 0.0 < qkv_ms < wall_ms, (w13_ms, qkv_ms, wall_ms)
+        for o in outs:
+            np.testing.assert_array_equal(o.logits, ref.logits)
+        c.profile_enable(hb.K_GEMM_W13, False)
+        c.forward(tok, tgt)
+        assert c.profile_read(hb.K_GEMM_W13)[1] == 0
