@@ -164,6 +164,9 @@ hipError_t launch_ce_backward(const float* logits, const uint32_t* targets, f16*
 // zero in columns R..Rp-1; map 1 reads the W1|W3 interleaved SwiGLU weight
 // as [W1 rows | W3 rows].  C % 128 == 0, Rp % 128 == 0.
 hipError_t launch_transpose_frag(const f16* src, f16* dst, int R, int C, int Rp, int map, hipStream_t st);
+// Two map-0 transposes with the same padded token count in one launch.
+hipError_t launch_transpose_frag2(const f16* src0, f16* dst0, int R0, int C0, const f16* src1, f16* dst1, int R1,
+                                  int C1, int Rp, hipStream_t st);
 // RMSNorm backward over M rows: dx = rmsnorm'(x)^T dy (+ dres), optional
 // fp16 fragment-order copy of hscale * dx, per-block dgamma partials
 // [rms_backward_blocks(M)][D].  dx may alias dres.

@@ -294,8 +294,7 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
     // CE gradient (internal units), dx_final = dl E, dembed += dl^T x_final
     LCK(rh::launch_ce_backward(ctx->logits, ctx->d_tgt, T->dlh, M, V, Vp, c.softcap, rh::GRAD_UNIT, st));
     RCK(data_gemm(ctx, T->dlh, T->embed_t, M, D, Vp, T->gout));
-    LCK(rh::launch_transpose_frag(T->dlh, T->dlT, M, Vp, Mp, 0, st));
-    LCK(rh::launch_transpose_frag(T->xf, T->T1, M, D, Mp, 0, st));
+    LCK(rh::launch_transpose_frag2(T->dlh, T->dlT, M, Vp, T->xf, T->T1, M, D, Mp, st));
     RCK(grad_gemm(ctx, T->dlT, T->T1, V, D, kappa, T->dembed));
     // final RMSNorm backward: dy -> dres, a*dy -> H1 (the last layer's dffn)
     LCK(rh::launch_rms_backward(T->gout, T->xlast, ctx->gfinal, nullptr, T->dres, T->H1, alpha, T->dgp, M, D,
@@ -307,8 +306,7 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         const TrainState::WT& wt = T->wt[l];
         float* const* G = T->dlay[l].data();
         // dW2 += dffn^T gate; dgate = dffn W2; SiLU backward
-        LCK(rh::launch_transpose_frag(T->H1, T->T1, M, D, Mp, 0, st));
-        LCK(rh::launch_transpose_frag(cc.gate, T->T2, M, F, Mp, 0, st));
+        LCK(rh::launch_transpose_frag2(T->H1, T->T1, M, D, cc.gate, T->T2, M, F, Mp, st));
         RCK(grad_gemm(ctx, T->T1, T->T2, D, F, kappa, G[6]));
         {  // dgate = dffn W2 with the SiLU-gate backward in the epilogue -> [dh1 | dh3]
             rh::GemmArgs g{};
@@ -319,8 +317,7 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         }
         // dx_ffn = [dh1 | dh3] [W1 | W3]^T; dW1, dW3 += x2n^T dh
         RCK(data_gemm(ctx, T->H2, wt.w13t, M, D, 2 * F, T->gout));
-        LCK(rh::launch_transpose_frag(T->H2, T->T3, M, 2 * F, Mp, 0, st));
-        LCK(rh::launch_transpose_frag(cc.x2n, T->T1, M, D, Mp, 0, st));
+        LCK(rh::launch_transpose_frag2(T->H2, T->T3, M, 2 * F, cc.x2n, T->T1, M, D, Mp, st));
         RCK(grad_gemm(ctx, T->T1, T->T3, D, F, kappa, G[4]));
         RCK(grad_gemm(ctx, T->T1, T->T3 + (size_t)F * Mp, D, F, kappa, G[5]));
         // dx2 = RMSNorm2'(dx_ffn) + dy (in place in dres); a*dx2 -> H1
@@ -329,8 +326,7 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         RCK(gamma_grad(ctx, nblk, D, kappa, G[8]));
         // da = (a dx2) Wo^T; dWo += attn^T (a dx2)
         RCK(data_gemm(ctx, T->H1, wt.ot, M, D, D, T->gout));
-        LCK(rh::launch_transpose_frag(T->H1, T->T1, M, D, Mp, 0, st));
-        LCK(rh::launch_transpose_frag(cc.attn, T->T2, M, D, Mp, 0, st));
+        LCK(rh::launch_transpose_frag2(T->H1, T->T1, M, D, cc.attn, T->T2, M, D, Mp, st));
         RCK(grad_gemm(ctx, T->T2, T->T1, D, D, kappa, G[3]));
         // attention backward -> dq | dk | dv, RoPE backward, fp16 pack
         float* dqkv = T->gout + (size_t)M * D;  // past da, which the attention kernels read
@@ -339,8 +335,7 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         LCK(rh::launch_rope_backward_pack(dqkv, ctx->rope, T->H2, M, S, D, hd, st));
         // dxn = dqkv [Wq | Wk | Wv]^T; dWq, dWk, dWv += xn^T d{q,k,v}
         RCK(data_gemm(ctx, T->H2, wt.qkvt, M, D, 3 * D, T->gout));
-        LCK(rh::launch_transpose_frag(T->H2, T->T3, M, 3 * D, Mp, 0, st));
-        LCK(rh::launch_transpose_frag(cc.xn, T->T1, M, D, Mp, 0, st));
+        LCK(rh::launch_transpose_frag2(T->H2, T->T3, M, 3 * D, cc.xn, T->T1, M, D, Mp, st));
         for (int j = 0; j < 3; ++j) RCK(grad_gemm(ctx, T->T1, T->T3 + (size_t)j * D * Mp, D, D, kappa, G[j]));
         // dy' = RMSNorm1'(dxn) + dx2 (in place); a*dy' -> H1 (the next layer's dffn)
         LCK(rh::launch_rms_backward(T->gout, cc.xin, W.g1, T->dres, T->dres, T->H1, alpha, T->dgp, M, D,

@@ -8,6 +8,8 @@
 // one divided by kappa = loss_scale / (S * GRAD_UNIT).  Weight gradients are
 // scaled back by kappa where they are accumulated (GEMM epilogue alpha, the
 // gamma reductions, the embedding scatter), in fp32.
+#include <algorithm>
+
 #include "rh_device.h"
 #include "rh_kernels.h"
 
@@ -84,10 +86,22 @@ __device__ __forceinline__ int src_row(int r, int map, int R) {
     return r;
 }
 
-__global__ __launch_bounds__(256) void transpose_frag_kernel(const f16* __restrict__ src, f16* __restrict__ dst,
-                                                             int R, int C, int Rp, int map) {
+// One transpose job; a launch runs one or two (blockIdx.z), so the backward's
+// paired operand transposes take one launch instead of two.
+struct TransposeJob {
+    const f16* src;
+    f16* dst;
+    int R, C, Rp, map;
+};
+
+__global__ __launch_bounds__(256) void transpose_frag_kernel(TransposeJob j0, TransposeJob j1) {
     __shared__ f16 tile[64][64 + 2];
+    const TransposeJob& jb = blockIdx.z ? j1 : j0;
+    const f16* __restrict__ src = jb.src;
+    f16* __restrict__ dst = jb.dst;
+    const int R = jb.R, C = jb.C, Rp = jb.Rp, map = jb.map;
     const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64, tid = threadIdx.x;
+    if (c0 >= C || r0 >= Rp) return;  // the grid covers the larger job (whole block)
     // load: 64 rows x 8 column groups of 8
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
@@ -283,8 +297,16 @@ hipError_t launch_ce_backward(const float* logits, const uint32_t* targets, f16*
 
 hipError_t launch_transpose_frag(const f16* src, f16* dst, int R, int C, int Rp, int map, hipStream_t st) {
     if (C % 128 != 0 || Rp % 128 != 0 || Rp < R || (map == 1 && R % 32 != 0)) return hipErrorInvalidValue;
-    const dim3 grid(C / 64, Rp / 64);
-    hipLaunchKernelGGL(transpose_frag_kernel, grid, dim3(256), 0, st, src, dst, R, C, Rp, map);
+    const TransposeJob j{src, dst, R, C, Rp, map};
+    hipLaunchKernelGGL(transpose_frag_kernel, dim3(C / 64, Rp / 64, 1), dim3(256), 0, st, j, j);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose_frag2(const f16* src0, f16* dst0, int R0, int C0, const f16* src1, f16* dst1, int R1,
+                                  int C1, int Rp, hipStream_t st) {
+    if (C0 % 128 != 0 || C1 % 128 != 0 || Rp % 128 != 0 || Rp < R0 || Rp < R1) return hipErrorInvalidValue;
+    const TransposeJob j0{src0, dst0, R0, C0, Rp, 0}, j1{src1, dst1, R1, C1, Rp, 0};
+    hipLaunchKernelGGL(transpose_frag_kernel, dim3(std::max(C0, C1) / 64, Rp / 64, 2), dim3(256), 0, st, j0, j1);
     return hipGetLastError();
 }
 
