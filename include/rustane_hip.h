@@ -136,6 +136,22 @@ int rh_prefill(rh_ctx* ctx, const uint32_t* tokens, int batch, int len, uint32_t
  * Contract: logits equal the forward's logits at that position. */
 int rh_decode_step(rh_ctx* ctx, const uint32_t* in_tok, uint32_t* out_tok, float* logits_out);
 
+/* rh_decode_step without any allocation: no counterpart in the reference.
+ * For callers that cannot allocate device memory or runtime objects (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  in_tok [batch], out_tok [batch] and logits_out (nullable
+ * [batch, vocab]) are DEVICE pointers; batch must equal the prefill batch.
+ * The step is enqueued on the context stream without synchronising (rh_sync
+ * waits and reports clamped out-of-range ids) and the position advances by
+ * one.  Its scratch (activations, attention partials, argmax partials,
+ * position state; the logits too when logits_out is NULL) lives in a fixed
+ * 64 MiB device array per GPU, shared by every call on that GPU: calls whose
+ * work overlaps on one GPU race.  RH_ERANGE when the batch, model width and
+ * max_ctx need more scratch than that (7B, batch 16, max_ctx 4096 needs
+ * about 12 MiB). */
+int rh_decode_step_noalloc(rh_ctx* ctx, int batch, const uint32_t* in_tok, uint32_t* out_tok,
+                           float* logits_out);
+
 /* nsteps greedy steps run entirely on the device (each step's argmax is the
  * next step's input); out_tokens [nsteps, batch].  Starts from in_tok. */
 int rh_decode(rh_ctx* ctx, const uint32_t* in_tok, int nsteps, uint32_t* out_tokens);

@@ -24,7 +24,7 @@ HARNESS_SOURCES = ["rh_gemm_harness.cpp"]
 HARNESS_DEPS = ["rh_gemm.hip", "rh_rowops.hip"]  # objects of SOURCES it links
 
 SOURCES = ["rh_gemm.hip", "rh_attn.hip", "rh_attn_bwd.hip", "rh_gemv.hip", "rh_rowops.hip", "rh_trainops.hip", "rh_optim.hip",
-           "rh_runtime.cpp", "rh_train.cpp", "rh_data.cpp", "rh_sched.cpp"]
+           "rh_runtime.cpp", "rh_train.cpp", "rh_data.cpp", "rh_sched.cpp", "rh_noalloc.cpp"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CFLAGS = [

@@ -69,7 +69,9 @@ struct rh_ctx {
     bool use_graphs = true;
     hipGraphExec_t dgraph = nullptr;
     int dgraph_B = 0;
-    bool capturing = false;
+    // no profiling events while set: a graph is being captured, or the call
+    // must not create runtime objects (rh_decode_step_noalloc)
+    bool events_off = false;
 
     float* staging = nullptr;
     size_t staging_elems = 0;
@@ -135,7 +137,7 @@ void dfree(rh_ctx* ctx, void* p);
 template <typename Fn>
 int timed(rh_ctx* ctx, int cls, Fn&& fn) {
     Prof& p = ctx->prof[cls];
-    const bool on = p.on && !ctx->capturing;
+    const bool on = p.on && !ctx->events_off;
     constexpr bool attached = std::is_invocable_v<Fn, hipEvent_t, hipEvent_t>;
     hipEvent_t a = nullptr, b = nullptr;
     if (on) {
@@ -178,5 +180,32 @@ int check_err_flag(rh_ctx* ctx);
 // Logits (+ CE loss rows and per-sequence means) from the final-norm rows in
 // ctx->xn, or in xf when given.
 int enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss, const f16* xf = nullptr);
+
+// Device buffers one greedy decode step uses besides the weights and the KV
+// cache: the residual rows, normalised rows, q, attention output and gate of
+// the B tokens, the logits, the attention's per-chunk partials, the logits
+// GEMV's argmax partials, the position state, and the token in/out arrays.
+struct DecodeBufs {
+    float* dx;                 // [B][D] fp32 residual stream
+    f16 *dxn, *dq, *dattn;     // [B][D]
+    f16* dgate;                // [B][F]
+    float* dlogits;            // [B][V]
+    float *pm, *pl, *po;       // [B][H][chunks] (m, l), [B][H][chunks][hd] o
+    float* am_v;               // [gemv_argmax_blocks(V)][16]
+    int* am_i;
+    int* state;                // [2]: position, step
+    const uint32_t* tok_in;    // [B] token ids of this step
+    uint32_t* tok_out;         // [B] argmax ids
+    uint32_t* next_in;         // nullable: argmax ids again, as the next step's input
+    uint32_t* seq;             // nullable: argmax ids at seq[state[1] * B + b]
+};
+// The context's own decode buffers (allocated by rh_create).
+DecodeBufs ctx_decode_bufs(rh_ctx* ctx);
+// One decode step for B tokens at position state[0] (then state += 1).
+int enqueue_decode_step(rh_ctx* ctx, int B, const DecodeBufs& b);
+// Resolves the device address of the fixed scratch array of
+// rh_decode_step_noalloc on ctx->device (once per device; the device must be
+// current).  Called by rh_create.
+int noalloc_init(rh_ctx* ctx);
 
 }  // namespace rhrt

@@ -184,12 +184,10 @@ int rhrt::enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss, const f16* xf)
     return RH_OK;
 }
 
-namespace {
-
-// One decode step for B tokens at position dstate[0].  For small B the
+// One decode step for B tokens at position b.state[0].  For small B the
 // RMSNorms run inside the QKV / W1|W3 / logits GEMVs (one launch fewer per
 // norm); otherwise a row kernel writes the normalised rows first.
-int enqueue_decode_step(rh_ctx* ctx, int B) {
+int rhrt::enqueue_decode_step(rh_ctx* ctx, int B, const DecodeBufs& b) {
     const rh_config& c = ctx->cfg;
     const int D = c.dim, F = c.hidden;
     const float alpha = 1.0f / std::sqrt(2.0f * (float)c.nlayers);
@@ -198,14 +196,14 @@ int enqueue_decode_step(rh_ctx* ctx, int B) {
     // input of a normed GEMV: fused (xres + gamma) or via the row kernel (X)
     auto normed = [&](rh::GemvArgs& g, const float* gamma) -> int {
         if (fuse_norm) {
-            g.xres = ctx->dx; g.gamma = gamma; g.eps = c.rms_eps;
+            g.xres = b.dx; g.gamma = gamma; g.eps = c.rms_eps;
         } else {
-            LCK(rh::launch_rmsnorm(ctx->dx, gamma, ctx->dxn, B, D, c.rms_eps, st));
-            g.X = ctx->dxn;
+            LCK(rh::launch_rmsnorm(b.dx, gamma, b.dxn, B, D, c.rms_eps, st));
+            g.X = b.dxn;
         }
         return RH_OK;
     };
-    LCK(rh::launch_embed(ctx->dtok, ctx->embed, ctx->dx, B, D, c.vocab, ctx->d_err, st));
+    LCK(rh::launch_embed(b.tok_in, ctx->embed, b.dx, B, D, c.vocab, ctx->d_err, st));
     for (int l = 0; l < c.nlayers; ++l) {
         const Layer& W = ctx->L[l];
         f16* kc = ctx->kcache + (size_t)l * ctx->kv_layer;
@@ -213,40 +211,52 @@ int enqueue_decode_step(rh_ctx* ctx, int B) {
         rh::GemvArgs g{};
         RCK(normed(g, W.g1));
         g.W = W.wqkv; g.B = B; g.N = 3 * D; g.K = D;
-        g.out_f16 = ctx->dq; g.kc = kc; g.vc = vc; g.rope = ctx->rope; g.pos = ctx->dstate;
+        g.out_f16 = b.dq; g.kc = kc; g.vc = vc; g.rope = ctx->rope; g.pos = b.state;
         g.D = D; g.H = c.heads; g.hd = c.head_dim; g.ctx = ctx->max_ctx;
         RCK(timed(ctx, RH_K_GEMV_QKV, [&] { return rh::launch_gemv(rh::GV_QKV, g, st); }));
         RCK(timed(ctx, RH_K_DECODE_ATTN, [&] {
-            return rh::launch_attn_decode(ctx->dq, kc, vc, ctx->dstate, ctx->pm, ctx->pl, ctx->po,
-                                          ctx->dattn, B, c.heads, c.head_dim, ctx->max_ctx, st);
+            return rh::launch_attn_decode(b.dq, kc, vc, b.state, b.pm, b.pl, b.po, b.dattn, B, c.heads,
+                                          c.head_dim, ctx->max_ctx, st);
         }));
         g = rh::GemvArgs{};
-        g.W = W.wo; g.X = ctx->dattn; g.B = B; g.N = D; g.K = D;
-        g.out_f32 = ctx->dx; g.ldo = D; g.alpha = alpha;
+        g.W = W.wo; g.X = b.dattn; g.B = B; g.N = D; g.K = D;
+        g.out_f32 = b.dx; g.ldo = D; g.alpha = alpha;
         RCK(timed(ctx, RH_K_GEMV_WO, [&] { return rh::launch_gemv(rh::GV_RESID, g, st); }));
         g = rh::GemvArgs{};
         RCK(normed(g, W.g2));
         g.W = W.w13; g.B = B; g.N = 2 * F; g.K = D;
-        g.out_f16 = ctx->dgate; g.ldo = F;
+        g.out_f16 = b.dgate; g.ldo = F;
         RCK(timed(ctx, RH_K_GEMV_W13, [&] { return rh::launch_gemv(rh::GV_SWIGLU, g, st); }));
         g = rh::GemvArgs{};
-        g.W = W.w2; g.X = ctx->dgate; g.B = B; g.N = D; g.K = F;
-        g.out_f32 = ctx->dx; g.ldo = D; g.alpha = alpha;
+        g.W = W.w2; g.X = b.dgate; g.B = B; g.N = D; g.K = F;
+        g.out_f32 = b.dx; g.ldo = D; g.alpha = alpha;
         RCK(timed(ctx, RH_K_GEMV_W2, [&] { return rh::launch_gemv(rh::GV_RESID, g, st); }));
     }
     rh::GemvArgs g{};
     RCK(normed(g, ctx->gfinal));
     g.W = ctx->embed; g.B = B; g.N = c.vocab; g.K = D;
-    g.out_f32 = ctx->dlogits; g.ldo = c.vocab; g.softcap = c.softcap;
-    g.am_val = ctx->dam_v; g.am_idx = ctx->dam_i;
+    g.out_f32 = b.dlogits; g.ldo = c.vocab; g.softcap = c.softcap;
+    g.am_val = b.am_v; g.am_idx = b.am_i;
     RCK(timed(ctx, RH_K_GEMV_LOGITS, [&] { return rh::launch_gemv(rh::GV_F32, g, st); }));
-    LCK(rh::launch_argmax_final(ctx->dam_v, ctx->dam_i, rh::gemv_argmax_blocks(c.vocab), B, ctx->dout,
-                                ctx->dtok, ctx->dseq, ctx->dstate, true, st));
+    LCK(rh::launch_argmax_final(b.am_v, b.am_i, rh::gemv_argmax_blocks(c.vocab), B, b.tok_out, b.next_in, b.seq,
+                                b.state, true, st));
     return RH_OK;
 }
 
+rhrt::DecodeBufs rhrt::ctx_decode_bufs(rh_ctx* ctx) {
+    DecodeBufs b{};
+    b.dx = ctx->dx; b.dxn = ctx->dxn; b.dq = ctx->dq; b.dattn = ctx->dattn; b.dgate = ctx->dgate;
+    b.dlogits = ctx->dlogits; b.pm = ctx->pm; b.pl = ctx->pl; b.po = ctx->po;
+    b.am_v = ctx->dam_v; b.am_i = ctx->dam_i; b.state = ctx->dstate;
+    b.tok_in = ctx->dtok; b.tok_out = ctx->dout; b.next_in = ctx->dtok; b.seq = ctx->dseq;
+    return b;
+}
+
+namespace {
+
 int run_decode_step(rh_ctx* ctx, int B) {
-    if (!ctx->use_graphs) return enqueue_decode_step(ctx, B);
+    const DecodeBufs bufs = ctx_decode_bufs(ctx);
+    if (!ctx->use_graphs) return enqueue_decode_step(ctx, B, bufs);
     if (!ctx->dgraph || ctx->dgraph_B != B) {
         if (ctx->dgraph) {
             HCK(hipGraphExecDestroy(ctx->dgraph));
@@ -254,9 +264,9 @@ int run_decode_step(rh_ctx* ctx, int B) {
         }
         hipGraph_t graph = nullptr;
         HCK(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-        ctx->capturing = true;
-        const int rc = enqueue_decode_step(ctx, B);
-        ctx->capturing = false;
+        ctx->events_off = true;
+        const int rc = enqueue_decode_step(ctx, B, bufs);
+        ctx->events_off = false;
         const hipError_t ec = hipStreamEndCapture(ctx->stream, &graph);
         if (rc != RH_OK) {
             if (graph) (void)hipGraphDestroy(graph);
@@ -382,6 +392,8 @@ int rh_create(const rh_config* cfg, int device, int max_batch, int max_ctx, rh_c
     if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) return bail(RH_EDEVICE);
     if (hipSetDevice(device) != hipSuccess) return bail(RH_EDEVICE);
     if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) return bail(RH_EDEVICE);
+    int rc0 = noalloc_init(ctx);  // device address of rh_decode_step_noalloc's scratch
+    if (rc0) return bail(rc0);
 
     const size_t D = c.dim, F = c.hidden, V = c.vocab;
     int rc = RH_OK;

@@ -128,6 +128,7 @@ def lib():
     L.rh_prefill.argtypes = [ctxp, _u32p, ctypes.c_int, ctypes.c_int, _u32p, _f32p]
     L.rh_decode_step.argtypes = [ctxp, _u32p, _u32p, _f32p]
     L.rh_decode.argtypes = [ctxp, _u32p, ctypes.c_int, _u32p]
+    L.rh_decode_step_noalloc.argtypes = [ctxp, ctypes.c_int, _vp, _vp, _vp]
     L.rh_decode_pos.argtypes = [ctxp, ctypes.POINTER(ctypes.c_int)]
     L.rh_set_softcap.argtypes = [ctxp, ctypes.c_float]
     L.rh_sync.argtypes = [ctxp]
@@ -329,6 +330,11 @@ class Context:
         lg = np.empty((len(in_tok), self.cfg.vocab), np.float32) if want_logits else None
         self._ck(lib().rh_decode_step(self.h, _u(in_tok), _u(out), _f(lg)), "rh_decode_step")
         return out, lg
+
+    def decode_step_noalloc(self, batch: int, in_tok_ptr: int, out_tok_ptr: int, logits_ptr=None):
+        """rh_decode_step_noalloc: device pointers, enqueued without a sync."""
+        self._ck(lib().rh_decode_step_noalloc(self.h, batch, in_tok_ptr, out_tok_ptr, logits_ptr),
+                 "rh_decode_step_noalloc")
 
     def decode(self, in_tok, nsteps: int):
         in_tok = np.ascontiguousarray(in_tok, np.uint32).reshape(-1)
