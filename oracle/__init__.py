@@ -27,6 +27,7 @@ class OrcConfig(ctypes.Structure):
         ("dim", ctypes.c_int32), ("hidden", ctypes.c_int32), ("heads", ctypes.c_int32),
         ("head_dim", ctypes.c_int32), ("nlayers", ctypes.c_int32), ("vocab", ctypes.c_int32),
         ("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float), ("softcap", ctypes.c_float),
+        ("fp16_operands", ctypes.c_int32),
     ]
 
 
@@ -88,6 +89,11 @@ def lib():
                                   ctypes.c_void_p, _u32p, ctypes.c_int, _f32p]
         L.orc_decode_step.argtypes = [ctypes.POINTER(OrcConfig), ctypes.POINTER(OrcWeights),
                                       ctypes.c_void_p, ctypes.c_uint32, _f32p]
+        L.orc_prefill_batch.argtypes = [ctypes.POINTER(OrcConfig), ctypes.POINTER(OrcWeights),
+                                        ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, _u32p, ctypes.c_int, _f32p]
+        L.orc_decode_step_batch.argtypes = [ctypes.POINTER(OrcConfig), ctypes.POINTER(OrcWeights),
+                                            ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, _u32p, _f32p,
+                                            ctypes.POINTER(ctypes.c_int32)]
         L.orc_num_threads.restype = ctypes.c_int
         L.orc_forward_backward.argtypes = [ctypes.POINTER(OrcConfig), ctypes.POINTER(OrcWeights),
                                            _u32p, _u32p, ctypes.c_int, ctypes.c_int, ctypes.c_float,
@@ -123,10 +129,19 @@ def up(a: np.ndarray):
     return a.ctypes.data_as(_u32p)
 
 
+# fp16 rounding points of the oracle's fp16-operand mode (oracle.h ORC_F16_*)
+F16_POINTS = {"xn": 1, "q": 2, "k": 4, "v": 8, "p": 16, "attn": 32, "xn2": 64, "gate": 128, "xf": 256}
+F16_ALL = 511
+
+
 def make_config(dim, hidden, heads, nlayers, vocab, head_dim=None, rms_eps=1e-5,
-                rope_base=1e4, softcap=0.0) -> OrcConfig:
+                rope_base=1e4, softcap=0.0, fp16_operands=0) -> OrcConfig:
+    """fp16_operands: True (every point) or a set of F16_POINTS bits at which
+    the forward and decode round to fp16, where an fp16-operand device path
+    does; 0 = the reference's fp32 arithmetic."""
     hd = head_dim if head_dim is not None else dim // heads
-    return OrcConfig(dim, hidden, heads, hd, nlayers, vocab, rms_eps, rope_base, softcap)
+    bits = F16_ALL if fp16_operands is True else int(fp16_operands)
+    return OrcConfig(dim, hidden, heads, hd, nlayers, vocab, rms_eps, rope_base, softcap, bits)
 
 
 class Weights:
@@ -193,6 +208,45 @@ class KV:
                                      int(token), fp(out))
         if best < 0:
             raise ValueError(f"orc_decode_step failed: {best}")
+        return best, out
+
+
+class KVBatch:
+    """B sequences with their own caches, stepped together
+    (orc_prefill_batch / orc_decode_step_batch)."""
+
+    def __init__(self, cfg: OrcConfig, batch: int, max_ctx: int):
+        self.cfg = cfg
+        self.kvs = [KV(cfg, max_ctx) for _ in range(batch)]
+        self._h = (ctypes.c_void_p * batch)(*[kv.h for kv in self.kvs])
+
+    @property
+    def pos(self):
+        return [kv.pos for kv in self.kvs]
+
+    def prefill(self, w: Weights, tokens: np.ndarray) -> np.ndarray:
+        """tokens [B, len] -> last-position logits [B, V]."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        B, n = tokens.shape
+        assert B == len(self.kvs)
+        out = np.zeros((B, self.cfg.vocab), np.float32)
+        rc = lib().orc_prefill_batch(ctypes.byref(self.cfg), ctypes.byref(w.c), self._h, B, up(tokens), n,
+                                     fp(out))
+        if rc != 0:
+            raise ValueError(f"orc_prefill_batch failed: {rc}")
+        return out
+
+    def step(self, w: Weights, tokens) -> tuple[np.ndarray, np.ndarray]:
+        """tokens [B] -> (argmax [B], logits [B, V])."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+        B = tokens.size
+        assert B == len(self.kvs)
+        out = np.zeros((B, self.cfg.vocab), np.float32)
+        best = np.zeros(B, np.int32)
+        rc = lib().orc_decode_step_batch(ctypes.byref(self.cfg), ctypes.byref(w.c), self._h, B, up(tokens),
+                                         fp(out), best.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)))
+        if rc != 0:
+            raise ValueError(f"orc_decode_step_batch failed: {rc}")
         return best, out
 
 

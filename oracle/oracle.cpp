@@ -29,6 +29,7 @@
 #include <algorithm>
 #ifdef _OPENMP
 #include <omp.h>
+#include <immintrin.h>
 #endif
 
 namespace {
@@ -41,6 +42,17 @@ inline v8 bc8(float x) { return v8{x, x, x, x, x, x, x, x}; }
 inline float hsum8(v8 v) {
     return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
 }
+
+// Rounds p[0..n) through fp16 in place (round to nearest even, F16C): the
+// operand precision of an fp16 device path (orc_config.fp16_operands).
+void round_f16(float* p, size_t n) {
+    const size_t n8 = n & ~size_t(7);
+#pragma omp parallel for schedule(static) if (n > 65536)
+    for (size_t i = 0; i < n8; i += 8)
+        _mm256_storeu_ps(p + i, _mm256_cvtph_ps(_mm256_cvtps_ph(_mm256_loadu_ps(p + i), _MM_FROUND_TO_NEAREST_INT)));
+    for (size_t i = n8; i < n; ++i) p[i] = _cvtsh_ss(_cvtss_sh(p[i], _MM_FROUND_TO_NEAREST_INT));
+}
+inline float r16(float x) { return _cvtsh_ss(_cvtss_sh(x, _MM_FROUND_TO_NEAREST_INT)); }
 
 // C[M,N] += A[M,K] * B[K,N]   (all row-major with leading dims)
 void gemm_nn(size_t M, size_t N, size_t K, const float* A, size_t lda, const float* B,
@@ -173,12 +185,26 @@ struct LayerCache {
     std::vector<float> x, xn, rms1, q, k, v, attn, x2, x2n, rms2, h1, h3, gate;
 };
 
-// One layer over n token-major rows at absolute positions p0..p0+n-1.
-// kc/vc: [ctx, D] token-major caches; positions p0..p0+n-1 are written, and
-// attention runs over keys 0..p0+n-1 with the additive -65504 causal mask of
-// kernels/sdpa_fwd.rs:41-51 (masked keys contribute exp(-65504 - max) = 0).
-void layer_rows(const orc_config* cfg, const float* const* lw, float* x, size_t n, size_t p0,
-                float* kc, float* vc, LayerCache* cache = nullptr) {
+// Where one row's K/V go and which keys it attends to: row t is at absolute
+// position pos and appends its k, v to kc/vc ([ctx, D] token-major caches) at
+// pos; its attention runs over keys 0..pos of the same caches.
+struct RowSlot {
+    float* kc;
+    float* vc;
+    size_t pos;
+};
+
+// One layer over n token-major rows, row t described by slots[t].  Rows of
+// one sequence share its caches (the forward and prefill: positions
+// p0..p0+n-1); rows of different sequences each have their own (a batched
+// decode step).  Attention over keys 0..pos is the additive -65504 causal
+// mask of kernels/sdpa_fwd.rs:41-51 applied to keys 0..p0+n-1: a masked key
+// contributes exp(-65504 + s - max) = 0 exactly in fp32 and never holds the
+// max, so leaving it out changes no bit of the result.
+void layer_rows_slots(const orc_config* cfg, const float* const* lw, float* x, size_t n,
+                      const RowSlot* slots, LayerCache* cache = nullptr, bool multi_token = true) {
+    const int32_t m16 = cfg->fp16_operands;
+    const bool p16 = (m16 & ORC_F16_P) && multi_token;  // P.V on fp16 probabilities (prefill passes)
     const size_t D = cfg->dim, F = cfg->hidden, H = cfg->heads, hd = cfg->head_dim;
     const float alpha = 1.0f / std::sqrt(2.0f * (float)cfg->nlayers);   // layer.rs:4640
     const float scale = 1.0f / std::sqrt((float)hd);                    // sdpa_fwd.rs:70
@@ -189,6 +215,7 @@ void layer_rows(const orc_config* cfg, const float* const* lw, float* x, size_t 
     std::vector<float> xn(n * D), q(n * D, 0.f), k(n * D, 0.f), v(n * D, 0.f), rms1(n);
     if (cache) cache->x.assign(x, x + n * D);
     rmsnorm_rows(x, g1, xn.data(), rms1.data(), n, D, cfg->rms_eps);
+    if (m16 & ORC_F16_XN) round_f16(xn.data(), n * D);
     // Q/K/V = xn^T W  (sdpa_fwd.rs:115-117)
     gemm_nn(n, D, D, xn.data(), D, wq, D, q.data(), D);
     gemm_nn(n, D, D, xn.data(), D, wk, D, k.data(), D);
@@ -197,7 +224,7 @@ void layer_rows(const orc_config* cfg, const float* const* lw, float* x, size_t 
     // rot[2i] = -x[2i+1], rot[2i+1] = x[2i]; x' = x*cos + rot*sin.
 #pragma omp parallel for schedule(static)
     for (size_t t = 0; t < n; ++t) {
-        const size_t p = p0 + t;
+        const size_t p = slots[t].pos;
         for (size_t h = 0; h < H; ++h)
             for (size_t i = 0; i < hd / 2; ++i) {
                 const float th = rope_theta(p, i, hd, cfg->rope_base);
@@ -209,25 +236,32 @@ void layer_rows(const orc_config* cfg, const float* const* lw, float* x, size_t 
                 kr[0] = k0 * c + (-k1) * s; kr[1] = k1 * c + k0 * s;
             }
     }
-    std::memcpy(kc + p0 * D, k.data(), n * D * sizeof(float));
-    std::memcpy(vc + p0 * D, v.data(), n * D * sizeof(float));
-    const size_t nk = p0 + n;
+    if (m16 & ORC_F16_Q) round_f16(q.data(), n * D);
+    if (m16 & ORC_F16_K) round_f16(k.data(), n * D);
+    if (m16 & ORC_F16_V) round_f16(v.data(), n * D);
+    for (size_t t = 0; t < n; ++t) {
+        std::memcpy(slots[t].kc + slots[t].pos * D, &k[t * D], D * sizeof(float));
+        std::memcpy(slots[t].vc + slots[t].pos * D, &v[t * D], D * sizeof(float));
+    }
+    size_t nk_max = 0;
+    for (size_t t = 0; t < n; ++t) nk_max = std::max(nk_max, slots[t].pos + 1);
     std::vector<float> attn(n * D, 0.f);
 #pragma omp parallel
     {
-        std::vector<float> sc(nk);
+        std::vector<float> sc(nk_max);
 #pragma omp for collapse(2) schedule(dynamic)
         for (size_t h = 0; h < H; ++h)
             for (size_t t = 0; t < n; ++t) {
-                const size_t pt = p0 + t;
+                const size_t nk = slots[t].pos + 1;
+                const float* kc = slots[t].kc;
+                const float* vc = slots[t].vc;
                 const float* qr = &q[t * D + h * hd];
                 float mx = -INFINITY;
                 for (size_t t2 = 0; t2 < nk; ++t2) {
                     const float* kr = kc + t2 * D + h * hd;
                     float d = 0.f;
                     for (size_t i = 0; i < hd; ++i) d += qr[i] * kr[i];
-                    float s = d * scale;
-                    if (t2 > pt) s += -65504.0f;
+                    const float s = d * scale;
                     sc[t2] = s;
                     mx = std::max(mx, s);
                 }
@@ -235,6 +269,17 @@ void layer_rows(const orc_config* cfg, const float* const* lw, float* x, size_t 
                 for (size_t t2 = 0; t2 < nk; ++t2) { sc[t2] = std::exp(sc[t2] - mx); sum += sc[t2]; }
                 const float inv = 1.0f / sum;
                 float* o = &attn[t * D + h * hd];
+                if (p16) {
+                    // unnormalised fp16 probabilities into P.V, then / sum
+                    for (size_t t2 = 0; t2 < nk; ++t2) {
+                        const float p = r16(sc[t2]);
+                        if (p == 0.f) continue;
+                        const float* vr = vc + t2 * D + h * hd;
+                        for (size_t i = 0; i < hd; ++i) o[i] += p * vr[i];
+                    }
+                    for (size_t i = 0; i < hd; ++i) o[i] *= inv;
+                    continue;
+                }
                 for (size_t t2 = 0; t2 < nk; ++t2) {
                     const float p = sc[t2] * inv;
                     if (p == 0.f) continue;
@@ -243,6 +288,7 @@ void layer_rows(const orc_config* cfg, const float* const* lw, float* x, size_t 
                 }
             }
     }
+    if (m16 & ORC_F16_ATTN) round_f16(attn.data(), n * D);
     // o = attn^T Wo, x2 = o*alpha + x  (dyn_matmul.rs:15-75, vdsp::vsma)
     std::vector<float> o(n * D, 0.f);
     gemm_nn(n, D, D, attn.data(), D, wo, D, o.data(), D);
@@ -255,14 +301,25 @@ void layer_rows(const orc_config* cfg, const float* const* lw, float* x, size_t 
     // f = gate W2^T, x_next = f*alpha + x2.
     std::vector<float> x2n(n * D), h1(n * F, 0.f), h3(n * F, 0.f), rms2(n);
     rmsnorm_rows(x, g2, x2n.data(), rms2.data(), n, D, cfg->rms_eps);
+    if (m16 & ORC_F16_XN2) round_f16(x2n.data(), n * D);
     gemm_nn(n, F, D, x2n.data(), D, w1, F, h1.data(), F);
     gemm_nn(n, F, D, x2n.data(), D, w3, F, h3.data(), F);
     if (cache) { cache->x2n = x2n; cache->rms2 = rms2; cache->h1 = h1; cache->h3 = h3; }
     orc_silu_gate(h1.data(), h3.data(), h1.data(), n * F);
+    if (m16 & ORC_F16_GATE) round_f16(h1.data(), n * F);
     if (cache) cache->gate = h1;
     std::vector<float> f(n * D, 0.f);
     gemm_nt(n, D, F, h1.data(), F, w2, F, f.data(), D);
     for (size_t i = 0; i < n * D; ++i) x[i] = f[i] * alpha + x[i];
+}
+
+// One layer over n rows of one sequence at absolute positions p0..p0+n-1,
+// its K/V cache kc/vc.
+void layer_rows(const orc_config* cfg, const float* const* lw, float* x, size_t n, size_t p0,
+                float* kc, float* vc, LayerCache* cache = nullptr) {
+    std::vector<RowSlot> slots(n);
+    for (size_t t = 0; t < n; ++t) slots[t] = RowSlot{kc, vc, p0 + t};
+    layer_rows_slots(cfg, lw, x, n, slots.data(), cache, n > 1);
 }
 
 // Final RMSNorm -> tied logits (logits.fill(0); sgemm_at) -> softcap
@@ -272,6 +329,7 @@ void tail_logits(const orc_config* cfg, const orc_weights* w, const float* x, si
     const size_t D = cfg->dim, V = cfg->vocab;
     std::vector<float> xf(n * D);
     rmsnorm_rows(x, w->gamma_final, xf.data(), nullptr, n, D, cfg->rms_eps);
+    if (cfg->fp16_operands & ORC_F16_XF) round_f16(xf.data(), n * D);
     std::fill(logits, logits + n * V, 0.f);
     gemm_nt(n, V, D, xf.data(), D, w->embed, D, logits, V);
     if (cfg->softcap > 0.f) {
@@ -850,6 +908,60 @@ int orc_decode_step(const orc_config* cfg, const orc_weights* w, orc_kv* kv, uin
     int best = 0;
     for (int i = 1; i < cfg->vocab; ++i) if (out[i] > out[best]) best = i;
     return best;
+}
+
+
+// B independent sequences, each with its own cache, run through the layers
+// as one set of rows (the GEMMs see all of them at once; attention stays per
+// sequence): rows r = b*n + t of sequence b at position kvs[b]->pos + t.
+static int run_rows_batch(const orc_config* cfg, const orc_weights* w, orc_kv* const* kvs, int B,
+                          const uint32_t* tokens, int n, float* last_logits) {
+    const size_t D = cfg->dim, V = cfg->vocab;
+    for (int b = 0; b < B; ++b)
+        if (!kvs[b] || kvs[b]->pos + n > kvs[b]->max_ctx || kvs[b]->nlayers != cfg->nlayers) return -3;
+    const size_t rows = (size_t)B * n;
+    for (size_t i = 0; i < rows; ++i) if (tokens[i] >= V) return -2;
+    std::vector<float> x(rows * D);
+    orc_embedding_forward(w->embed, D, tokens, rows, x.data());
+    std::vector<RowSlot> slots(rows);
+    for (int l = 0; l < cfg->nlayers; ++l) {
+        for (int b = 0; b < B; ++b)
+            for (int t = 0; t < n; ++t)
+                slots[(size_t)b * n + t] = RowSlot{kvs[b]->k[l].data(), kvs[b]->v[l].data(),
+                                                   (size_t)(kvs[b]->pos + t)};
+        layer_rows_slots(cfg, w->layers + 9 * l, x.data(), rows, slots.data(), nullptr, n > 1);
+    }
+    for (int b = 0; b < B; ++b) kvs[b]->pos += n;
+    if (last_logits) {
+        std::vector<float> xl((size_t)B * D);
+        for (int b = 0; b < B; ++b)
+            std::memcpy(&xl[(size_t)b * D], &x[((size_t)b * n + n - 1) * D], D * sizeof(float));
+        tail_logits(cfg, w, xl.data(), B, last_logits);
+    }
+    return 0;
+}
+
+int orc_prefill_batch(const orc_config* cfg, const orc_weights* w, orc_kv* const* kvs, int B,
+                      const uint32_t* tokens, int len, float* last_logits) {
+    if (!cfg || !w || !kvs || !tokens || B <= 0 || len <= 0) return -1;
+    for (int b = 0; b < B; ++b)
+        if (kvs[b]) kvs[b]->pos = 0;
+    return run_rows_batch(cfg, w, kvs, B, tokens, len, last_logits);
+}
+
+int orc_decode_step_batch(const orc_config* cfg, const orc_weights* w, orc_kv* const* kvs, int B,
+                          const uint32_t* tokens, float* logits_out, int32_t* argmax_out) {
+    if (!cfg || !w || !kvs || !tokens || !logits_out || B <= 0) return -1;
+    const int rc = run_rows_batch(cfg, w, kvs, B, tokens, 1, logits_out);
+    if (rc) return rc;
+    if (argmax_out)
+        for (int b = 0; b < B; ++b) {
+            const float* r = logits_out + (size_t)b * cfg->vocab;
+            int best = 0;
+            for (int i = 1; i < cfg->vocab; ++i) if (r[i] > r[best]) best = i;
+            argmax_out[b] = best;
+        }
+    return 0;
 }
 
 }  // extern "C"

@@ -69,7 +69,24 @@ typedef struct {
     float rms_eps;   /* 1e-5, cpu/rmsnorm.rs:10 */
     float rope_base; /* 1e4,  kernels/sdpa_fwd.rs:29 */
     float softcap;   /* 0 = off, full_model.rs:75 */
+    /* 0: fp32 throughout (the reference's CPU arithmetic).  Otherwise a set
+     * of ORC_F16_* bits: the forward and decode round to fp16 (round to
+     * nearest even) at those points, which are where an fp16-operand device
+     * path must round (ORC_F16_ALL).  Used to separate kernel error from the
+     * fp16 operand precision at full depth; not used by the backward pass. */
+    int32_t fp16_operands;
 } orc_config;
+
+#define ORC_F16_XN 1     /* first RMSNorm output (QKV operand)                  */
+#define ORC_F16_Q 2      /* q after RoPE                                        */
+#define ORC_F16_K 4      /* k after RoPE (the K cache)                          */
+#define ORC_F16_V 8      /* v (the V cache)                                     */
+#define ORC_F16_P 16     /* unnormalised probabilities into P.V, multi-token passes only; row sums stay fp32 */
+#define ORC_F16_ATTN 32  /* attention output (Wo operand)                       */
+#define ORC_F16_XN2 64   /* second RMSNorm output (W1|W3 operand)               */
+#define ORC_F16_GATE 128 /* SwiGLU gate (W2 operand)                            */
+#define ORC_F16_XF 256   /* final RMSNorm output (logits operand)               */
+#define ORC_F16_ALL 511
 
 /* ModelWeights (full_model.rs:19-23) + LayerWeights (layer.rs:52-63), fp32 host
  * arrays in the reference orientation.  layers[9*l + j], j in RSTK order:
@@ -185,6 +202,15 @@ int orc_decode_step(const orc_config* cfg, const orc_weights* w, orc_kv* kv, uin
                     float* logits_out);
 
 /* Threads the oracle's OpenMP loops use. */
+/* B sequences with their own caches in one pass (the layers' GEMMs over all
+ * B*len rows at once, attention per sequence); same results as B separate
+ * orc_prefill / orc_decode_step calls up to fp32 summation order.
+ * tokens [B*len] (sequence-major); last_logits nullable [B, V];
+ * decode: tokens [B], logits_out [B, V], argmax_out nullable [B]. */
+int orc_prefill_batch(const orc_config* cfg, const orc_weights* w, orc_kv* const* kvs, int B,
+                      const uint32_t* tokens, int len, float* last_logits);
+int orc_decode_step_batch(const orc_config* cfg, const orc_weights* w, orc_kv* const* kvs, int B,
+                          const uint32_t* tokens, float* logits_out, int32_t* argmax_out);
 int orc_num_threads(void);
 
 #ifdef __cplusplus

@@ -1,17 +1,40 @@
-"""GPU parity at the benchmark model widths (600M, 5B, 7B).
+"""GPU parity at every benchmark configuration (600M, 5B, 7B; prefill B 1/4/16,
+decode B 1/16 from a 2048-token prompt) against the CPU oracle.
 
-Two kinds of check:
-  * oracle parity at the real widths, seq 512, vocab 32000, with the depth cut
-    to two layers (every per-layer kernel runs at its real GEMM/attention
-    shape; the oracle finishes in about a second);
-  * size-independent properties of the full-depth 7B forward and decode
-    (32 layers, weights generated on the device): determinism, causality
-    (a token changed at position p leaves every logit row before p bit for
-    bit unchanged), loss finite and near ln(V) for N(0, 0.02) weights, and
-    greedy decode agreeing with a teacher-forced prefill of its own output.
+Weights are N(0, 0.02) generated on the device and read back, so the oracle
+sees exactly the fp16 values the kernels use.
+
+Bars.  The reference's own bar for equivalent forwards
+(crates/engine/tests/test_combined_forward_correctness.rs:13-14) is logits
+max-abs <= 2e-2 and cosine >= 0.999, with the mean loss within 1e-3
+relative; the 7B-width tests (every per-layer kernel at its real shape, depth
+cut to 1-2 layers) meet it.  At full depth it is not a property fp16
+operands can have: rounding the GEMM and attention operands to fp16 (the
+path's data type) moves a 32-layer 7B forward's logits by up to ~3.6e-2 from
+the fp32 oracle however exact the kernels are.  So the full-depth tests also
+run the oracle with fp16 rounding at exactly those operands
+(fp16_operands, pinned point by point in test_oracle_kats.py) and require the
+GPU's deviation from the fp32 oracle to be no larger than 1.5x the
+fp16-rounded oracle's own deviation from it, in RMS and in max-abs -- a
+kernel with a wrong index or a dropped term deviates by orders of magnitude
+more -- plus cosine >= 0.9999 and the mean loss within 1e-4 relative
+(both tighter than the reference's bar).
+
+Decode follows the contract of crates/metal-decode/src/lib.rs:1-8: every
+step's logits within the bar of the oracle's, and the greedy id equal to the
+oracle's argmax except where the oracle's top-2 margin is below 4e-2 (a
+near-tie the fp16 error can flip); the oracle is teacher-forced on the GPU's
+ids, so one near-tie does not end the comparison, and the test prints how
+many steps were near-ties and their margins.
+
+  * full depth: the 600M (20 layers), 5B (60 layers) and 7B (32 layers)
+    forwards at seq 512; the 7B greedy decode from a 512-token prompt;
+  * 7B width: prefill at batch 4 and 16 (the GEMM tile choice depends on the
+    row count), decode at batch 1 (2 layers) and 16 (1 layer) from
+    2048-token prompts (the decode attention's 16-18 context chunks), 64
+    steps each; and the 600M / 5B widths;
+  * full-depth 7B properties: two forwards bit-identical, causality.
 """
-import math
-
 import numpy as np
 import pytest
 
@@ -22,54 +45,153 @@ from helpers import LOGIT_ATOL, LOSS_RTOL, cosine, oracle_cfg, tokens_uniform
 
 pytestmark = pytest.mark.gpu
 
+# oracle top-2 margin below which a greedy id may legitimately differ
+NEAR_TIE = 4e-2
+# full depth: GPU deviation <= this x the fp16-operand oracle's deviation
+FP16_FACTOR = 1.5
 
-def _width_cfg(name):
+
+def _cfg(name, nlayers=None):
     cfg = {"600m": cfg_600m, "5b": cfg_5b_deep, "7b": cfg_7b}[name]()
-    cfg.nlayers = 2
+    if nlayers is not None:
+        cfg.nlayers = nlayers
     return cfg
 
 
-@pytest.mark.parametrize("name,batch", [("600m", 2), ("5b", 1), ("7b", 1)])
-def test_width_matches_oracle(orc, name, batch):
-    """Weights N(0, 0.02) generated on the device and read back, so the
-    oracle sees exactly the fp16 values the kernels use."""
-    cfg = _width_cfg(name)
-    tok, tgt = tokens_uniform(62, cfg.vocab, batch, cfg.seq)
-    print(f"[case] {name} width dim={cfg.dim} F={cfg.hidden} L={cfg.nlayers} B={batch} "
-          f"S={cfg.seq}", flush=True)
-    with hb.Context(cfg.to_rh(), 0, batch, 0) as c:
-        c.init_normal(seed=61, std=0.02)
-        out = c.forward(tok, tgt)
-        embed, gf, layers = c.read_weights()
-    lg, tl, ml = orc.forward(oracle_cfg(orc, cfg), orc.Weights(embed, gf, layers), tok, tgt)
+def _oc16(orc, cfg):
+    return orc.make_config(cfg.dim, cfg.hidden, cfg.heads, cfg.nlayers, cfg.vocab, head_dim=cfg.hd,
+                           fp16_operands=True)
+
+
+def _device_weights(orc, c):
+    embed, gf, layers = c.read_weights()
+    return orc.Weights(embed, gf, layers)
+
+
+def _rms(a):
+    return float(np.sqrt(np.mean(np.square(a, dtype=np.float64))))
+
+
+def _check_forward(tag, out, lg, ml):
+    """The reference's bar (depth-cut runs)."""
     err = float(np.abs(out.logits - lg).max())
-    print(f"[result] {name}: max|dlogit|={err:.3e} loss gpu={out.mean_loss} cpu={ml}", flush=True)
+    cs = cosine(out.logits, lg)
+    print(f"[result] {tag}: max|dlogit|={err:.3e} cos={cs:.6f} loss gpu={out.mean_loss} cpu={ml}", flush=True)
     assert err <= LOGIT_ATOL
-    assert cosine(out.logits, lg) >= 0.999
+    assert cs >= 0.999
     np.testing.assert_allclose(out.mean_loss, ml, rtol=LOSS_RTOL)
 
 
+def _check_fp16_bar(tag, got, lg32, lg16):
+    """GPU deviation from the fp32 oracle vs the fp16-operand oracle's."""
+    dev, ref = got - lg32, lg16 - lg32
+    g_rms, f_rms = _rms(dev), _rms(ref)
+    g_max, f_max = float(np.abs(dev).max()), float(np.abs(ref).max())
+    print(f"[result] {tag}: vs fp32 oracle rms {g_rms:.3e} max {g_max:.3e}; fp16-operand oracle vs fp32 "
+          f"rms {f_rms:.3e} max {f_max:.3e}; GPU vs fp16-operand oracle max {np.abs(got - lg16).max():.3e}",
+          flush=True)
+    assert g_rms <= FP16_FACTOR * f_rms
+    assert g_max <= FP16_FACTOR * f_max
+
+
+def _check_full_depth(tag, out, lg32, ml32, lg16):
+    _check_fp16_bar(tag, out.logits, lg32, lg16)
+    cs = cosine(out.logits, lg32)
+    print(f"[result] {tag}: cos={cs:.7f} loss gpu={out.mean_loss} cpu={ml32}", flush=True)
+    assert cs >= 0.9999
+    np.testing.assert_allclose(out.mean_loss, ml32, rtol=1e-4)
+
+
+def _check_decode(tag, c, orc, oc, ow, prompts, nsteps, oc16=None):
+    """Prefill + nsteps greedy steps on the GPU; the oracle runs the same
+    prompts and is fed the GPU's ids (so is the fp16-operand oracle, when
+    given, which sets the logit bar; otherwise the bar is 2e-2).  Returns the
+    near-tie flips."""
+    B, P = prompts.shape
+    nxt, glog = c.prefill(prompts, want_logits=True)
+    kb = orc.KVBatch(oc, B, P + nsteps + 1)
+    olog = kb.prefill(ow, prompts)
+    kb16 = orc.KVBatch(oc16, B, P + nsteps + 1) if oc16 is not None else None
+    o16 = kb16.prefill(ow, prompts) if kb16 else None
+    got, want, want16, ties = [], [], [], []
+    tok = nxt
+    for step in range(nsteps + 1):
+        if step > 0:
+            tok, glog = c.decode_step(prev, want_logits=True)
+            _, olog = kb.step(ow, prev)
+            if kb16:
+                _, o16 = kb16.step(ow, prev)
+        got.append(glog)
+        want.append(olog)
+        if kb16:
+            want16.append(o16)
+        for b in range(B):
+            top2 = np.sort(olog[b])[-2:]
+            margin = float(top2[1] - top2[0])
+            if int(tok[b]) != int(np.argmax(olog[b])):
+                ties.append((step, b, margin))
+                assert margin < NEAR_TIE, (tag, step, b, margin)
+                assert olog[b, tok[b]] >= top2[0] - 1e-6, (tag, step, b)  # the GPU chose the oracle's top two
+        prev = tok
+    got, want = np.stack(got), np.stack(want)
+    worst = float(np.abs(got - want).max())
+    print(f"[result] {tag}: {B} x {nsteps + 1} greedy ids, worst max|dlogit| {worst:.3e}, "
+          f"{len(ties)} near-tie flips (oracle margins {[round(t[2], 5) for t in ties]})", flush=True)
+    if kb16:
+        _check_fp16_bar(tag, got, want, np.stack(want16))
+    else:
+        assert worst <= LOGIT_ATOL
+    return ties
+
+
+# ---------------------------------------------------------------- full depth
+@pytest.mark.parametrize("name", ["600m", "5b"])
+def test_full_depth_forward_matches_oracle(orc, name):
+    cfg = _cfg(name)
+    tok, tgt = tokens_uniform(62, cfg.vocab, 1, cfg.seq)
+    print(f"[case] {name} full depth dim={cfg.dim} F={cfg.hidden} L={cfg.nlayers} S={cfg.seq}", flush=True)
+    with hb.Context(cfg.to_rh(), 0, 1, 0) as c:
+        c.init_normal(seed=61, std=0.02)
+        out = c.forward(tok, tgt)
+        ow = _device_weights(orc, c)
+    lg, _, ml = orc.forward(oracle_cfg(orc, cfg), ow, tok, tgt)
+    lg16, _, _ = orc.forward(_oc16(orc, cfg), ow, tok, tgt)
+    _check_full_depth(f"{name} full depth", out, lg, ml, lg16)
+
+
 @pytest.fixture(scope="module")
-def ctx7b():
-    cfg = cfg_7b()
+def full7b(orc):
+    cfg = _cfg("7b")
     print("[case] 7b full depth, device-initialised weights", flush=True)
-    c = hb.Context(cfg.to_rh(), 0, 2, 1024)
+    c = hb.Context(cfg.to_rh(), 0, 1, 600)
     c.init_normal(seed=71, std=0.02)
-    yield cfg, c
+    ow = _device_weights(orc, c)
+    yield cfg, c, ow, oracle_cfg(orc, cfg)
     c.close()
 
 
-def test_7b_full_depth_deterministic_and_causal(ctx7b):
-    cfg, c = ctx7b
+def test_7b_full_depth_forward_matches_oracle(orc, full7b):
+    cfg, c, ow, oc = full7b
     tok, tgt = tokens_uniform(72, cfg.vocab, 1, cfg.seq)
+    out = c.forward(tok, tgt)
+    lg, _, ml = orc.forward(oc, ow, tok, tgt)
+    lg16, _, _ = orc.forward(_oc16(orc, cfg), ow, tok, tgt)
+    _check_full_depth("7b full depth", out, lg, ml, lg16)
+
+
+def test_7b_full_depth_decode_matches_oracle(orc, full7b):
+    cfg, c, ow, oc = full7b
+    prompt, _ = tokens_uniform(74, cfg.vocab, 1, 512)
+    _check_decode("7b full depth decode B1 ctx 512", c, orc, oc, ow, prompt, 32, oc16=_oc16(orc, cfg))
+
+
+def test_7b_full_depth_deterministic_and_causal(full7b):
+    cfg, c, _, _ = full7b
+    tok, tgt = tokens_uniform(73, cfg.vocab, 1, cfg.seq)
     a = c.forward(tok, tgt)
     b = c.forward(tok, tgt)
     np.testing.assert_array_equal(a.logits, b.logits)
     np.testing.assert_array_equal(a.token_losses, b.token_losses)
-    assert np.isfinite(a.logits).all()
-    lnv = math.log(cfg.vocab)
-    print(f"[result] 7b loss {a.mean_loss[0]:.4f} (ln V = {lnv:.4f})", flush=True)
-    assert abs(a.mean_loss[0] - lnv) < 2.0
     p = 300
     tok2 = tok.copy()
     tok2[0, p] = (tok2[0, p] + 1) % cfg.vocab
@@ -78,36 +200,27 @@ def test_7b_full_depth_deterministic_and_causal(ctx7b):
     assert np.abs(d.logits[0, p] - a.logits[0, p]).max() > 1e-3
 
 
-def test_7b_full_depth_batch_rows_independent(ctx7b):
-    """Two sequences in one batch give each one's batch-1 logits (the GEMM
-    tiling depends on the row count, so equality is to the fp16 bar)."""
-    cfg, c = ctx7b
-    tok, tgt = tokens_uniform(73, cfg.vocab, 2, cfg.seq)
-    both = c.forward(tok, tgt)
-    for i in range(2):
-        one = c.forward(tok[i:i + 1], tgt[i:i + 1])
-        err = float(np.abs(both.logits[i] - one.logits[0]).max())
-        print(f"[result] 7b batch row {i}: max|dlogit| vs batch 1 = {err:.3e}", flush=True)
-        assert err <= LOGIT_ATOL
-        np.testing.assert_allclose(both.mean_loss[i], one.mean_loss[0], rtol=LOSS_RTOL)
+# ---------------------------------------------------------------- 7B width
+@pytest.mark.parametrize("name,batch", [("600m", 2), ("5b", 1), ("7b", 4), ("7b", 16)])
+def test_width_batches_match_oracle(orc, name, batch):
+    cfg = _cfg(name, nlayers=2)
+    tok, tgt = tokens_uniform(63 + batch, cfg.vocab, batch, cfg.seq)
+    print(f"[case] {name} width L=2 B={batch} S={cfg.seq}", flush=True)
+    with hb.Context(cfg.to_rh(), 0, batch, 0) as c:
+        c.init_normal(seed=64, std=0.02)
+        out = c.forward(tok, tgt)
+        ow = _device_weights(orc, c)
+    lg, _, ml = orc.forward(oracle_cfg(orc, cfg), ow, tok, tgt)
+    _check_forward(f"{name} width B{batch}", out, lg, ml)
 
 
-def test_7b_full_depth_decode_matches_teacher_forced_prefill(ctx7b):
-    """Greedy decode from a 700-token prompt, 64 steps; a prefill forward of
-    prompt + generated tokens then has, at each generated position, the
-    decoded token as its argmax (or within the fp16 bar of it)."""
-    cfg, c = ctx7b
-    P, n = 700, 64
-    prompt, _ = tokens_uniform(74, cfg.vocab, 1, P)
-    nxt, _ = c.prefill(prompt)
-    gen = [int(nxt[0])] + [int(t) for t in c.decode(nxt, n - 1)[:, 0]]
-    full = np.concatenate([prompt[0], np.array(gen[:-1], np.uint32)])[None, :]
-    out = c.forward(np.ascontiguousarray(full))
-    mism = 0
-    for i, g in enumerate(gen):
-        row = out.logits[0, P - 1 + i]
-        top = int(np.argmax(row))
-        if top != g:
-            mism += 1
-            assert row[top] - row[g] <= 2 * LOGIT_ATOL, (i, g, top, float(row[top] - row[g]))
-    print(f"[result] 7b decode: {n - mism} of {n} tokens are the prefill argmax", flush=True)
+@pytest.mark.parametrize("batch,nlayers", [(1, 2), (16, 1)])
+def test_7b_width_decode_ctx2048_matches_oracle(orc, batch, nlayers):
+    cfg = _cfg("7b", nlayers=nlayers)
+    P, n = 2048, 64
+    prompts, _ = tokens_uniform(80 + batch, cfg.vocab, batch, P)
+    print(f"[case] 7b width decode L={nlayers} B={batch} prompt {P}, {n} steps", flush=True)
+    with hb.Context(cfg.to_rh(), 0, batch, P + n + 8) as c:
+        c.init_normal(seed=81, std=0.02)
+        ow = _device_weights(orc, c)
+        _check_decode(f"7b width decode B{batch} ctx {P}", c, orc, oracle_cfg(orc, cfg), ow, prompts, n)

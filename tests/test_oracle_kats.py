@@ -316,9 +316,115 @@ def test_decode_cache_matches_forward(orc):
     assert kv.pos == cfg.seq
 
 
+def test_batched_decode_equals_separate_sequences(orc):
+    """orc_prefill_batch / orc_decode_step_batch over 3 sequences (prompts of
+    equal length, different tokens) against each sequence's own forward: the
+    last prefill position and every teacher-forced step equal the forward's
+    logits at that position, and a batch of 1 equals orc_decode_step."""
+    cfg = small_cfg(dim=128, hidden=256, heads=2, hd=64, nlayers=2, vocab=80, seq=20)
+    w = ModelWeights.normal(cfg, seed=34, std=0.08, fp16_round=False)
+    tok, tgt = tokens_uniform(35, cfg.vocab, 3, cfg.seq)
+    oc, ow = oracle_cfg(orc, cfg), oracle_weights(orc, w)
+    lg, _, _ = orc.forward(oc, ow, tok, tgt)
+    kb = orc.KVBatch(oc, 3, 32)
+    last = kb.prefill(ow, tok[:, :8])
+    np.testing.assert_allclose(last, lg[:, 7], rtol=1e-5, atol=1e-5)
+    for p in range(8, cfg.seq):
+        best, step = kb.step(ow, tok[:, p])
+        np.testing.assert_allclose(step, lg[:, p], rtol=1e-5, atol=1e-5)
+        np.testing.assert_array_equal(best, np.argmax(lg[:, p], axis=1))
+    assert kb.pos == [cfg.seq] * 3
+    # batch of 1 == the single-sequence path, bit for bit
+    k1, kb1 = orc.KV(oc, 32), orc.KVBatch(oc, 1, 32)
+    np.testing.assert_array_equal(k1.prefill(ow, tok[1, :8]), kb1.prefill(ow, tok[1:2, :8])[0])
+    b1, s1 = k1.step(ow, tok[1, 8])
+    bb, sb = kb1.step(ow, tok[1:2, 8])
+    np.testing.assert_array_equal(s1, sb[0])
+    assert b1 == bb[0]
+
+
 def test_oracle_rejects_bad_tokens(orc):
     cfg = small_cfg(dim=128, hidden=256, heads=2, hd=64, nlayers=1, vocab=64, seq=4)
     w = ModelWeights.normal(cfg, seed=33, fp16_round=False)
     tok = np.array([[1, 2, 64, 3]], np.uint32)
     with pytest.raises(ValueError):
         orc.forward(oracle_cfg(orc, cfg), oracle_weights(orc, w), tok, tok)
+
+
+ROUND_POINTS = ("xn", "q", "k", "v", "p", "attn", "xn2", "gate", "xf")
+
+
+def forward_fp16_operands_np(w, tok, H, L, points, p_rows):
+    """Float64 restatement of the forward with fp16 rounding (numpy's
+    round-to-nearest-even) at the named points; 'p' rounds the unnormalised
+    probabilities of the rows in p_rows (the row sums stay unrounded)."""
+    f16 = lambda a: a.astype(np.float16).astype(np.float64)
+    r = lambda name, a: f16(a) if name in points else a
+    rms = lambda y, g: y / np.sqrt((y ** 2).mean(-1, keepdims=True) + 1e-5) * g
+    x = w.embed[tok].astype(np.float64)
+    S, D = x.shape
+    hd = D // H
+    al = 1 / math.sqrt(2 * L)
+    mask = np.triu(np.full((S, S), -np.inf), 1)
+    for lw in w.layers:
+        wq, wk, wv, wo, w1, w3, w2, g1, g2 = [np.asarray(t, np.float64) for t in lw.tensors()]
+        xn = r("xn", rms(x, g1))
+        q = r("q", rope_complex((xn @ wq).reshape(S, H, hd)))
+        k = r("k", rope_complex((xn @ wk).reshape(S, H, hd)))
+        v = r("v", (xn @ wv).reshape(S, H, hd))
+        o = np.empty((S, H, hd))
+        for h in range(H):
+            s = q[:, h] @ k[:, h].T / math.sqrt(hd) + mask
+            p = np.exp(s - s.max(-1, keepdims=True))
+            l = p.sum(-1, keepdims=True)
+            if "p" in points:
+                p[p_rows] = f16(p[p_rows])
+            o[:, h] = p @ v[:, h] / l
+        x = x + al * (r("attn", o.reshape(S, D)) @ wo)
+        xn2 = r("xn2", rms(x, g2))
+        h1 = xn2 @ w1
+        x = x + al * (r("gate", h1 / (1 + np.exp(-h1)) * (xn2 @ w3)) @ w2.T)
+    return r("xf", rms(x, w.gamma_final.astype(np.float64))) @ w.embed.T.astype(np.float64)
+
+
+def test_fp16_operand_mode_matches_rounding_restatement(orc):
+    """Each rounding point of the oracle's fp16-operand mode, alone, against
+    the float64 restatement rounding at the same point: their difference is
+    a small fraction of that point's own effect on the logits (RMS ratio
+    <= 0.25; rounding at another place, e.g. q before RoPE or the gate before
+    the SiLU product, gives a ratio near 1).  Rounded chains cannot agree bit
+    for bit -- the two compute each pre-rounding value in a different order,
+    and every later rounding turns that tiny difference into an ulp -- so the
+    points are checked one at a time.  Decode steps keep P in fp32: with only
+    the probability point set, a step equals the fp32 oracle's step."""
+    cfg = small_cfg(dim=128, hidden=256, heads=2, hd=64, nlayers=2, vocab=96, seq=40)
+    w = ModelWeights.normal(cfg, seed=37, std=0.08)
+    tok, tgt = tokens_uniform(38, cfg.vocab, 1, cfg.seq)
+    ow = oracle_weights(orc, w)
+    S = cfg.seq
+    rms = lambda a: float(np.sqrt((np.asarray(a, np.float64) ** 2).mean()))
+    lg32, _, _ = orc.forward(oracle_cfg(orc, cfg), ow, tok, tgt)
+    ref32 = forward_fp16_operands_np(w, tok[0], cfg.heads, cfg.nlayers, [], np.arange(S))
+    assert np.abs(lg32[0] - ref32).max() < 1e-4
+
+    def cfg16(bits):
+        return orc.make_config(cfg.dim, cfg.hidden, cfg.heads, cfg.nlayers, cfg.vocab, head_dim=cfg.hd,
+                               fp16_operands=bits)
+
+    for pt in ROUND_POINTS:
+        lg, _, _ = orc.forward(cfg16(orc.F16_POINTS[pt]), ow, tok, tgt)
+        ref = forward_fp16_operands_np(w, tok[0], cfg.heads, cfg.nlayers, [pt], np.arange(S))
+        effect, match = rms(lg[0] - lg32[0]), rms(lg[0] - ref)
+        assert effect > 5e-5, (pt, effect)
+        assert match <= 0.25 * effect, (pt, match, effect)
+    # all points: the effect is the sum of the parts (no point cancels another)
+    lg_all, _, _ = orc.forward(cfg16(True), ow, tok, tgt)
+    ref_all = forward_fp16_operands_np(w, tok[0], cfg.heads, cfg.nlayers, ROUND_POINTS, np.arange(S))
+    assert rms(lg_all[0] - lg32[0]) == pytest.approx(rms(ref_all - ref32), rel=0.3)
+    # decode steps keep the probabilities in fp32: from a one-token prefill
+    # (P = 1 exactly, nothing to round) every step equals the fp32 oracle's
+    kvp, kv32 = orc.KV(cfg16(orc.F16_POINTS["p"]), S + 1), orc.KV(oracle_cfg(orc, cfg), S + 1)
+    kvp.prefill(ow, tok[0, :1])
+    kv32.prefill(ow, tok[0, :1])
+    for t in tok[0, 1:12]:
+        np.testing.assert_array_equal(kvp.step(ow, int(t))[1], kv32.step(ow, int(t))[1])
