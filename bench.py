@@ -75,6 +75,9 @@ def main():
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode with eager launches instead of graph replay (profilers that "
                          "cannot follow graph capture)")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="eager launches everywhere, prefill included (profilers that cannot follow "
+                         "graph capture)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
@@ -99,6 +102,9 @@ def main():
     t0 = time.time()
     ctx = hb.Context(cfg.to_rh(), 0, max_batch, max_ctx)
     ctx.init_normal(seed=1234, std=0.02)
+    if args.no_graphs:
+        args.decode_eager = True
+        ctx.set_graphs(False)
     log(f"[bench] context + weights ready in {time.time() - t0:.1f}s")
 
     stream = ctx.stream
@@ -109,27 +115,35 @@ def main():
         tok = hip_rt.DeviceArray.from_numpy(toks[:, :-1])
         tgt = hip_rt.DeviceArray.from_numpy(toks[:, 1:])
         mean = hip_rt.DeviceArray((B,), np.float32)
-        for _ in range(warmup):
+        for _ in range(warmup):  # the first call captures the forward's graph
             ctx.forward_dev(tok.ptr, tgt.ptr, B, cfg.seq, None, None, mean.ptr)
         ctx.sync()
-        if profile:
-            ctx.profile_enable(hb.K_GEMM_W13, True)
-        ev0, ev1 = hip_rt.Event(), hip_rt.Event()
-        hip_rt.synchronize()
-        ev0.record(stream)
-        t = time.perf_counter()
-        for _ in range(steps):
-            ctx.forward_dev(tok.ptr, tgt.ptr, B, cfg.seq, None, None, mean.ptr)
-        ev1.record(stream)
-        ctx.sync()
-        hip_rt.synchronize()
-        wall = time.perf_counter() - t
-        ms = ev0.elapsed_ms(ev1)
-        k_ms, k_n = ctx.profile_read(hb.K_GEMM_W13) if profile else (0.0, 0)
-        if profile:
-            ctx.profile_enable(hb.K_GEMM_W13, False)
+
+        def timed_steps():
+            ev0, ev1 = hip_rt.Event(), hip_rt.Event()
+            hip_rt.synchronize()
+            ev0.record(stream)
+            t = time.perf_counter()
+            for _ in range(steps):
+                ctx.forward_dev(tok.ptr, tgt.ptr, B, cfg.seq, None, None, mean.ptr)
+            ev1.record(stream)
+            ctx.sync()
+            hip_rt.synchronize()
+            return ev0.elapsed_ms(ev1), time.perf_counter() - t
+
+        # the timed region: one graph launch per step (eager with --no-graphs)
+        ms, wall = timed_steps()
         loss = mean.numpy()
-        return ms, wall, k_ms, k_n, loss
+        k_ms, k_n, eager_ms = 0.0, 0, None
+        if profile:
+            # The W1|W3 GEMM's own duration: the same steps launched eagerly
+            # with a HIP event pair attached to each of its dispatches (a
+            # graph replays the same kernels with the same arguments).
+            ctx.profile_enable(hb.K_GEMM_W13, True)
+            eager_ms, _ = timed_steps()
+            k_ms, k_n = ctx.profile_read(hb.K_GEMM_W13)
+            ctx.profile_enable(hb.K_GEMM_W13, False)
+        return ms, wall, k_ms, k_n, loss, eager_ms
 
     if args.decode_only:
         print(json.dumps({"decode": run_decode(ctx, cfg, args, hb, E, hip_rt, stream)}), flush=True)
@@ -151,7 +165,7 @@ def main():
         log(f"[bench] copy calibration: 3 x {nb} bytes device-to-device")
 
     B = args.batch
-    ms, wall, k_ms, k_n, loss = run_prefill(B, args.steps, args.warmup)
+    ms, wall, k_ms, k_n, loss, eager_ms = run_prefill(B, args.steps, args.warmup)
     ms_step = ms / args.steps
     tok_s = B * cfg.seq * args.steps / (ms / 1e3)
     fl = E.prefill_flops(cfg, cfg.seq, B)
@@ -159,12 +173,13 @@ def main():
     w13_avg_s = (k_ms / k_n) / 1e3 if k_n else float("nan")
     w13_tflops = w13_launch_flops / w13_avg_s / 1e12
     fwd_tflops = fl["total"] / (ms_step / 1e3) / 1e12
-    log(f"[bench] prefill B={B}: {ms_step:.3f} ms/step, {tok_s:.0f} tok/s, loss {loss}, "
+    log(f"[bench] prefill B={B}: {ms_step:.3f} ms/step ({'eager' if args.no_graphs else 'graph'}; "
+        f"eager {eager_ms / args.steps if eager_ms else float('nan'):.3f}), {tok_s:.0f} tok/s, loss {loss}, "
         f"W13 GEMM {w13_avg_s * 1e6:.1f} us ({w13_tflops:.0f} TFLOP/s), forward {fwd_tflops:.0f} TFLOP/s")
 
     extra_lines = {}
     for eb in extra:
-        e_ms, _, ek_ms, ek_n, _ = run_prefill(eb, max(3, args.steps // max(1, eb // 2)), 1)
+        e_ms, _, ek_ms, ek_n, _, _ = run_prefill(eb, max(3, args.steps // max(1, eb // 2)), 1)
         esteps = max(3, args.steps // max(1, eb // 2))
         efl = E.prefill_flops(cfg, cfg.seq, eb)
         extra_lines[f"B{eb}"] = {
@@ -221,12 +236,17 @@ def main():
                      "frac": round(w13_tflops / PEAK_FP16_TFLOPS, 4),
                      "traffic": measured_traffic(args.config, B, cfg.seq),
                      "flops_per_launch": w13_launch_flops,
-                     "mean_launch_us": round(w13_avg_s * 1e6, 2), "launches": k_n},
+                     "mean_launch_us": round(w13_avg_s * 1e6, 2), "launches": k_n,
+                     "timing": "HIP event pair attached to each W1|W3 GEMM dispatch, over the same steps "
+                               "launched eagerly right after the timed region",
+                     "traffic_source": "rocprofv3 FETCH_SIZE/WRITE_SIZE passes recorded in profiles/"},
         "forward_mfma": {"achieved_tflops": round(fwd_tflops, 1),
                          "frac": round(fwd_tflops / PEAK_FP16_TFLOPS, 4),
                          "flops_per_step": fl["total"]},
         "loss": float(loss[0]),
         "wall_s_timed": round(wall, 3),
+        "launch": "eager" if args.no_graphs else "hip graph per forward",
+        "eager_ms_per_step": round(eager_ms / args.steps, 4) if eager_ms else None,
     }
     if extra_lines:
         line["prefill_batches"] = extra_lines
@@ -365,6 +385,7 @@ def other_config_prefill(name, args, hb, E, hip_rt, steps=10, warmup=2):
     cfg.seq = 512
     with hb.Context(cfg.to_rh(), 0, 1, 0) as c:
         c.init_normal(seed=4321, std=0.02)
+        c.set_graphs(not args.no_graphs)
         rng = np.random.default_rng(11)
         toks = rng.integers(0, cfg.vocab, size=(1, cfg.seq + 1)).astype(np.uint32)
         tok = hip_rt.DeviceArray.from_numpy(toks[:, :-1])
@@ -451,12 +472,60 @@ def run_decode(ctx, cfg, args, hb, E, hip_rt, stream, batch=None):
     return out
 
 
+CPU_METHOD = "1 warm-up + 3 timed runs, median (tests/bench_fwd_only_scale.rs:117-131)"
+
+
+def median_time(fn, warmup=1, reps=3):
+    """The reference's probe methodology: warm-up runs, then the median of
+    the timed runs (tests/bench_fwd_only_scale.rs:117-131)."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return float(np.median(ts))
+
+
+def _oracle_layer_weights(rng, D, F):
+    def mat(*s):
+        return (rng.standard_normal(s, dtype=np.float32) * np.float32(0.02))
+
+    return [mat(D, D), mat(D, D), mat(D, D), mat(D, D), mat(D, F), mat(D, F), mat(D, F),
+            np.ones(D, np.float32), np.ones(D, np.float32)], mat
+
+
+def cpu_host_info(L):
+    return {"cores": int(L.orc_num_threads()), "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "nproc": os.cpu_count(), "method": CPU_METHOD}
+
+
+def cpu_full_forward(oracle, E, name):
+    """Full oracle forward + CE loss of a whole (small) model config, timed by
+    the reference's method: the tiny config of the reference's CPU path
+    (dim 512 / 8 layers / vocab 8192, seq 256) and the 600M shape at seq 512."""
+    cfg = {"tiny": E.tiny_config, "600m": E.cfg_600m}[name]()
+    D, F, V, S = cfg.dim, cfg.hidden, cfg.vocab, cfg.seq
+    rng = np.random.default_rng(9)
+    lw, mat = _oracle_layer_weights(rng, D, F)
+    ocfg = oracle.make_config(D, F, cfg.heads, cfg.nlayers, V, head_dim=cfg.hd)
+    w = oracle.Weights(mat(V, D), np.ones(D, np.float32), [lw] * cfg.nlayers)
+    tok = rng.integers(0, V, size=(1, S + 1)).astype(np.uint32)
+    a, b = np.ascontiguousarray(tok[:, :-1]), np.ascontiguousarray(tok[:, 1:])
+    t = median_time(lambda: oracle.forward(ocfg, w, a, b, want_logits=False))
+    return {"tok_s": round(S / t, 2), "ms_per_forward": round(t * 1e3, 2), "dim": D, "hidden": F,
+            "nlayers": cfg.nlayers, "vocab": V, "seq_len": S}
+
+
 def cpu_baseline(cfg, args):
-    """Oracle forward at the same shape over a bounded sample: 1 and 2 layers
-    (+ embedding, final norm, logits, CE) at seq 512, extrapolated linearly."""
-    import ctypes
+    """Oracle forward at the benchmark shape over a bounded sample: 1 and 2
+    layers (+ embedding, final norm, logits, CE) at seq 512, each timed by the
+    reference's method, extrapolated linearly in the layer count; plus full
+    forwards of the tiny and 600M configs."""
     try:
         import oracle
+        from rustane_amd import engine as E
     except Exception as e:  # pragma: no cover
         log(f"[bench] no oracle: {e}")
         return None
@@ -464,29 +533,24 @@ def cpu_baseline(cfg, args):
     L = oracle.lib()
     D, F, V, S = cfg.dim, cfg.hidden, cfg.vocab, cfg.seq
     rng = np.random.default_rng(5)
-
-    def mat(*s):
-        return (rng.standard_normal(s, dtype=np.float32) * np.float32(0.02))
-
-    lw = [mat(D, D), mat(D, D), mat(D, D), mat(D, D), mat(D, F), mat(D, F), mat(D, F),
-          np.ones(D, np.float32), np.ones(D, np.float32)]
+    lw, mat = _oracle_layer_weights(rng, D, F)
     embed = mat(V, D)
     tok = rng.integers(0, V, size=(1, S + 1)).astype(np.uint32)
+    a, b = np.ascontiguousarray(tok[:, :-1]), np.ascontiguousarray(tok[:, 1:])
     times = {}
     for nl in (1, 2):
         ocfg = oracle.make_config(D, F, cfg.heads, nl, V, head_dim=cfg.hd)
         w = oracle.Weights(embed, np.ones(D, np.float32), [lw] * nl)
-        t = time.perf_counter()
-        oracle.forward(ocfg, w, np.ascontiguousarray(tok[:, :-1]), np.ascontiguousarray(tok[:, 1:]),
-                       want_logits=False)
-        times[nl] = time.perf_counter() - t
+        times[nl] = median_time(lambda: oracle.forward(ocfg, w, a, b, want_logits=False))
     t_layer = max(times[2] - times[1], 1e-9)
     t_total = times[1] + (cfg.nlayers - 1) * t_layer
-    return {"value": round(S / t_total, 2), "unit": "tok/s", "cores": int(L.orc_num_threads()),
-            "kind": "port",
-            "sample": f"oracle fp32 forward at dim {D}/hidden {F}/vocab {V}/seq {S} with 1 and 2 layers "
-                      f"({times[1]:.2f}s, {times[2]:.2f}s), extrapolated linearly to {cfg.nlayers} layers "
-                      f"({t_total:.1f}s per forward)"}
+    out = {"value": round(S / t_total, 2), "unit": "tok/s", "kind": "port", **cpu_host_info(L),
+           "sample": f"oracle fp32 forward at dim {D}/hidden {F}/vocab {V}/seq {S} with 1 and 2 layers "
+                     f"(medians {times[1]:.3f}s, {times[2]:.3f}s), extrapolated linearly to {cfg.nlayers} "
+                     f"layers ({t_total:.2f}s per forward)"}
+    out["full_forward"] = {name: cpu_full_forward(oracle, E, name) for name in ("tiny", "600m")}
+    log(f"[bench] cpu baseline: {out}")
+    return out
 
 
 def cpu_baseline_train(cfg, args):
@@ -504,24 +568,21 @@ def cpu_baseline_train(cfg, args):
     def mat(*s):
         return (rng.standard_normal(s, dtype=np.float32) * np.float32(0.02))
 
-    lw = [mat(D, D), mat(D, D), mat(D, D), mat(D, D), mat(D, F), mat(D, F), mat(D, F),
-          np.ones(D, np.float32), np.ones(D, np.float32)]
+    lw, mat = _oracle_layer_weights(rng, D, F)
     embed = mat(V, D)
     tok = rng.integers(0, V, size=(1, S + 1)).astype(np.uint32)
+    a, b = np.ascontiguousarray(tok[:, :-1]), np.ascontiguousarray(tok[:, 1:])
     times = {}
     for nl in (1, 2):
         ocfg = oracle.make_config(D, F, cfg.heads, nl, V, head_dim=cfg.hd)
         w = oracle.Weights(embed, np.ones(D, np.float32), [lw] * nl)
-        t = time.perf_counter()
-        oracle.forward_backward(ocfg, w, np.ascontiguousarray(tok[:, :-1]), np.ascontiguousarray(tok[:, 1:]))
-        times[nl] = time.perf_counter() - t
+        times[nl] = median_time(lambda: oracle.forward_backward(ocfg, w, a, b))
     t_layer = max(times[2] - times[1], 1e-9)
     t_total = times[1] + (cfg.nlayers - 1) * t_layer
-    return {"value": round(S / t_total, 2), "unit": "tok/s", "cores": int(oracle.lib().orc_num_threads()),
-            "kind": "port",
+    return {"value": round(S / t_total, 2), "unit": "tok/s", "kind": "port", **cpu_host_info(oracle.lib()),
             "sample": f"oracle fp32 forward + backward at dim {D}/hidden {F}/vocab {V}/seq {S} with 1 and 2 "
-                      f"layers ({times[1]:.2f}s, {times[2]:.2f}s), extrapolated linearly to {cfg.nlayers} "
-                      f"layers ({t_total:.1f}s per step)"}
+                      f"layers (medians {times[1]:.2f}s, {times[2]:.2f}s), extrapolated linearly to "
+                      f"{cfg.nlayers} layers ({t_total:.1f}s per step)"}
 
 
 def cpu_baseline_decode(cfg, args, steps=4):
@@ -542,29 +603,26 @@ def cpu_baseline_decode(cfg, args, steps=4):
     def mat(*s):
         return (rng.standard_normal(s, dtype=np.float32) * np.float32(0.02))
 
-    lw = [mat(D, D), mat(D, D), mat(D, D), mat(D, D), mat(D, F), mat(D, F), mat(D, F),
-          np.ones(D, np.float32), np.ones(D, np.float32)]
+    lw, mat = _oracle_layer_weights(rng, D, F)
     embed = mat(V, D)
     prompt = rng.integers(0, V, size=ctx_len).astype(np.uint32)
     step_s = {}
     for nl in (1, 2):
         ocfg = oracle.make_config(D, F, cfg.heads, nl, V, head_dim=cfg.hd)
         w = oracle.Weights(embed, np.ones(D, np.float32), [lw] * nl)
-        kv = oracle.KV(ocfg, ctx_len + steps + 1)
+        kv = oracle.KV(ocfg, ctx_len + steps + 2)
         lg = kv.prefill(w, prompt)
-        tok = int(np.argmax(lg))
-        ts = []
-        for _ in range(steps):
-            t = time.perf_counter()
-            tok, _ = kv.step(w, tok)
-            ts.append(time.perf_counter() - t)
-        step_s[nl] = float(np.median(ts))
+        state = {"tok": int(np.argmax(lg))}
+
+        def one():
+            state["tok"], _ = kv.step(w, state["tok"])
+
+        step_s[nl] = median_time(one, warmup=1, reps=steps - 1)
     t_layer = max(step_s[2] - step_s[1], 1e-9)
     t_step = step_s[1] + (cfg.nlayers - 1) * t_layer
-    return {"value": round(1.0 / t_step, 3), "unit": "tok/s", "cores": int(L.orc_num_threads()),
-            "kind": "port", "batch": 1,
+    return {"value": round(1.0 / t_step, 3), "unit": "tok/s", "kind": "port", "batch": 1, **cpu_host_info(L),
             "sample": f"oracle fp32 KV-cached greedy step at dim {D}/hidden {F}/vocab {V}, ctx {ctx_len}, "
-                      f"1 and 2 layers (median of {steps} steps: {step_s[1] * 1e3:.1f} ms, "
+                      f"1 and 2 layers (1 warm-up step, median of {steps - 1}: {step_s[1] * 1e3:.1f} ms, "
                       f"{step_s[2] * 1e3:.1f} ms), extrapolated linearly to {cfg.nlayers} layers "
                       f"({t_step * 1e3:.0f} ms per token)"}
 

@@ -71,13 +71,20 @@ int rh_context_info(const rh_ctx* ctx, rh_config* cfg_out, int* max_batch_out, i
  * staging of layer.rs:4670-4705 (done once here).  layer_tensors holds
  * nlayers*9 pointers in RSTK order (bin/train.rs:238-345):
  *   wq[D,D] wk[D,D] wv[D,D] wo[D,D] w1[D,F] w3[D,F] w2[D,F] gamma1[D] gamma2[D]
- * (wq/wk/wv/wo/w1/w3 are in x out; w2 is out x in, used transposed). */
+ * (wq/wk/wv/wo/w1/w3 are in x out; w2 is out x in, used transposed).
+ * The fp32 matrices are also kept on the device as the optimizer's master
+ * weights (allocated by the first load, 4 bytes per parameter), so
+ * rh_read_weights_f32 returns them exactly and training resumes from them;
+ * any optimizer moments restart from zero (ModelOptState::zeros after
+ * load_checkpoint, bin/train.rs:444-449). */
 int rh_load_weights_f32(rh_ctx* ctx, const float* embed, const float* gamma_final,
                         const float* const* layer_tensors);
 
-/* Downloads the device weights back into the reference orientation
- * (fp16 widened to fp32); same argument layout as rh_load_weights_f32, but
- * writable.  Any pointer may be NULL to skip that tensor. */
+/* Downloads the weights in the reference orientation: the fp32 masters when
+ * they hold the current weights (after an fp32 load or an optimizer step),
+ * otherwise the fp16 device copy widened; same argument layout as
+ * rh_load_weights_f32, but writable.  Any pointer may be NULL to skip that
+ * tensor. */
 int rh_read_weights_f32(rh_ctx* ctx, float* embed, float* gamma_final,
                         float* const* layer_tensors);
 
@@ -130,11 +137,13 @@ int rh_read_grads_f32(rh_ctx* ctx, float* dembed, float* dgamma_final, float* co
 int rh_prefill(rh_ctx* ctx, const uint32_t* tokens, int batch, int len, uint32_t* next_tok_out,
                float* last_logits_out);
 
-/* One greedy decode step for the batch set by rh_prefill: embeds in_tok
- * [batch] at the current position, appends K/V, returns the argmax token
- * (ties -> lowest id) in out_tok [batch] and optionally logits [batch, vocab].
- * Contract: logits equal the forward's logits at that position. */
-int rh_decode_step(rh_ctx* ctx, const uint32_t* in_tok, uint32_t* out_tok, float* logits_out);
+/* One greedy decode step for the batch set by rh_prefill (batch must equal
+ * it, RH_EINVAL otherwise; the arrays hold exactly batch entries): embeds
+ * in_tok [batch] at the current position, appends K/V, returns the argmax
+ * token (ties -> lowest id) in out_tok [batch] and optionally logits
+ * [batch, vocab].  Contract: logits equal the forward's logits at that
+ * position. */
+int rh_decode_step(rh_ctx* ctx, int batch, const uint32_t* in_tok, uint32_t* out_tok, float* logits_out);
 
 /* rh_decode_step without any allocation: no counterpart in the reference.
  * For callers that cannot allocate device memory or runtime objects (code
@@ -153,8 +162,9 @@ int rh_decode_step_noalloc(rh_ctx* ctx, int batch, const uint32_t* in_tok, uint3
                            float* logits_out);
 
 /* nsteps greedy steps run entirely on the device (each step's argmax is the
- * next step's input); out_tokens [nsteps, batch].  Starts from in_tok. */
-int rh_decode(rh_ctx* ctx, const uint32_t* in_tok, int nsteps, uint32_t* out_tokens);
+ * next step's input); out_tokens [nsteps, batch].  Starts from in_tok
+ * [batch]; batch must equal the prefill batch. */
+int rh_decode(rh_ctx* ctx, int batch, const uint32_t* in_tok, int nsteps, uint32_t* out_tokens);
 
 /* Logit softcap c for later calls (c * tanh(z / c), 0 = off); the reference
  * passes it per forward call (full_model.rs:569-576). */
@@ -190,7 +200,10 @@ void* rh_stream(rh_ctx* ctx);
 int rh_profile_enable(rh_ctx* ctx, int kernel_class, int enable);
 int rh_profile_read(rh_ctx* ctx, int kernel_class, double* total_ms, int64_t* launches);
 
-/* Decode steps as a captured HIP graph (1, default) or eager launches (0). */
+/* Forward calls (one graph per batch, seq and loss/no-loss, built on first
+ * use) and decode steps as captured HIP graphs (1, default), or eager
+ * launches (0).  While a kernel class is being timed (rh_profile_enable)
+ * forwards launch eagerly. */
 int rh_set_graphs(rh_ctx* ctx, int enable);
 
 /* ---- on-disk formats either side of the forward ----------------------- */
@@ -262,11 +275,12 @@ int rh_grad_norm(rh_ctx* ctx, float* norm_out);
  * multiplied by grad_scale: the embedding at lr * embed_lr_scale and the
  * gammas at lr without weight decay, the seven matrices per layer at
  * lr * matrix_lr_scale with weight_decay.  The first call allocates the
- * optimizer state: fp32 master weights (read from the device weights),
- * first and second moments (zero).  Weights written by rh_load_weights_f32,
- * rh_init_weights_normal or a checkpoint load reset the masters; the
- * moments persist.  After an update rh_read_weights_f32 (and
- * rh_save_checkpoint) return the fp32 masters. */
+ * optimizer state: first and second moments (zero) and, unless an fp32
+ * load made them, the fp32 master weights (read from the fp16 device
+ * weights).  rh_load_weights_f32 and rh_load_checkpoint write the masters
+ * exactly, rh_init_weights_normal leaves them to be re-read from the fp16
+ * copy; every weight write restarts the moments from zero.  After an update
+ * rh_read_weights_f32 (and rh_save_checkpoint) return the fp32 masters. */
 int rh_update_weights(rh_ctx* ctx, uint32_t t, float lr, const rh_train_config* tc, float grad_scale);
 /* train_step / train_step_with_options (full_model.rs:1488-1600): zero the
  * gradients; accum_steps sequences of the context's seq from `data` at
@@ -275,8 +289,8 @@ int rh_update_weights(rh_ctx* ctx, uint32_t t, float lr, const rh_train_config* 
  * tc->loss_scale (up to max_batch sequences per launch); clip by the global
  * norm (combined scale = grad_clip / norm when norm / (accum_steps *
  * loss_scale) > grad_clip, else 1 / (accum_steps * loss_scale)); AdamW at
- * t = step + 1 with learning_rate(step).  Sets the softcap to tc->softcap
- * (as rh_set_softcap).  loss_out: mean loss of the microbatches;
+ * t = step + 1 with learning_rate(step).  The training forward uses
+ * tc->softcap; the context's own softcap is unchanged afterwards.  loss_out: mean loss of the microbatches;
  * grad_norm_out: the norm divided by accum_steps * loss_scale. */
 int rh_train_step(rh_ctx* ctx, const rh_tokens* data, uint32_t step, const rh_train_config* tc, float* loss_out,
                   float* grad_norm_out);

@@ -27,6 +27,13 @@ struct Prof {
     int64_t n = 0;
 };
 
+// A captured forward (body + logits/loss tail) for one (batch, seq, loss).
+struct FwdGraph {
+    int B = 0, S = 0;
+    bool loss = false;
+    hipGraphExec_t exec = nullptr;
+};
+
 struct TrainState;                 // rh_train.cpp
 void train_state_free(TrainState* t);  // host side only; device buffers are context allocations
 
@@ -69,6 +76,7 @@ struct rh_ctx {
     bool use_graphs = true;
     hipGraphExec_t dgraph = nullptr;
     int dgraph_B = 0;
+    std::vector<rhrt::FwdGraph> fgraphs;  // forward graphs, most recent last
     // no profiling events while set: a graph is being captured, or the call
     // must not create runtime objects (rh_decode_step_noalloc)
     bool events_off = false;
@@ -171,6 +179,15 @@ TensorMap layer_map(rh_ctx* ctx, int l, int j);
 // embedding) kept by the optimizer, or null when there is none or the
 // device weights changed since it was written.
 const float* train_master(const rh_ctx* ctx, int l, int j);
+// The fp32 master of weight tensor j of layer l (j = -1: the embedding),
+// allocating the masters on first use; a weight load writes through it.
+int master_for_load(rh_ctx* ctx, int l, int j, float** out);
+// After a weight write (wgen already bumped): the masters hold the new
+// weights when masters_hold_them is set (an fp32 load), otherwise they are
+// stale; the moments restart from zero (ModelOptState::zeros).
+int weights_written(rh_ctx* ctx, bool masters_hold_them);
+// Destroys the captured graphs (their kernel arguments hold buffer addresses).
+void drop_graphs(rh_ctx* ctx);
 
 void set_sk(const rh_ctx* ctx, rh::GemmArgs& g);
 int ensure_rope(rh_ctx* ctx, int npos);

@@ -54,6 +54,7 @@ int ensure_rope(rh_ctx* ctx, int npos) {
             t[(size_t)p * (hd / 2) + i] = make_float2(std::cos(th), std::sin(th));
         }
     HCK(hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);  // captured steps hold the old table's address
     dfree(ctx, ctx->rope);
     ctx->rope = nullptr;
     RCK(dalloc(ctx, &ctx->rope, t.size()));
@@ -62,9 +63,18 @@ int ensure_rope(rh_ctx* ctx, int npos) {
     return RH_OK;
 }
 
+void drop_graphs(rh_ctx* ctx) {
+    if (ctx->dgraph) (void)hipGraphExecDestroy(ctx->dgraph);
+    ctx->dgraph = nullptr;
+    ctx->dgraph_B = 0;
+    for (auto& g : ctx->fgraphs) (void)hipGraphExecDestroy(g.exec);
+    ctx->fgraphs.clear();
+}
+
 int ensure_workspace(rh_ctx* ctx, int M) {
     if (M <= ctx->ws_M) return RH_OK;
     HCK(hipStreamSynchronize(ctx->stream));
+    drop_graphs(ctx);  // captured forwards hold the old buffers' addresses
     void* olds[] = {ctx->x, ctx->xn, ctx->q, ctx->kbuf, ctx->vbuf, ctx->attn, ctx->gate,
                     ctx->logits, ctx->tok_loss, ctx->mean, ctx->d_tok, ctx->d_tgt};
     for (void* p : olds) dfree(ctx, p);
@@ -183,6 +193,58 @@ int rhrt::enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss, const f16* xf)
     }
     return RH_OK;
 }
+
+namespace {
+
+bool profiling(const rh_ctx* ctx) {
+    for (const auto& p : ctx->prof)
+        if (p.on) return true;
+    return false;
+}
+
+// The forward over d_tok (and d_tgt): enqueue_body + enqueue_tail, replayed
+// from a captured graph per (B, S, loss) -- about 226 launches at 7B become
+// one -- or launched eagerly when graphs are off or a kernel class is being
+// timed (per-launch events need the eager launches).
+constexpr size_t kMaxFwdGraphs = 8;
+int run_forward(rh_ctx* ctx, int B, int S, bool with_loss) {
+    if (!ctx->use_graphs || profiling(ctx)) {
+        RCK(enqueue_body(ctx, B, S, false, true));
+        return enqueue_tail(ctx, B, S, with_loss);
+    }
+    auto& gs = ctx->fgraphs;
+    auto it = std::find_if(gs.begin(), gs.end(),
+                           [&](const FwdGraph& g) { return g.B == B && g.S == S && g.loss == with_loss; });
+    if (it == gs.end()) {
+        if (gs.size() >= kMaxFwdGraphs) {
+            (void)hipGraphExecDestroy(gs.front().exec);
+            gs.erase(gs.begin());
+        }
+        hipGraph_t graph = nullptr;
+        HCK(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+        ctx->events_off = true;
+        int rc = enqueue_body(ctx, B, S, false, true);
+        if (rc == RH_OK) rc = enqueue_tail(ctx, B, S, with_loss);
+        ctx->events_off = false;
+        const hipError_t ec = hipStreamEndCapture(ctx->stream, &graph);
+        if (rc != RH_OK) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return rc;
+        }
+        HCK(ec);
+        FwdGraph g;
+        g.B = B; g.S = S; g.loss = with_loss;
+        const hipError_t ei = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        HCK(ei);
+        gs.push_back(g);
+        it = gs.end() - 1;
+    }
+    HCK(hipGraphLaunch(it->exec, ctx->stream));
+    return RH_OK;
+}
+
+}  // namespace
 
 // One decode step for B tokens at position b.state[0].  For small B the
 // RMSNorms run inside the QKV / W1|W3 / logits GEMVs (one launch fewer per
@@ -321,12 +383,12 @@ int rhrt::check_tokens(rh_ctx* ctx, const uint32_t* t, size_t n) {
 
 namespace {
 
-// staging (fp32, reference orientation) -> device fp16 layout
-int pack_from_staging(rh_ctx* ctx, const TensorMap& m) {
+// src (fp32, reference orientation, on the device) -> device fp16 layout
+int pack_from(rh_ctx* ctx, const float* src, const TensorMap& m) {
     if (m.map < 0) {
-        LCK(rh::launch_pack_rows(ctx->staging, m.dst, m.R, m.C, ctx->stream));
+        LCK(rh::launch_pack_rows(src, m.dst, m.R, m.C, ctx->stream));
     } else {
-        LCK(rh::launch_pack_transpose(ctx->staging, m.dst, m.R, m.C, m.ldd, m.map, m.row_off, ctx->stream));
+        LCK(rh::launch_pack_transpose(src, m.dst, m.R, m.C, m.ldd, m.map, m.row_off, ctx->stream));
     }
     return RH_OK;
 }
@@ -344,7 +406,7 @@ void destroy_ctx(rh_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    if (ctx->dgraph) (void)hipGraphExecDestroy(ctx->dgraph);
+    drop_graphs(ctx);
     for (auto& p : ctx->prof)
         for (auto& e : p.ev) { (void)hipEventDestroy(e.first); (void)hipEventDestroy(e.second); }
     rhrt::train_state_free(ctx->train);
@@ -447,23 +509,30 @@ int rh_load_weights_f32(rh_ctx* ctx, const float* embed, const float* gamma_fina
     const size_t D = c.dim, F = c.hidden, V = c.vocab;
     for (int i = 0; i < 9 * c.nlayers; ++i)
         if (!layer_tensors[i]) return fail(ctx, RH_EINVAL, "null layer tensor " + std::to_string(i));
-    RCK(ensure_staging(ctx, std::max({V * D, D * F, D * D})));
+    // Each matrix lands in its fp32 master copy (kept for the optimizer and
+    // rh_read_weights_f32, so training resumes from the exact values), which
+    // is then packed to the fp16 device layout.
     hipStream_t st = ctx->stream;
-    HCK(hipMemcpyAsync(ctx->staging, embed, V * D * sizeof(float), hipMemcpyHostToDevice, st));
-    LCK(rh::launch_pack_rows(ctx->staging, ctx->embed, (int)V, (int)D, st));
+    float* mst = nullptr;
+    RCK(master_for_load(ctx, 0, -1, &mst));
+    HCK(hipMemcpyAsync(mst, embed, V * D * sizeof(float), hipMemcpyHostToDevice, st));
+    LCK(rh::launch_pack_rows(mst, ctx->embed, (int)V, (int)D, st));
     HCK(hipMemcpyAsync(ctx->gfinal, gamma_final, D * sizeof(float), hipMemcpyHostToDevice, st));
     for (int l = 0; l < c.nlayers; ++l) {
         const float* const* t = layer_tensors + 9 * l;
         for (int j = 0; j < 7; ++j) {
             const TensorMap m = layer_map(ctx, l, j);
-            HCK(hipMemcpyAsync(ctx->staging, t[j], (size_t)m.R * m.C * sizeof(float), hipMemcpyHostToDevice, st));
-            RCK(pack_from_staging(ctx, m));
+            RCK(master_for_load(ctx, l, j, &mst));
+            HCK(hipMemcpyAsync(mst, t[j], (size_t)m.R * m.C * sizeof(float), hipMemcpyHostToDevice, st));
+            RCK(pack_from(ctx, mst, m));
         }
         HCK(hipMemcpyAsync(ctx->L[l].g1, t[7], D * sizeof(float), hipMemcpyHostToDevice, st));
         HCK(hipMemcpyAsync(ctx->L[l].g2, t[8], D * sizeof(float), hipMemcpyHostToDevice, st));
     }
     HCK(hipStreamSynchronize(st));
     ++ctx->wgen;
+    RCK(weights_written(ctx, true));
+    (void)F;
     return RH_OK;
 }
 
@@ -523,13 +592,14 @@ int rh_init_weights_normal(rh_ctx* ctx, uint64_t seed, float std_) {
         for (int j = 0; j < 7; ++j) {
             const TensorMap m = layer_map(ctx, l, j);
             LCK(rh::launch_init_normal(ctx->staging, (size_t)m.R * m.C, seed, 1u + 9u * l + j, std_, st));
-            RCK(pack_from_staging(ctx, m));
+            RCK(pack_from(ctx, ctx->staging, m));
         }
         LCK(rh::launch_fill_f32(ctx->L[l].g1, 1.0f, D, st));
         LCK(rh::launch_fill_f32(ctx->L[l].g2, 1.0f, D, st));
     }
     HCK(hipStreamSynchronize(st));
     ++ctx->wgen;
+    RCK(weights_written(ctx, false));
     (void)F;
     return RH_OK;
 }
@@ -549,8 +619,7 @@ int rh_forward_dev(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets,
     HCK(hipMemcpyAsync(ctx->d_tok, tokens, (size_t)M * sizeof(uint32_t), hipMemcpyDeviceToDevice, st));
     if (targets)
         HCK(hipMemcpyAsync(ctx->d_tgt, targets, (size_t)M * sizeof(uint32_t), hipMemcpyDeviceToDevice, st));
-    RCK(enqueue_body(ctx, batch, seq, false, true));
-    RCK(enqueue_tail(ctx, batch, seq, targets != nullptr));
+    RCK(run_forward(ctx, batch, seq, targets != nullptr));
     const size_t V = V_(ctx);
     if (logits_out)
         HCK(hipMemcpyAsync(logits_out, ctx->logits, (size_t)M * V * sizeof(float), hipMemcpyDeviceToDevice, st));
@@ -577,8 +646,7 @@ int rh_forward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int
     hipStream_t st = ctx->stream;
     HCK(hipMemcpyAsync(ctx->d_tok, tokens, M * sizeof(uint32_t), hipMemcpyHostToDevice, st));
     if (targets) HCK(hipMemcpyAsync(ctx->d_tgt, targets, M * sizeof(uint32_t), hipMemcpyHostToDevice, st));
-    RCK(enqueue_body(ctx, batch, seq, false, true));
-    RCK(enqueue_tail(ctx, batch, seq, targets != nullptr));
+    RCK(run_forward(ctx, batch, seq, targets != nullptr));
     const size_t V = V_(ctx);
     if (logits_out) HCK(hipMemcpyAsync(logits_out, ctx->logits, M * V * sizeof(float), hipMemcpyDeviceToHost, st));
     if (token_losses_out)
@@ -622,9 +690,12 @@ int rh_prefill(rh_ctx* ctx, const uint32_t* tokens, int batch, int len, uint32_t
     return check_err_flag(ctx);
 }
 
-int rh_decode_step(rh_ctx* ctx, const uint32_t* in_tok, uint32_t* out_tok, float* logits_out) {
+int rh_decode_step(rh_ctx* ctx, int batch, const uint32_t* in_tok, uint32_t* out_tok, float* logits_out) {
     if (!ctx || !in_tok) return fail(ctx, RH_EINVAL, "null argument");
     if (!ctx->have_prefill) return fail(ctx, RH_ESTATE, "rh_decode_step before rh_prefill");
+    if (batch != ctx->dec_B)
+        return fail(ctx, RH_EINVAL, "batch " + std::to_string(batch) + " differs from the prefill batch " +
+                                        std::to_string(ctx->dec_B));
     if (ctx->host_pos >= ctx->max_ctx) return fail(ctx, RH_ERANGE, "KV cache is full");
     const int B = ctx->dec_B;
     RCK(check_tokens(ctx, in_tok, B));
@@ -642,9 +713,12 @@ int rh_decode_step(rh_ctx* ctx, const uint32_t* in_tok, uint32_t* out_tok, float
     return check_err_flag(ctx);
 }
 
-int rh_decode(rh_ctx* ctx, const uint32_t* in_tok, int nsteps, uint32_t* out_tokens) {
+int rh_decode(rh_ctx* ctx, int batch, const uint32_t* in_tok, int nsteps, uint32_t* out_tokens) {
     if (!ctx || !in_tok || !out_tokens) return fail(ctx, RH_EINVAL, "null argument");
     if (!ctx->have_prefill) return fail(ctx, RH_ESTATE, "rh_decode before rh_prefill");
+    if (batch != ctx->dec_B)
+        return fail(ctx, RH_EINVAL, "batch " + std::to_string(batch) + " differs from the prefill batch " +
+                                        std::to_string(ctx->dec_B));
     if (nsteps <= 0 || ctx->host_pos + nsteps > ctx->max_ctx)
         return fail(ctx, RH_ERANGE, "nsteps must be >= 1 and fit in the KV cache");
     const int B = ctx->dec_B;
@@ -663,10 +737,7 @@ int rh_decode(rh_ctx* ctx, const uint32_t* in_tok, int nsteps, uint32_t* out_tok
 int rh_set_softcap(rh_ctx* ctx, float softcap) {
     if (!ctx) return RH_EINVAL;
     if (!(softcap >= 0.f)) return fail(ctx, RH_EINVAL, "softcap must be >= 0");
-    if (softcap != ctx->cfg.softcap && ctx->dgraph) {
-        (void)hipGraphExecDestroy(ctx->dgraph);  // the captured step bakes the softcap in
-        ctx->dgraph = nullptr;
-    }
+    if (softcap != ctx->cfg.softcap) drop_graphs(ctx);  // captured launches bake the softcap in
     ctx->cfg.softcap = softcap;
     return RH_OK;
 }

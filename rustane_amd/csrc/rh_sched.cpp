@@ -36,7 +36,18 @@ struct Job {
     int len = 0, nsteps = 0;
     uint32_t* out_tokens = nullptr;         // generate: caller's [nsteps]
     Clock::time_point submitted;
+    int status = RH_OK;                     // set at submit for a request that cannot run
+    std::string message;
 };
+
+// The first id >= vocab in ids[0..n), as an error message; empty if none.
+std::string bad_id(const std::vector<uint32_t>& ids, int vocab, const char* what) {
+    for (size_t i = 0; i < ids.size(); ++i)
+        if (ids[i] >= (uint32_t)vocab)
+            return std::string(what) + " id " + std::to_string(ids[i]) + " at index " + std::to_string(i) +
+                   " >= vocab " + std::to_string(vocab);
+    return std::string();
+}
 
 float ms_between(Clock::time_point a, Clock::time_point b) {
     return std::chrono::duration<float, std::milli>(b - a).count();
@@ -47,7 +58,7 @@ float ms_between(Clock::time_point a, Clock::time_point b) {
 struct rh_sched {
     rh_ctx* ctx = nullptr;
     rh_sched_config cfg{};
-    int ctx_max_batch = 0, ctx_max_ctx = 0;
+    int ctx_max_batch = 0, ctx_max_ctx = 0, vocab = 0;
     std::mutex mu;
     std::condition_variable cv_jobs, cv_space, cv_results;
     std::deque<Job> queue;
@@ -85,6 +96,10 @@ void rh_sched::serve(std::vector<Job>& batch) {
     const auto t0 = Clock::now();
     int rc = RH_OK;
     std::vector<float> loss(B, 0.0f);
+    if (j0.status != RH_OK) {  // refused at submit; always served alone
+        post(j0, j0.status, 0.0f, 1, t0, Clock::now(), j0.message);
+        return;
+    }
     if (j0.kind == RH_JOB_FORWARD) {
         const int S = j0.len;
         std::vector<uint32_t> tok((size_t)B * S), tgt((size_t)B * S);
@@ -98,7 +113,7 @@ void rh_sched::serve(std::vector<Job>& batch) {
         std::vector<uint32_t> prompt((size_t)B * P), first(B), rest((size_t)std::max(n - 1, 0) * B);
         for (int b = 0; b < B; ++b) std::memcpy(&prompt[(size_t)b * P], batch[b].tokens.data(), (size_t)P * 4);
         rc = rh_prefill(ctx, prompt.data(), B, P, first.data(), nullptr);
-        if (rc == RH_OK && n > 1) rc = rh_decode(ctx, first.data(), n - 1, rest.data());
+        if (rc == RH_OK && n > 1) rc = rh_decode(ctx, B, first.data(), n - 1, rest.data());
         if (rc == RH_OK)
             for (int b = 0; b < B; ++b) {
                 batch[b].out_tokens[0] = first[b];
@@ -127,15 +142,19 @@ void rh_sched::run() {
                     if (stop) return true;
                     int same = 0;
                     for (const Job& j : queue)
-                        same += j.kind == queue.front().kind && j.len == queue.front().len &&
-                                j.nsteps == queue.front().nsteps;
-                    return same >= cap;
+                        same += j.status == RH_OK && j.kind == queue.front().kind &&
+                                j.len == queue.front().len && j.nsteps == queue.front().nsteps;
+                    return queue.front().status != RH_OK || same >= cap;
                 });
             }
-            // FIFO: the head, then every later job with the same shape, up to cap.
+            // FIFO: the head, then every later runnable job with the same
+            // shape, up to cap.  A job refused at submit is never batched: its
+            // bad ids would fail the whole launch.
             const int kind = queue.front().kind, len = queue.front().len, nsteps = queue.front().nsteps;
-            for (auto it = queue.begin(); it != queue.end() && (int)batch.size() < cap;) {
-                if (it->kind == kind && it->len == len && it->nsteps == nsteps) {
+            const int batch_cap = queue.front().status == RH_OK ? cap : 1;
+            for (auto it = queue.begin(); it != queue.end() && (int)batch.size() < batch_cap;) {
+                if (batch.empty() ||
+                    (it->status == RH_OK && it->kind == kind && it->len == len && it->nsteps == nsteps)) {
                     batch.push_back(std::move(*it));
                     it = queue.erase(it);
                 } else {
@@ -159,7 +178,9 @@ int rh_sched_create(rh_ctx* ctx, const rh_sched_config* cfg, rh_sched** out) {
     if (!s) return rh_internal_fail(ctx, RH_ENOMEM, "out of host memory");
     s->ctx = ctx;
     s->cfg = *cfg;
-    rh_context_info(ctx, nullptr, &s->ctx_max_batch, &s->ctx_max_ctx);
+    rh_config c{};
+    rh_context_info(ctx, &c, &s->ctx_max_batch, &s->ctx_max_ctx);
+    s->vocab = c.vocab;
     try {
         s->worker = std::thread([s] { s->run(); });
     } catch (...) {
@@ -200,6 +221,11 @@ int rh_sched_submit(rh_sched* s, const rh_sched_request* rq) {
     } else {
         return RH_EINVAL;
     }
+    // Out-of-range ids fail this request alone (its result carries
+    // RH_ERANGE); the reference's per-request workers are independent too.
+    j.message = bad_id(j.tokens, s->vocab, "token");
+    if (j.message.empty() && j.kind == RH_JOB_FORWARD) j.message = bad_id(j.targets, s->vocab, "target");
+    if (!j.message.empty()) j.status = RH_ERANGE;
     std::unique_lock<std::mutex> lk(s->mu);
     if (s->stop) return RH_ESTATE;
     s->cv_space.wait(lk, [&] { return (int)s->queue.size() < s->cfg.queue_capacity; });

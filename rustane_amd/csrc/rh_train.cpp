@@ -57,20 +57,39 @@ struct TrainState {
     float *gout = nullptr, *dres = nullptr, *Drow = nullptr, *dgp = nullptr;
     uint32_t* utok = nullptr;
     int *ustart = nullptr, *uidx = nullptr;
-    // optimizer (ModelOptState + the fp32 master weights), created by the first update
+    // optimizer: the fp32 master weights (created by the first fp32 weight
+    // load or optimizer call) and ModelOptState's moments (first optimizer call)
     struct Opt {
         float* emb = nullptr;                  // master embedding [V][D]
         std::vector<std::array<float*, 7>> w;  // masters of the 7 matrices per layer
+        uint64_t synced = 0;                   // weight version the masters hold
+        bool moments = false;                  // moments and norm partials allocated
         float *emb_m = nullptr, *emb_v = nullptr, *gf_m = nullptr, *gf_v = nullptr;
         std::vector<std::array<float*, 9>> m, v;
         float* part = nullptr;  // sum-of-squares partials of the gradient norm
-        uint64_t synced = 0;    // weight version the masters hold
     };
     Opt* opt = nullptr;
     ~TrainState() { delete opt; }
 };
 
 void train_state_free(TrainState* t) { delete t; }
+
+int ensure_masters(rh_ctx* ctx);
+int zero_moments(rh_ctx* ctx);
+
+int master_for_load(rh_ctx* ctx, int l, int j, float** out) {
+    RCK(ensure_masters(ctx));
+    *out = j < 0 ? ctx->train->opt->emb : ctx->train->opt->w[l][j];
+    return RH_OK;
+}
+
+int weights_written(rh_ctx* ctx, bool masters_hold_them) {
+    TrainState* T = ctx->train;
+    if (!T || !T->opt) return RH_OK;
+    if (masters_hold_them) T->opt->synced = ctx->wgen;
+    if (T->opt->moments) RCK(zero_moments(ctx));
+    return RH_OK;
+}
 
 const float* train_master(const rh_ctx* ctx, int l, int j) {
     const TrainState* T = ctx->train;
@@ -86,15 +105,18 @@ namespace {
 
 size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
 
+// The host side of the training state (no device memory yet).
+int ensure_train_host(rh_ctx* ctx) {
+    if (ctx->train) return RH_OK;
+    ctx->train = new (std::nothrow) TrainState;
+    return ctx->train ? RH_OK : fail(ctx, RH_ENOMEM, "out of host memory");
+}
+
 // Gradients and transposed weights: allocated once per context.
 int ensure_train_static(rh_ctx* ctx) {
+    RCK(ensure_train_host(ctx));
     TrainState* T = ctx->train;
-    if (T && T->dembed) return RH_OK;
-    if (!T) {
-        T = new (std::nothrow) TrainState;
-        if (!T) return fail(ctx, RH_ENOMEM, "out of host memory");
-        ctx->train = T;
-    }
+    if (T->dembed) return RH_OK;
     const rh_config& c = ctx->cfg;
     const size_t D = c.dim, F = c.hidden, V = c.vocab, Vp = round_up(V, 128);
     RCK(dalloc(ctx, &T->dembed, V * D));
@@ -354,46 +376,81 @@ const size_t* tensor_sizes(const rh_config& c, size_t out[9]) {
     return out;
 }
 
-// Optimizer state: moments (zeroed) and fp32 masters, re-read from the
-// device weights whenever those changed outside the optimizer.
+}  // namespace
+
+// fp32 master weights (reference orientation): allocated once.
+int rhrt::ensure_masters(rh_ctx* ctx) {
+    RCK(ensure_train_host(ctx));
+    TrainState* T = ctx->train;
+    if (!T->opt) {
+        T->opt = new (std::nothrow) TrainState::Opt;
+        if (!T->opt) return fail(ctx, RH_ENOMEM, "out of host memory");
+    }
+    auto* o = T->opt;
+    if (o->emb) return RH_OK;
+    const rh_config& c = ctx->cfg;
+    size_t sz[9];
+    tensor_sizes(c, sz);
+    RCK(dalloc(ctx, &o->emb, (size_t)c.vocab * c.dim));
+    o->w.resize(c.nlayers);
+    for (int l = 0; l < c.nlayers; ++l)
+        for (int j = 0; j < 7; ++j) RCK(dalloc(ctx, &o->w[l][j], sz[j]));
+    return RH_OK;
+}
+
+// Zeroes the moments (ModelOptState::zeros).
+int rhrt::zero_moments(rh_ctx* ctx) {
+    auto* o = ctx->train->opt;
+    const rh_config& c = ctx->cfg;
+    size_t sz[9];
+    tensor_sizes(c, sz);
+    hipStream_t st = ctx->stream;
+    const size_t VD = (size_t)c.vocab * c.dim;
+    LCK(rh::launch_fill_f32(o->emb_m, 0.f, VD, st));
+    LCK(rh::launch_fill_f32(o->emb_v, 0.f, VD, st));
+    LCK(rh::launch_fill_f32(o->gf_m, 0.f, c.dim, st));
+    LCK(rh::launch_fill_f32(o->gf_v, 0.f, c.dim, st));
+    for (int l = 0; l < c.nlayers; ++l)
+        for (int j = 0; j < 9; ++j) {
+            LCK(rh::launch_fill_f32(o->m[l][j], 0.f, sz[j], st));
+            LCK(rh::launch_fill_f32(o->v[l][j], 0.f, sz[j], st));
+        }
+    return RH_OK;
+}
+
+namespace {
+
+// Optimizer state: masters, moments (zeroed when created) and the norm's
+// partials.  Masters older than the device weights (rh_init_weights_normal)
+// are re-read from the fp16 device copy.
 int ensure_opt(rh_ctx* ctx) {
     RCK(ensure_train_static(ctx));
+    RCK(ensure_masters(ctx));
     TrainState* T = ctx->train;
+    auto* o = T->opt;
     const rh_config& c = ctx->cfg;
     const size_t D = c.dim, V = c.vocab;
     size_t sz[9];
     tensor_sizes(c, sz);
     hipStream_t st = ctx->stream;
-    if (!T->opt) {
-        T->opt = new (std::nothrow) TrainState::Opt;
-        if (!T->opt) return fail(ctx, RH_ENOMEM, "out of host memory");
-        auto* o = T->opt;
-        RCK(dalloc(ctx, &o->emb, V * D));
+    if (!o->moments) {
         RCK(dalloc(ctx, &o->emb_m, V * D));
         RCK(dalloc(ctx, &o->emb_v, V * D));
         RCK(dalloc(ctx, &o->gf_m, D));
         RCK(dalloc(ctx, &o->gf_v, D));
-        o->w.resize(c.nlayers);
         o->m.resize(c.nlayers);
         o->v.resize(c.nlayers);
         size_t nparts = rh::sumsq_blocks(V * D) + rh::sumsq_blocks(D);
-        for (int l = 0; l < c.nlayers; ++l) {
+        for (int l = 0; l < c.nlayers; ++l)
             for (int j = 0; j < 9; ++j) {
-                if (j < 7) RCK(dalloc(ctx, &o->w[l][j], sz[j]));
                 RCK(dalloc(ctx, &o->m[l][j], sz[j]));
                 RCK(dalloc(ctx, &o->v[l][j], sz[j]));
-                LCK(rh::launch_fill_f32(o->m[l][j], 0.f, sz[j], st));
-                LCK(rh::launch_fill_f32(o->v[l][j], 0.f, sz[j], st));
                 nparts += rh::sumsq_blocks(sz[j]);
             }
-        }
         RCK(dalloc(ctx, &o->part, nparts));
-        LCK(rh::launch_fill_f32(o->emb_m, 0.f, V * D, st));
-        LCK(rh::launch_fill_f32(o->emb_v, 0.f, V * D, st));
-        LCK(rh::launch_fill_f32(o->gf_m, 0.f, D, st));
-        LCK(rh::launch_fill_f32(o->gf_v, 0.f, D, st));
+        o->moments = true;
+        RCK(zero_moments(ctx));
     }
-    auto* o = T->opt;
     if (o->synced != ctx->wgen) {
         LCK(rh::launch_unpack_rows(ctx->embed, o->emb, (int)V, (int)D, st));
         for (int l = 0; l < c.nlayers; ++l)
@@ -533,6 +590,15 @@ int rh_update_weights(rh_ctx* ctx, uint32_t t, float lr, const rh_train_config* 
     return RH_OK;
 }
 
+}  // extern "C"
+
+namespace {
+int train_step_body(rh_ctx* ctx, const rh_tokens* data, uint32_t step, const rh_train_config* tc,
+                    uint64_t max_pos, float* loss_out, float* grad_norm_out);
+}  // namespace
+
+extern "C" {
+
 int rh_train_step(rh_ctx* ctx, const rh_tokens* data, uint32_t step, const rh_train_config* tc, float* loss_out,
                   float* grad_norm_out) {
     if (!ctx || !data || !tc) return fail(ctx, RH_EINVAL, "null argument");
@@ -542,7 +608,22 @@ int rh_train_step(rh_ctx* ctx, const rh_tokens* data, uint32_t step, const rh_tr
     const int64_t n = rh_tokens_len(data);
     if (n < (int64_t)S + 2) return fail(ctx, RH_ERANGE, "token data shorter than seq + 2");
     const uint64_t max_pos = (uint64_t)(n - S - 1);
+    // The training forward uses tc->softcap; the context's own softcap (the
+    // one later forwards and decodes use) is restored on every exit.
+    const float saved_softcap = ctx->cfg.softcap;
     RCK(rh_set_softcap(ctx, tc->softcap));
+    const int rc = train_step_body(ctx, data, step, tc, max_pos, loss_out, grad_norm_out);
+    RCK(rh_set_softcap(ctx, saved_softcap));
+    return rc;
+}
+
+}  // extern "C"
+
+namespace {
+
+int train_step_body(rh_ctx* ctx, const rh_tokens* data, uint32_t step, const rh_train_config* tc,
+                    uint64_t max_pos, float* loss_out, float* grad_norm_out) {
+    const int S = ctx->cfg.seq;
     RCK(rh_zero_grads(ctx));
     // train_step_with_options (full_model.rs:1510-1600): accum_steps sequences
     // at pseudo-random positions (step*7919 + micro*104729) % max_pos, run as
@@ -572,6 +653,10 @@ int rh_train_step(rh_ctx* ctx, const rh_tokens* data, uint32_t step, const rh_tr
     if (grad_norm_out) *grad_norm_out = scaled;
     return RH_OK;
 }
+
+}  // namespace
+
+extern "C" {
 
 // Zeroing is logical: the next backward's weight-gradient GEMMs and gamma
 // reductions store instead of accumulating, and reads return zeros until

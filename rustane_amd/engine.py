@@ -179,7 +179,12 @@ class ModelWeights:
     embed: np.ndarray        # [VOCAB, DIM]
     layers: list             # [LayerWeights]
     gamma_final: np.ndarray  # [DIM]
-    generation: int = field(default=0)
+    # Upload-cache key.  None (the default): a forward uploads the weights on
+    # every call, as the reference re-stages them on every call
+    # (layer.rs:4670-4705), so in-place changes are always seen.  An int:
+    # the context keeps the upload while (object, version) is unchanged, and
+    # every in-place write must be followed by bump().
+    version: int | None = field(default=None)
 
     @staticmethod
     def random(cfg: ModelConfig) -> "ModelWeights":
@@ -208,8 +213,9 @@ class ModelWeights:
         return ModelWeights(mat(cfg.vocab, D), layers, np.ones(D, np.float32))
 
     def bump(self):
-        """Marks the weights as changed (the reference's w2_generation idea)."""
-        self.generation += 1
+        """Marks the weights as changed and opts into upload caching (the
+        reference's w2_generation idea, training.rs:121)."""
+        self.version = 1 if self.version is None else self.version + 1
 
 
 # --------------------------------------------------------------------------- kernels
@@ -232,8 +238,10 @@ class CompiledKernels:
     try_compile = compile
 
     def ensure_weights(self, weights: ModelWeights):
-        key = (id(weights), weights.generation)
-        if self._loaded != key:
+        """Uploads the weights unless they carry a version and that
+        (object, version) is the one uploaded last."""
+        key = None if weights.version is None else (id(weights), weights.version)
+        if key is None or self._loaded != key:
             self.ctx.load_weights(weights.embed, weights.gamma_final,
                                   [lw.tensors() for lw in weights.layers])
             self._loaded = key

@@ -126,8 +126,8 @@ def lib():
     L.rh_read_grads_f32.argtypes = [ctxp, _f32p, _f32p, ctypes.POINTER(_f32p)]
     L.rh_forward_dev.argtypes = [ctxp, _vp, _vp, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp]
     L.rh_prefill.argtypes = [ctxp, _u32p, ctypes.c_int, ctypes.c_int, _u32p, _f32p]
-    L.rh_decode_step.argtypes = [ctxp, _u32p, _u32p, _f32p]
-    L.rh_decode.argtypes = [ctxp, _u32p, ctypes.c_int, _u32p]
+    L.rh_decode_step.argtypes = [ctxp, ctypes.c_int, _u32p, _u32p, _f32p]
+    L.rh_decode.argtypes = [ctxp, ctypes.c_int, _u32p, ctypes.c_int, _u32p]
     L.rh_decode_step_noalloc.argtypes = [ctxp, ctypes.c_int, _vp, _vp, _vp]
     L.rh_decode_pos.argtypes = [ctxp, ctypes.POINTER(ctypes.c_int)]
     L.rh_set_softcap.argtypes = [ctxp, ctypes.c_float]
@@ -328,7 +328,7 @@ class Context:
         in_tok = np.ascontiguousarray(in_tok, np.uint32).reshape(-1)
         out = np.empty_like(in_tok)
         lg = np.empty((len(in_tok), self.cfg.vocab), np.float32) if want_logits else None
-        self._ck(lib().rh_decode_step(self.h, _u(in_tok), _u(out), _f(lg)), "rh_decode_step")
+        self._ck(lib().rh_decode_step(self.h, len(in_tok), _u(in_tok), _u(out), _f(lg)), "rh_decode_step")
         return out, lg
 
     def decode_step_noalloc(self, batch: int, in_tok_ptr: int, out_tok_ptr: int, logits_ptr=None):
@@ -339,7 +339,7 @@ class Context:
     def decode(self, in_tok, nsteps: int):
         in_tok = np.ascontiguousarray(in_tok, np.uint32).reshape(-1)
         out = np.empty((nsteps, len(in_tok)), np.uint32)
-        self._ck(lib().rh_decode(self.h, _u(in_tok), nsteps, _u(out)), "rh_decode")
+        self._ck(lib().rh_decode(self.h, len(in_tok), _u(in_tok), nsteps, _u(out)), "rh_decode")
         return out
 
     @property

@@ -104,8 +104,9 @@ def test_null_context_is_rejected_everywhere(lib):
     assert lib.rh_forward(None, tp, tp, 1, 4, None, None, ctypes.byref(f)) == hb.RH_EINVAL
     assert lib.rh_forward_dev(None, None, None, 1, 4, None, None, None) == hb.RH_EINVAL
     assert lib.rh_prefill(None, tp, 1, 4, None, None) == hb.RH_EINVAL
-    assert lib.rh_decode_step(None, tp, tp, None) == hb.RH_EINVAL
-    assert lib.rh_decode(None, tp, 1, tp) == hb.RH_EINVAL
+    assert lib.rh_decode_step(None, 1, tp, tp, None) == hb.RH_EINVAL
+    assert lib.rh_decode(None, 1, tp, 1, tp) == hb.RH_EINVAL
+    assert lib.rh_decode_step_noalloc(None, 1, None, None, None) == hb.RH_EINVAL
     assert lib.rh_decode_pos(None, ctypes.byref(pos)) == hb.RH_EINVAL
     assert lib.rh_set_softcap(None, 1.0) == hb.RH_EINVAL
     assert lib.rh_sync(None) == hb.RH_EINVAL

@@ -183,3 +183,33 @@ def test_profile_counts_and_times_launches(orc):
         c.profile_enable(hb.K_GEMM_W13, False)
         c.forward(tok, tgt)
         assert c.profile_read(hb.K_GEMM_W13)[1] == 0
+
+
+def test_forward_graph_replays_equal_eager_launches():
+    """Forwards replayed from captured graphs (one per batch, seq and
+    loss/no-loss) are bit-identical to eager launches of the same kernels:
+    several replays with eager work and synchronisations between them, new
+    tokens each time, two shapes, a softcap change (which drops the graphs)
+    and a context whose workspace grows after capture."""
+    cfg = small_cfg(dim=512, hidden=1024, heads=4, hd=128, nlayers=2, vocab=1000, seq=96)
+    w = random_gammas(ModelWeights.normal(cfg, seed=221, std=0.05), seed=222)
+    cases = [tokens_uniform(223 + i, cfg.vocab, b, s) for i, (b, s) in
+             enumerate([(1, 96), (1, 96), (3, 40), (1, 96), (3, 40), (2, 130)])]
+    results = {}
+    for graphs in (False, True):
+        with _ctx(cfg, w, max_batch=3) as c:
+            c.set_graphs(graphs)
+            outs = []
+            for i, (tok, tgt) in enumerate(cases):
+                if i == 4:
+                    c.set_softcap(20.0)
+                outs.append(c.forward(tok, tgt))
+                outs.append(c.forward(tok, None, want_token_losses=False))   # the no-loss graph
+                c.sync()
+            results[graphs] = outs
+    for i, (a, b) in enumerate(zip(results[False], results[True])):
+        np.testing.assert_array_equal(a.logits, b.logits, err_msg=f"call {i}")
+        if a.token_losses is not None:
+            np.testing.assert_array_equal(a.token_losses, b.token_losses)
+            np.testing.assert_array_equal(a.mean_loss, b.mean_loss)
+    print(f"[result] {len(results[True])} graph-replayed forwards bit-identical to eager", flush=True)

@@ -75,3 +75,29 @@ def test_request_errors():
         with pytest.raises(hb.HipBridgeError) as e:  # prompt + steps beyond the KV cache
             s.run_batch([(4, np.zeros(30, np.uint32), None, 8)])
         assert e.value.code == hb.RH_ERANGE
+
+
+def test_request_error_fails_alone_in_a_batch():
+    """With max_batch 4 the bad request is queued among good ones of the same
+    shape; it fails alone and the others are batched and succeed."""
+    cfg = small_cfg(seq=16)
+    w = ModelWeights.normal(cfg, seed=96)
+    good = np.arange(17, dtype=np.uint32) % cfg.vocab
+    bad_tok, bad_tgt = good.copy(), good.copy()
+    bad_tok[5] = cfg.vocab + 7
+    bad_tgt[9] = cfg.vocab
+    reqs = [(1, good[:-1], good[1:]), (2, bad_tok[:-1], good[1:]), (3, good[:-1], good[1:]),
+            (4, good[:-1], bad_tgt[1:]), (5, good[:-1], good[1:])]
+    prompt_bad = good[:10].copy()
+    prompt_bad[2] = cfg.vocab
+    with _ctx(cfg, w, 4, 64) as c, hb.Scheduler(c, max_batch=4, max_wait_us=200000) as s:
+        res = s.run_batch(reqs)
+        gen = s.run_batch([(6, good[:10], None, 4), (7, prompt_bad, None, 4), (8, good[:10], None, 4)])
+    print(f"[result] statuses {[r.status for r in res]}, batches {[r.batch for r in res]}", flush=True)
+    assert [r.status for r in res] == [hb.RH_OK, hb.RH_ERANGE, hb.RH_OK, hb.RH_ERANGE, hb.RH_OK]
+    assert "token" in res[1].message and "target" in res[3].message
+    assert res[1].batch == res[3].batch == 1
+    assert max(res[i].batch for i in (0, 2, 4)) > 1
+    assert res[0].loss == res[2].loss == res[4].loss
+    assert [r.status for r in gen] == [hb.RH_OK, hb.RH_ERANGE, hb.RH_OK]
+    np.testing.assert_array_equal(gen[0].tokens, gen[2].tokens)
