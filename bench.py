@@ -145,6 +145,15 @@ def main():
             ctx.profile_enable(hb.K_GEMM_W13, False)
         return ms, wall, k_ms, k_n, loss, eager_ms
 
+    if args.copy_calibration:
+        nb = 256 << 20
+        src, dst = hip_rt.DeviceArray((nb,), np.uint8), hip_rt.DeviceArray((nb,), np.uint8)
+        for _ in range(3):
+            hip_rt.copy_d2d(dst, src, nb)
+        hip_rt.synchronize()
+        del src, dst
+        log(f"[bench] copy calibration: 3 x {nb} bytes device-to-device")
+
     if args.decode_only:
         print(json.dumps({"decode": run_decode(ctx, cfg, args, hb, E, hip_rt, stream)}), flush=True)
         return
@@ -155,14 +164,6 @@ def main():
             out["train_step_accum10"] = run_train_full(ctx, cfg, hb, E)
         print(json.dumps(out), flush=True)
         return
-
-    if args.copy_calibration:
-        nb = 256 << 20
-        src, dst = hip_rt.DeviceArray((nb,), np.uint8), hip_rt.DeviceArray((nb,), np.uint8)
-        for _ in range(3):
-            hip_rt.copy_d2d(dst, src, nb)
-        hip_rt.synchronize()
-        log(f"[bench] copy calibration: 3 x {nb} bytes device-to-device")
 
     B = args.batch
     ms, wall, k_ms, k_n, loss, eager_ms = run_prefill(B, args.steps, args.warmup)

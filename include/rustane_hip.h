@@ -155,9 +155,8 @@ int rh_decode_step(rh_ctx* ctx, int batch, const uint32_t* in_tok, uint32_t* out
  * one.  Its scratch (activations, attention partials, argmax partials,
  * position state; the logits too when logits_out is NULL) lives in a fixed
  * 64 MiB device array per GPU, shared by every call on that GPU: calls whose
- * work overlaps on one GPU race.  RH_ERANGE when the batch, model width and
- * max_ctx need more scratch than that (7B, batch 16, max_ctx 4096 needs
- * about 12 MiB). */
+ * work overlaps on one GPU race.  RH_ERANGE when the batch and model need
+ * more scratch than that (7B at batch 16 needs about 4 MiB). */
 int rh_decode_step_noalloc(rh_ctx* ctx, int batch, const uint32_t* in_tok, uint32_t* out_tok,
                            float* logits_out);
 

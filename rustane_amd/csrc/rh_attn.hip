@@ -454,24 +454,31 @@ __global__ __launch_bounds__(256) void attn_prefill_dma_kernel(const f16* __rest
     }
 }
 
-// Decode attention: one block per (chunk of DCH positions, head, sequence),
-// 4 waves.  Lane = LPP * slot + j: j owns dims 8j..8j+7 of one position
-// (16-byte K/V loads), so a wave covers 64 / LPP positions per pass.  Each
-// wave takes DCH/4 consecutive positions, issues every K and V load of them
-// first, and keeps an online-softmax state (m, l, o) per slot; slots merge
-// with shuffles and the 4 waves through LDS once at the end, so the block
-// pays the memory latency once and synchronises once.  Positions past the
-// current one read a clamped (valid) row and are masked.
-template <int HD, int DCH>
+// Decode attention: one block per (chunk, head, sequence), 4 waves.  A chunk
+// covers `per` consecutive positions (0: ceil(positions / chunks), computed
+// on the device from the current position), split evenly over the 4 waves.
+// Small batches split the context into many short chunks so the grid fills
+// the chip and every load of a block is in flight at once; large batches
+// give each (head, sequence) one block, which then writes the fp16 output
+// itself (no partials, no merge).  Lane = LPP * slot + j: j owns dims
+// 8j..8j+7 of one position (16-byte K/V loads), so a wave covers
+// SL = 64 / LPP positions per load instruction and STEP = SL * NP positions
+// per iteration.  K and V are streamed with nontemporal loads, double-
+// buffered in registers over iterations: the next iteration's loads are in
+// flight while the current one computes.  Each lane slot keeps an online-
+// softmax state (m, l, o); slots merge with shuffles and the 4 waves through
+// LDS once at the end.  Positions past the wave's range read a clamped
+// (valid) row and are masked; a chunk past the current position stores an
+// empty partial (m = -inf, l = 0, o = 0).
+template <int HD, int NP>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict__ Q,
                                                           const f16* __restrict__ Kc,
                                                           const f16* __restrict__ Vc,
                                                           const int* __restrict__ pos,
                                                           float* part_m, float* part_l,
-                                                          float* part_o, int H, int ctx,
-                                                          float scale) {
-    constexpr int LPP = HD / 8, SL = 64 / LPP, PW = DCH / 4, NP = PW / SL;
-    static_assert(NP * SL * 4 == DCH, "chunk must split over 4 waves x slots");
+                                                          float* part_o, f16* out, int H, int ctx,
+                                                          int per_fixed, float scale) {
+    constexpr int LPP = HD / 8, SL = 64 / LPP, STEP = SL * NP;
     __shared__ float sm_[4], sl_[4];
     __shared__ float so_[4][HD];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -479,42 +486,71 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict_
     const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int nch = gridDim.x;
     const int nctx = *pos + 1;
-    const int t0 = chunk * DCH, t1 = min(nctx, t0 + DCH);
+    const int per = per_fixed > 0 ? per_fixed : (nctx + nch - 1) / nch;
+    const int t0 = min(chunk * per, nctx), t1 = min(nctx, t0 + per);
     const size_t bh = (size_t)b * H + h;
-    const size_t pidx = bh * nch + chunk;
-    if (t0 >= t1) {
+    if (t0 >= t1) {  // chunk past the current position (only with fixed chunks, nch > 1)
+        const size_t pidx = bh * nch + chunk;
         if (tid == 0) { part_m[pidx] = -INFINITY; part_l[pidx] = 0.f; }
         if (tid < HD) part_o[pidx * HD + tid] = 0.f;
         return;
     }
+    const int wper = (t1 - t0 + 3) / 4;
+    const int w0 = min(t0 + w * wper, t1), w1 = min(t1, w0 + wper);
     const f16x8 qv = *(const f16x8*)(Q + bh * HD + 8 * j);
     const f16* Kb = Kc + bh * ctx * HD + 8 * j;
     const f16* Vb = Vc + bh * ctx * HD + 8 * j;
-    const int tw = t0 + w * PW + slot;  // this lane's first position; then + SL per pass
-    f16x8 kv[NP], vv[NP];
+    // iterations of this wave (wave-uniform); an empty range loads row 0
+    const int niter = (w1 - w0 + STEP - 1) / STEP;
+    const int last = w1 > w0 ? w1 - 1 : 0;
+    float m = -INFINITY, l = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    f16x8 ka[NP], va[NP], kb[NP], vb[NP];
+    auto load = [&](int it, f16x8 (&kr)[NP], f16x8 (&vr)[NP]) {
+        const int tb = w0 + it * STEP + slot;
 #pragma unroll
-    for (int i = 0; i < NP; ++i) kv[i] = *(const f16x8*)(Kb + (size_t)min(tw + i * SL, t1 - 1) * HD);
+        for (int i = 0; i < NP; ++i) kr[i] = ld_stream((const f16x8*)(Kb + (size_t)min(tb + i * SL, last) * HD));
 #pragma unroll
-    for (int i = 0; i < NP; ++i) vv[i] = *(const f16x8*)(Vb + (size_t)min(tw + i * SL, t1 - 1) * HD);
-    float sc[NP];
-    float m = -INFINITY;
+        for (int i = 0; i < NP; ++i) vr[i] = ld_stream((const f16x8*)(Vb + (size_t)min(tb + i * SL, last) * HD));
+    };
+    auto step = [&](int it, const f16x8 (&kr)[NP], const f16x8 (&vr)[NP]) {
+        const int tb = w0 + it * STEP + slot;
+        float sc[NP];
+        float mloc = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        float d = 0.f;
+        for (int i = 0; i < NP; ++i) {
+            float d = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) d += (float)qv[e] * (float)kv[i][e];
+            for (int e = 0; e < 8; ++e) d += (float)qv[e] * (float)kr[i][e];
 #pragma unroll
-        for (int o = LPP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, RH_WAVE);
-        sc[i] = tw + i * SL < t1 ? d * scale : -INFINITY;
-        m = fmaxf(m, sc[i]);
-    }
-    float l = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int x = LPP / 2; x > 0; x >>= 1) d += __shfl_xor(d, x, RH_WAVE);
+            sc[i] = tb + i * SL < w1 ? d * scale : -INFINITY;
+            mloc = fmaxf(mloc, sc[i]);
+        }
+        const float mn = fmaxf(m, mloc);
+        if (mn == -INFINITY) return;  // nothing live in this slot yet
+        const float c = m == -INFINITY ? 0.f : __expf(m - mn);
+        l *= c;
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const float p = sc[i] == -INFINITY ? 0.f : __expf(sc[i] - m);
-        l += p;
+        for (int e = 0; e < 8; ++e) o[e] *= c;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] += p * (float)vv[i][e];
+        for (int i = 0; i < NP; ++i) {
+            const float p = sc[i] == -INFINITY ? 0.f : __expf(sc[i] - mn);
+            l += p;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] += p * (float)vr[i][e];
+        }
+        m = mn;
+    };
+    load(0, ka, va);
+    if (niter <= 1) {  // wave-uniform: a short range needs no second buffer
+        step(0, ka, va);
+    } else {
+        for (int it = 0; it < niter; it += 2) {
+            load(it + 1, kb, vb);
+            step(it, ka, va);
+            load(it + 2, ka, va);
+            step(it + 1, kb, vb);
+        }
     }
     // merge the SL slots of the wave (lanes with equal j)
 #pragma unroll
@@ -543,14 +579,21 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict_
             L += sl_[v] * c;
             O += so_[v][tid] * c;
         }
-        part_o[pidx * HD + tid] = O;
-        if (tid == 0) { part_m[pidx] = M; part_l[pidx] = L; }
+        if (nch == 1) {
+            out[bh * HD + tid] = (f16)(O / L);
+        } else {
+            const size_t pidx = bh * nch + chunk;
+            part_o[pidx * HD + tid] = O;
+            if (tid == 0) { part_m[pidx] = M; part_l[pidx] = L; }
+        }
     }
 }
 
-// Merges the chunk partials of one (head, sequence).  The loads of 8 chunks
-// are issued together (the partials come from other XCDs' L2s, so each load
-// is a long round trip); empty chunks carry m = -inf, l = 0, o = 0.
+// Merges the chunk partials of one (head, sequence), MAXCH chunks per round:
+// all loads of a round are issued before the first use, so the block pays
+// one round trip per MAXCH partials (written by blocks on other XCDs);
+// empty chunks carry m = -inf, l = 0, o = 0.
+template <int MAXCH>
 __global__ void attn_merge_kernel(const float* part_m, const float* part_l, const float* part_o,
                                   f16* out, int H, int HD, int nch) {
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
@@ -558,16 +601,30 @@ __global__ void attn_merge_kernel(const float* part_m, const float* part_l, cons
     const float* pm = part_m + bh * nch;
     const float* pl = part_l + bh * nch;
     const float* po = part_o + bh * nch * HD + d;
-    float M = -INFINITY;
-#pragma unroll 8
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, pm[c]);
-    float l = 0.f, o = 0.f;
-#pragma unroll 8
-    for (int c = 0; c < nch; ++c) {
-        const float mc = pm[c];
-        const float wgt = mc == -INFINITY ? 0.f : __expf(mc - M);
-        l += pl[c] * wgt;
-        o += po[(size_t)c * HD] * wgt;
+    float M = -INFINITY, l = 0.f, o = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += MAXCH) {
+        float mv[MAXCH], lv[MAXCH], ov[MAXCH];
+#pragma unroll
+        for (int c = 0; c < MAXCH; ++c) {
+            const int cc = min(c0 + c, nch - 1);
+            mv[c] = pm[cc];
+            lv[c] = pl[cc];
+            ov[c] = po[(size_t)cc * HD];
+        }
+        float Mn = M;
+#pragma unroll
+        for (int c = 0; c < MAXCH; ++c) Mn = c0 + c < nch ? fmaxf(Mn, mv[c]) : Mn;
+        if (Mn == -INFINITY) continue;  // nothing live yet
+        const float r = M == -INFINITY ? 0.f : __expf(M - Mn);
+        l *= r;
+        o *= r;
+#pragma unroll
+        for (int c = 0; c < MAXCH; ++c) {
+            const float wgt = (c0 + c >= nch || mv[c] == -INFINITY) ? 0.f : __expf(mv[c] - Mn);
+            l += lv[c] * wgt;
+            o += ov[c] * wgt;
+        }
+        M = Mn;
     }
     out[bh * HD + d] = (f16)(o / l);
 }
@@ -591,32 +648,39 @@ hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* ou
     return hipGetLastError();
 }
 
-// positions per decode chunk block
-constexpr int DCH_DEFAULT = 128;
-
-int attn_decode_chunks(int ctx) { return (ctx + DCH_DEFAULT - 1) / DCH_DEFAULT; }
+// Small batches: chunks of ATTN_DEC_CHUNK positions over the whole cache
+// (ceil(ctx / ATTN_DEC_CHUNK) blocks per (head, sequence), those past the
+// current position exit at once).  Once B * H blocks fill the chip: one
+// chunk per (head, sequence).  Measured at 7B, ctx 2176: B 1 7.3 us +
+// 3.5 us merge (128-position chunks; 8 or 16 whole-context chunks took
+// 9.2 - 9.6 us), B 16 86 us (one chunk) vs 91 (128-position chunks).
+int attn_decode_chunks(int B, int H, int ctx) {
+    return B * H >= 256 ? 1 : (ctx + ATTN_DEC_CHUNK - 1) / ATTN_DEC_CHUNK;
+}
 
 hipError_t launch_attn_decode(const f16* q, const f16* k, const f16* v, const int* pos,
                               float* part_m, float* part_l, float* part_o, f16* out, int B, int H,
-                              int hd, int ctx, hipStream_t st, int dch) {
-    if (dch == 0) dch = DCH_DEFAULT;
-    const int nch = (ctx + dch - 1) / dch;
+                              int hd, int ctx, hipStream_t st, int nch) {
+    if (B < 1 || H < 1 || ctx < 1) return hipErrorInvalidValue;
+    int per = 0;  // whole context split over nch chunks (forced nch: tuning)
+    if (nch <= 0) {
+        nch = attn_decode_chunks(B, H, ctx);
+        if (nch > 1) per = ATTN_DEC_CHUNK;
+    }
     const dim3 grid(nch, H, B);
     const float scale = 1.0f / sqrtf((float)hd);
-#define RH_ATTN_DEC(HD_, DCH_)                                                                     \
-    hipLaunchKernelGGL((attn_decode_kernel<HD_, DCH_>), grid, dim3(256), 0, st, q, k, v, pos, part_m, \
-                       part_l, part_o, H, ctx, scale)
-    if (hd == 128 && dch == 64) RH_ATTN_DEC(128, 64);
-    else if (hd == 128 && dch == 128) RH_ATTN_DEC(128, 128);
-    else if (hd == 128 && dch == 256) RH_ATTN_DEC(128, 256);
-    else if (hd == 64 && dch == 64) RH_ATTN_DEC(64, 64);
-    else if (hd == 64 && dch == 128) RH_ATTN_DEC(64, 128);
-    else return hipErrorInvalidValue;
-#undef RH_ATTN_DEC
+    if (hd == 128)
+        hipLaunchKernelGGL((attn_decode_kernel<128, 8>), grid, dim3(256), 0, st, q, k, v, pos, part_m, part_l,
+                           part_o, out, H, ctx, per, scale);
+    else if (hd == 64)
+        hipLaunchKernelGGL((attn_decode_kernel<64, 4>), grid, dim3(256), 0, st, q, k, v, pos, part_m, part_l,
+                           part_o, out, H, ctx, per, scale);
+    else
+        return hipErrorInvalidValue;
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(H, B), dim3(hd), 0, st, part_m, part_l, part_o, out,
-                       H, hd, nch);
+    if (e != hipSuccess || nch == 1) return e;
+    hipLaunchKernelGGL((attn_merge_kernel<16>), dim3(H, B), dim3(hd), 0, st, part_m, part_l, part_o, out, H, hd,
+                       nch);
     return hipGetLastError();
 }
 

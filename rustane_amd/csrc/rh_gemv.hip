@@ -64,7 +64,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int t = 0; t < RT; ++t)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) wr[t][u] = *(const f16x8*)(wp[t] + c * 2048 + 512 * u);
+            for (int u = 0; u < 4; ++u) wr[t][u] = ld_stream((const f16x8*)(wp[t] + c * 2048 + 512 * u));
     };
     auto xload = [&](int i, f16x8 (&xr)[4]) {
         const int off = min(w + i * NW, nch - 1) * 128;
@@ -306,14 +306,16 @@ hipError_t launch_variant(int v, const GemvArgs& a, int nblk, hipStream_t st) {
 }
 
 // Default variant per shape, from sweeps of the 7B decode shapes on MI355X
-// with fragment-ordered weights streamed from HBM (footprint > 2 GiB):
-// SwiGLU pair rows 8 waves x 2 deep; long rows (K 11008) 4 x 2; 16 tokens
-// 8 x 2; otherwise 4 waves, 4 deep for the tall matrices.
+// with fragment-ordered weights streamed from HBM by nontemporal loads
+// (footprint > 2 GiB): 4 waves x 2 deep everywhere except the tall
+// matrices at few tokens (QKV, logits: 8 x 2) and the SwiGLU pair rows at
+// 16 tokens (8 x 2).  B 1: QKV 17.8 us, W1|W3 29.1, W2 15.4, Wo 7.3,
+// logits 40.1 (5.5 - 6.5 TB/s).
 int pick_variant(int epi, const GemvArgs& a) {
-    if (epi == GV_SWIGLU) return 4;
+    if (epi == GV_SWIGLU) return a.B > 4 ? 4 : 1;
     if (a.K > 4096) return 1;
-    if (a.B >= 8) return 4;
-    return a.N >= 8192 ? 3 : 1;
+    if (a.N >= 8192) return a.B >= 8 ? 1 : 4;
+    return 1;
 }
 
 }  // namespace

@@ -86,13 +86,16 @@ hipError_t launch_gemm_resid_norm(const GemmArgs& a, const float* gamma, float e
 hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* out, int B, int H,
                                int S, int hd, int ctx, hipStream_t st, float* lse = nullptr);
 // Decode attention over positions 0..*pos (the current token is at *pos):
-// q [B][H*hd]; per (b, h, chunk) partial (m, l, o[hd]), then a merge kernel.
-// Partial buffers hold B*H*attn_decode_chunks(ctx) entries; dch (positions per
-// chunk, 0 = default) is for tuning and must not exceed those buffers.
+// q [B][H*hd], K/V caches [B][H][ctx][hd], out [B][H*hd] fp16.  The cache is
+// split into nch = attn_decode_chunks(B, H, ctx) chunks per (b, h) (a
+// positive nch forces that many equal chunks: tuning); with more than one,
+// per-chunk partials (m, l, o[hd]) go to part_* ([B][H][nch] entries) and a
+// merge kernel writes out.
+constexpr int ATTN_DEC_CHUNK = 128;
 hipError_t launch_attn_decode(const f16* q, const f16* k, const f16* v, const int* pos,
                               float* part_m, float* part_l, float* part_o, f16* out, int B, int H,
-                              int hd, int ctx, hipStream_t st, int dch = 0);
-int attn_decode_chunks(int ctx);
+                              int hd, int ctx, hipStream_t st, int nch = 0);
+int attn_decode_chunks(int B, int H, int ctx);
 
 // ---------------- decode GEMV (B <= 16 tokens) ----------------
 enum GemvEpi { GV_F32 = 0, GV_RESID = 1, GV_SWIGLU = 2, GV_QKV = 3 };

@@ -40,7 +40,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 size_t layout(const rh_ctx* ctx, int B, bool own_logits, unsigned char* base, rhrt::DecodeBufs* b) {
     const rh_config& c = ctx->cfg;
     const size_t D = c.dim, F = c.hidden, V = c.vocab;
-    const size_t nch = (size_t)rh::attn_decode_chunks(ctx->max_ctx);
+    const size_t nch = (size_t)rh::attn_decode_chunks(B, c.heads, ctx->max_ctx);
     const size_t part = (size_t)B * c.heads * nch;
     const size_t am = (size_t)rh::gemv_argmax_blocks(c.vocab) * 16;
     size_t off = 0;

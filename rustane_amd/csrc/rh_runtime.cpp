@@ -476,7 +476,7 @@ int rh_create(const rh_config* cfg, int device, int max_batch, int max_ctx, rh_c
     if (max_ctx > 0) {
         const int Bd = std::min(max_batch, 16);
         ctx->kv_layer = (size_t)max_batch * c.heads * (size_t)max_ctx * c.head_dim;
-        const int nch = rh::attn_decode_chunks(max_ctx);
+        const int nch = rh::attn_decode_chunks(1, c.heads, max_ctx);  // decode attention partials per (sequence, head)
         if ((rc = dalloc(ctx, &ctx->kcache, ctx->kv_layer * c.nlayers)) ||
             (rc = dalloc(ctx, &ctx->vcache, ctx->kv_layer * c.nlayers)) ||
             (rc = dalloc(ctx, &ctx->dx, 16 * D)) || (rc = dalloc(ctx, &ctx->dxn, 16 * D)) ||
