@@ -424,6 +424,21 @@ def measured_traffic(config, batch, seq):
         return None
 
 
+def measured_decode_traffic(config, batch, ctx_start, mean_ctx):
+    """HBM bytes per decode step at the run's mean context from the rocprofv3
+    counter passes recorded in profiles/ (null when that workload has not
+    been profiled)."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "decode_traffic.json")) as f:
+            rec = json.load(f).get(f"{config}_b{batch}_ctx{ctx_start}")
+    except (OSError, ValueError):
+        return None
+    if not rec:
+        return None
+    pts = sorted((float(c), v) for c, v in rec["per_step_bytes_at_ctx"].items())
+    return int(round(float(np.interp(mean_ctx, [c for c, _ in pts], [v for _, v in pts]))))
+
+
 def run_decode(ctx, cfg, args, hb, E, hip_rt, stream, batch=None):
     B = batch or args.decode_batch
     ctx.set_graphs(not args.decode_eager)
@@ -462,7 +477,10 @@ def run_decode(ctx, cfg, args, hb, E, hip_rt, stream, batch=None):
         "batch": B, "ctx_start": args.decode_ctx, "steps": args.decode_steps,
         "bytes_per_step": by["total"],
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": measured_decode_traffic(args.config, B, args.decode_ctx, mean_ctx),
+                     "traffic_source": "rocprofv3 FETCH_SIZE/WRITE_SIZE per decode kernel, summed over one step, "
+                                       "recorded in profiles/decode_traffic.json"},
         "gemv_w13": {"bytes_per_launch": w13_bytes,
                      "mean_launch_us": round((k_ms / k_n) * 1e3, 2) if k_n else None,
                      "achieved_gbs": round(w13_gbs, 1) if w13_gbs else None},

@@ -679,7 +679,8 @@ hipError_t launch_attn_decode(const f16* q, const f16* k, const f16* v, const in
         return hipErrorInvalidValue;
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || nch == 1) return e;
-    hipLaunchKernelGGL((attn_merge_kernel<16>), dim3(H, B), dim3(hd), 0, st, part_m, part_l, part_o, out, H, hd,
+    // one round of loads covers contexts up to 32 * ATTN_DEC_CHUNK positions
+    hipLaunchKernelGGL((attn_merge_kernel<32>), dim3(H, B), dim3(hd), 0, st, part_m, part_l, part_o, out, H, hd,
                        nch);
     return hipGetLastError();
 }
