@@ -257,19 +257,28 @@ __device__ __forceinline__ void wait_vm() {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-template <int NS>
-__global__ __launch_bounds__(256) void attn_prefill_dma_kernel(const f16* __restrict__ Q,
-                                                               const f16* __restrict__ Kc,
-                                                               const f16* __restrict__ Vc,
-                                                               f16* __restrict__ out, float* __restrict__ lse,
-                                                               int H, int S, int ctx, float scale_log2) {
+// NG = 2: two groups of 4 waves share the block's 64 queries and split its
+// key blocks (group G takes blocks G, G + 2, ...), each through its own half
+// of every stage's LDS arrays; the groups step in lockstep under the block's
+// barrier (a group without a block in the last step only joins the barrier)
+// and group 1 hands its (m, l, o) to group 0 through LDS at the end.  This
+// halves the serial key-block chain of the heavy (late) query tiles, which
+// sets the kernel time when there are few (sequence, head) pairs.
+template <int NS, int NG>
+__global__ __launch_bounds__(256 * NG) void attn_prefill_dma_kernel(const f16* __restrict__ Q,
+                                                                    const f16* __restrict__ Kc,
+                                                                    const f16* __restrict__ Vc,
+                                                                    f16* __restrict__ out, float* __restrict__ lse,
+                                                                    int H, int S, int ctx, float scale_log2) {
     constexpr int HD = 128, KB = 64, NKK = HD / 32, NHT = HD / 16;
     constexpr int TILE = KB * HD;  // halves of one K or V block (16 KB)
     static_assert(NS == 2 || NS == 3, "2 or 3 stages");
+    static_assert(NG == 1 || (NG == 2 && NS == 2), "two groups run the 2-stage pipeline");
     // one LDS array per stage and operand: the compiler's wait-count pass then
     // knows a stage's reads do not alias the DMA filling another stage (one
     // array would make it drain every DMA before the first read)
-    __shared__ __attribute__((aligned(1024))) f16 sK0[TILE], sV0[TILE], sK1[TILE], sV1[TILE], sK2[TILE], sV2[TILE];
+    __shared__ __attribute__((aligned(1024))) f16 sK0[NG * TILE], sV0[NG * TILE], sK1[NG * TILE], sV1[NG * TILE],
+        sK2[TILE], sV2[TILE];
     auto kbuf = [&](auto I) -> f16* {
         if constexpr (decltype(I)::value == 0) return sK0;
         else if constexpr (decltype(I)::value == 1) return sK1;
@@ -281,7 +290,8 @@ __global__ __launch_bounds__(256) void attn_prefill_dma_kernel(const f16* __rest
         else return sV2;
     };
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r = lane & 15;
+    const int w = (tid >> 6) & 3, grp = NG == 1 ? 0 : tid >> 8;  // wave within its group, group
     const int nqt = (S + 63) / 64;
     // 1-D grid: the query tiles of one (sequence, head) are consecutive
     // logical tiles, which xcd_remap puts on one XCD, so that XCD's L2 serves
@@ -316,8 +326,8 @@ __global__ __launch_bounds__(256) void attn_prefill_dma_kernel(const f16* __rest
     // last row (masked below).
     auto issue = [&](int kb, auto ST) {
         const int k0 = kb * KB;
-        f16* dk = kbuf(ST);
-        f16* dv = vbuf(ST);
+        f16* dk = kbuf(ST) + grp * TILE;
+        f16* dv = vbuf(ST) + grp * TILE;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int i = w + 4 * t, row = 4 * i + (lane >> 4);
@@ -328,11 +338,12 @@ __global__ __launch_bounds__(256) void attn_prefill_dma_kernel(const f16* __rest
                                              (__attribute__((address_space(3))) void*)(dv + i * 512), 16, 0, 0);
         }
     };
-    issue(0, std::integral_constant<int, 0>{});  // nkb >= 1
+    if (grp < nkb) issue(grp, std::integral_constant<int, 0>{});  // nkb >= 1
     if constexpr (NS == 3)
         if (nkb > 1) issue(1, std::integral_constant<int, 1>{});
 
-    // one key block on stage ST (a compile-time buffer choice)
+    // one key block on stage ST (a compile-time buffer choice); with two
+    // groups, kb is this group's block (kb >= nkb: a barrier-only step)
     auto step = [&](int kb, auto ST) {
         constexpr int cur = decltype(ST)::value;
         const int k0 = kb * KB;
@@ -345,9 +356,10 @@ __global__ __launch_bounds__(256) void attn_prefill_dma_kernel(const f16* __rest
         else if (ahead == 1) wait_vm<8>();
         else wait_vm<0>();
         lds_barrier();
-        if (kb + NS - 1 < nkb) issue(kb + NS - 1, std::integral_constant<int, (cur + NS - 1) % NS>{});
-        const f16* sK = kbuf(ST);
-        const f16* sV = vbuf(ST);
+        if (kb + NG * (NS - 1) < nkb) issue(kb + NG * (NS - 1), std::integral_constant<int, (cur + NS - 1) % NS>{});
+        if (NG > 1 && kb >= nkb) return;  // group-uniform
+        const f16* sK = kbuf(ST) + grp * TILE;
+        const f16* sV = vbuf(ST) + grp * TILE;
 
         f16x8 kf[2][2][NKK];
 #pragma unroll
@@ -435,11 +447,44 @@ __global__ __launch_bounds__(256) void attn_prefill_dma_kernel(const f16* __rest
 #pragma unroll
             for (int j = 0; j < NHT; ++j) o[j] = mfma16(vf[c][j], pf[c], o[j]);
     };
-    for (int kb0 = 0; kb0 < nkb; kb0 += NS) {
-        step(kb0, std::integral_constant<int, 0>{});
-        if (kb0 + 1 < nkb) step(kb0 + 1, std::integral_constant<int, 1>{});
-        if constexpr (NS == 3)
-            if (kb0 + 2 < nkb) step(kb0 + 2, std::integral_constant<int, 2>{});
+    if constexpr (NG == 1) {
+        for (int kb0 = 0; kb0 < nkb; kb0 += NS) {
+            step(kb0, std::integral_constant<int, 0>{});
+            if (kb0 + 1 < nkb) step(kb0 + 1, std::integral_constant<int, 1>{});
+            if constexpr (NS == 3)
+                if (kb0 + 2 < nkb) step(kb0 + 2, std::integral_constant<int, 2>{});
+        }
+    } else {
+        // both groups take ceil(nkb / 2) steps (block-uniform count)
+        const int nst = (nkb + 1) / 2;
+        for (int s0 = 0; s0 < nst; s0 += 2) {
+            step(2 * s0 + grp, std::integral_constant<int, 0>{});
+            if (s0 + 1 < nst) step(2 * (s0 + 1) + grp, std::integral_constant<int, 1>{});
+        }
+        // group 1 hands (m, l, o) to group 0 through the (now idle) stage buffers
+        lds_barrier();
+        float* xo = (float*)sK0;  // [4 waves][32 values][64 lanes]: 32 KB
+        float* xm = (float*)sV0;  // [4 waves][2][64 lanes]
+        if (grp == 1) {
+#pragma unroll
+            for (int j = 0; j < NHT; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xo[(w * 32 + 4 * j + e) * 64 + lane] = o[j][e];
+            xm[(w * 2) * 64 + lane] = m_run;
+            xm[(w * 2 + 1) * 64 + lane] = l_run;
+        }
+        lds_barrier();
+        if (grp == 1) return;
+        const float m1 = xm[(w * 2) * 64 + lane], l1 = xm[(w * 2 + 1) * 64 + lane];
+        const float mm = fmaxf(m_run, m1);
+        const float c0 = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - mm);
+        const float c1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
+        l_run = l_run * c0 + l1 * c1;
+#pragma unroll
+        for (int j = 0; j < NHT; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[j][e] = o[j][e] * c0 + xo[(w * 32 + 4 * j + e) * 64 + lane] * c1;
+        m_run = mm;
     }
     float lt = l_run + __shfl_xor(l_run, 16, RH_WAVE);
     lt += __shfl_xor(lt, 32, RH_WAVE);
@@ -631,6 +676,13 @@ __global__ void attn_merge_kernel(const float* part_m, const float* part_l, cons
 
 }  // namespace
 
+// Two key-splitting wave groups per block while the grid is at most about
+// two blocks per CU, where the heaviest query tile's serial chain sets the
+// time; one group (two blocks per CU) once the grid is larger.
+int attn_prefill_groups(int B, int H, int S) {
+    return (long long)B * H * ((S + 63) / 64) <= 512 ? 2 : 1;
+}
+
 hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* out, int B, int H,
                                int S, int hd, int ctx, hipStream_t st, float* lse) {
     const dim3 grid((S + 63) / 64, H, B);
@@ -638,9 +690,12 @@ hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* ou
     constexpr int PF = 1;  // deeper register prefetch measured no faster
     // hd 128: DMA pipeline with 2 stages (64 KB of LDS, two blocks per CU; 3
     // stages measured slower at every shape for the lost occupancy)
-    if (hd == 128)
-        hipLaunchKernelGGL((attn_prefill_dma_kernel<2>), dim3((S + 63) / 64 * H * B), dim3(256), 0, st, q, k, v, out,
-                           lse, H, S, ctx, sl2);
+    if (hd == 128 && attn_prefill_groups(B, H, S) == 2)
+        hipLaunchKernelGGL((attn_prefill_dma_kernel<2, 2>), dim3((S + 63) / 64 * H * B), dim3(512), 0, st, q, k, v,
+                           out, lse, H, S, ctx, sl2);
+    else if (hd == 128)
+        hipLaunchKernelGGL((attn_prefill_dma_kernel<2, 1>), dim3((S + 63) / 64 * H * B), dim3(256), 0, st, q, k, v,
+                           out, lse, H, S, ctx, sl2);
     else if (hd == 64)
         hipLaunchKernelGGL((attn_prefill_kernel<64, PF>), grid, dim3(256), 0, st, q, k, v, out, lse, H, S, ctx, sl2);
     else
