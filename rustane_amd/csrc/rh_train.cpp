@@ -278,17 +278,26 @@ int gamma_grad(rh_ctx* ctx, int nblk, int D, float kappa, float* dgamma) {
 // C[rows][cols] += kappa * X W^T with X [rows][Mp], W [cols][Mp] (token-inner).
 // When every gradient is still zero the epilogue stores kappa * acc instead
 // (the same values; it skips reading the fp32 gradient back).  K is the
-// token count.  Below 2048 tokens it is short next to the fp32 output these
-// GEMMs write, so they use 192x128 tiles, whose 80 KB of LDS lets two blocks
-// share a CU and one's epilogue stores overlap the other's MFMAs (measured at
-// 7B: 40.4 vs 44.1 ms per B1 step with the 256x256 tiles the FLOP model
-// picks); from 2048 tokens on the model's larger tiles are faster (4096 x
-// 11008 at K 2048: 198 vs 235 us).
+// token count, short next to the fp32 output these GEMMs write, so the tile
+// is picked from MI355X timings at K = 512 / 2048 / 8192 (store | accumulate
+// epilogue, us) rather than by the FLOP model:
+//   4096 x 4096:  256x128 8-wave 29.6 | 39.1, 73.7 | 79.1  (192x128 4-wave
+//                 34 | 55, 84 | 97); at K 8192 the model's pick, 280 | 297
+//   4096 x 11008: 192x256 8-wave 80 | 105, 220 | 242, 744 | 790  (192x128
+//                 4-wave 88 | 124, 263 | 278)
+//   32000 x 4096 (tied embedding): 192x256 256 | 364, 694 | 772; at K 8192
+//                 256x128 2079 | 2164
 int grad_gemm(rh_ctx* ctx, const f16* X, const f16* W, int rows, int cols, float kappa, float* out) {
     rh::GemmArgs g{};
     g.X = X; g.W = W; g.M = rows; g.N = cols; g.K = ctx->train->Mp;
     g.out_f32 = out; g.ldo = cols; g.alpha = kappa;
-    g.force_cfg = g.K < 2048 ? rh::GCFG_D4_192x128 : rh::GCFG_AUTO;
+    const bool long_k = g.K >= 8192;
+    if (cols > 4096)
+        g.force_cfg = rh::GCFG_D8_192x256;
+    else if (rows > 4096)
+        g.force_cfg = long_k ? rh::GCFG_D8_256x128 : rh::GCFG_D8_192x256;
+    else
+        g.force_cfg = long_k ? rh::GCFG_AUTO : rh::GCFG_D8_256x128;
     set_sk(ctx, g);
     LCK(rh::launch_gemm(ctx->train->zero ? rh::EPI_F32 : rh::EPI_RESID, g, ctx->stream));
     return RH_OK;
