@@ -75,10 +75,15 @@ def main():
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode with eager launches instead of graph replay (profilers that "
                          "cannot follow graph capture)")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="only time hipBLASLt (torch.mm) at the 7B batch-1 prefill GEMM shapes, for reference")
     ap.add_argument("--no-graphs", action="store_true",
                     help="eager launches everywhere, prefill included (profilers that cannot follow "
                          "graph capture)")
     args = ap.parse_args()
+    if args.vendor_gemm:
+        print(json.dumps({"vendor_gemm": run_vendor_gemm()}), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
               "(multi-GPU sharding is design-only).", file=sys.stderr)
@@ -644,6 +649,40 @@ def cpu_baseline_decode(cfg, args, steps=4):
                       f"1 and 2 layers (1 warm-up step, median of {steps - 1}: {step_s[1] * 1e3:.1f} ms, "
                       f"{step_s[2] * 1e3:.1f} ms), extrapolated linearly to {cfg.nlayers} layers "
                       f"({t_step * 1e3:.0f} ms per token)"}
+
+
+def run_vendor_gemm(iters=30):
+    """hipBLASLt through torch.mm at the 7B batch-1 prefill GEMM shapes (M = 512
+    tokens, fp16 operands, fp16 output, weights [N, K] as the library stores
+    them), each weight rotated over more than 1 GiB of copies so every launch
+    reads it from HBM past the 256 MB last-level cache, as the forward does.
+    A reference point for the library's GEMMs, which also fuse their
+    epilogues (RoPE and the cache scatter, SwiGLU, residual + RMSNorm)."""
+    import torch
+    shapes = {"QKV": (512, 12288, 4096), "W1|W3": (512, 22016, 4096), "W2": (512, 4096, 11008),
+              "Wo": (512, 4096, 4096), "logits": (512, 32000, 4096)}
+    out = {}
+    for name, (M, N, K) in shapes.items():
+        g = torch.Generator(device="cuda").manual_seed(5)
+        a = torch.randn(M, K, device="cuda", dtype=torch.float16, generator=g)
+        nrot = (1 << 30) // (N * K * 2) + 2
+        ws = [torch.randn(N, K, device="cuda", dtype=torch.float16, generator=g) for _ in range(nrot)]
+        for w in ws[:2]:
+            torch.mm(a, w.t())
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(iters):
+            torch.mm(a, ws[i % nrot].t())
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / iters
+        tf = 2.0 * M * N * K / us / 1e6
+        out[name] = {"M": M, "N": N, "K": K, "us": round(us, 2), "tflops": round(tf, 1),
+                     "mfma_frac": round(tf / PEAK_FP16_TFLOPS, 4)}
+        log(f"[bench] hipBLASLt {name} {M}x{N}x{K}: {us:.2f} us, {tf:.0f} TFLOP/s")
+        del ws
+    return out
 
 
 if __name__ == "__main__":
