@@ -266,8 +266,9 @@ void rh_train_config_default(rh_train_config* out);
 /* learning_rate (full_model.rs:903-913): linear warmup, cosine decay to
  * max_lr * min_lr_frac. */
 float rh_learning_rate(uint32_t step, const rh_train_config* tc);
-/* grad_norm (full_model.rs:1403-1450): L2 norm of all gradients (per-tensor
- * sums of squares added in double; 0 while the gradients are zero). */
+/* grad_norm (full_model.rs:1403-1450): L2 norm of all gradients (per-block
+ * fp32 sums of squares of every tensor, added in double on the device; 0
+ * while the gradients are zero). */
 int rh_grad_norm(rh_ctx* ctx, float* norm_out);
 /* update_weights (full_model.rs:1123-1400): one AdamW step_fused
  * (cpu/adam.rs:95-132) at step count t >= 1 over every parameter, gradients

@@ -211,6 +211,8 @@ hipError_t launch_adam_transpose(float* p, const float* g, float* m, float* v, i
 // Per-block sums of squares of x[0..n) into part[0..sumsq_blocks(n)).
 int sumsq_blocks(size_t n);
 hipError_t launch_sumsq(const float* x, size_t n, float* part, hipStream_t st);
+// *out = the sum of part[0..n) in double (one block; a fixed order).
+hipError_t launch_sum_parts(const float* part, size_t n, double* out, hipStream_t st);
 
 // ---------------- weight packing ----------------
 // Device weights are fp16 [N, K] in fragment order (frag_off in rh_device.h),

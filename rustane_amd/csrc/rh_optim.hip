@@ -128,6 +128,22 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ x,
     if (threadIdx.x == 0) part[blockIdx.x] = t;
 }
 
+// One block: the sum of part[0..n) in double (each thread a strided run,
+// then a fixed tree), written to *out.
+__global__ __launch_bounds__(1024) void sum_parts_kernel(const float* __restrict__ part, size_t n,
+                                                         double* __restrict__ out) {
+    __shared__ double red[1024];
+    double s = 0.0;
+    for (size_t i = threadIdx.x; i < n; i += 1024) s += (double)part[i];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 512; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *out = red[0];
+}
+
 int grid_for(size_t n, int per) {
     const size_t g = (n + per - 1) / per;
     return (int)(g > 16384 ? 16384 : (g ? g : 1));
@@ -152,6 +168,12 @@ hipError_t launch_adam_transpose(float* p, const float* g, float* m, float* v, i
 }
 
 int sumsq_blocks(size_t n) { return (int)std::min<size_t>(2048, (n + 8191) / 8192); }
+
+hipError_t launch_sum_parts(const float* part, size_t n, double* out, hipStream_t st) {
+    if (n == 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(sum_parts_kernel, dim3(1), dim3(1024), 0, st, part, n, out);
+    return hipGetLastError();
+}
 
 hipError_t launch_sumsq(const float* x, size_t n, float* part, hipStream_t st) {
     if (n % 4 != 0 || n == 0) return hipErrorInvalidValue;

@@ -67,6 +67,7 @@ struct TrainState {
         float *emb_m = nullptr, *emb_v = nullptr, *gf_m = nullptr, *gf_v = nullptr;
         std::vector<std::array<float*, 9>> m, v;
         float* part = nullptr;  // sum-of-squares partials of the gradient norm
+        double* sumsq = nullptr;  // their sum
     };
     Opt* opt = nullptr;
     ~TrainState() { delete opt; }
@@ -457,6 +458,7 @@ int ensure_opt(rh_ctx* ctx) {
                 nparts += rh::sumsq_blocks(sz[j]);
             }
         RCK(dalloc(ctx, &o->part, nparts));
+        RCK(dalloc(ctx, &o->sumsq, 1));
         o->moments = true;
         RCK(zero_moments(ctx));
     }
@@ -520,23 +522,16 @@ int rh_grad_norm(rh_ctx* ctx, float* norm_out) {
     std::vector<std::pair<const float*, size_t>> ts{{T->dembed, (size_t)c.vocab * c.dim}, {T->dgf, (size_t)c.dim}};
     for (int l = 0; l < c.nlayers; ++l)
         for (int j = 0; j < 9; ++j) ts.emplace_back(T->dlay[l][j], sz[j]);
-    std::vector<int> nb;
+    // per-block partials of every tensor, then their sum in double on the device
     size_t off = 0;
     for (auto& t : ts) {
         LCK(rh::launch_sumsq(t.first, t.second, T->opt->part + off, st));
-        nb.push_back(rh::sumsq_blocks(t.second));
-        off += nb.back();
+        off += rh::sumsq_blocks(t.second);
     }
-    std::vector<float> part(off);
-    HCK(hipMemcpyAsync(part.data(), T->opt->part, off * sizeof(float), hipMemcpyDeviceToHost, st));
-    HCK(hipStreamSynchronize(st));
+    LCK(rh::launch_sum_parts(T->opt->part, off, T->opt->sumsq, st));
     double total = 0.0;
-    size_t k = 0;
-    for (int n : nb) {
-        double s = 0.0;
-        for (int i = 0; i < n; ++i) s += part[k++];
-        total += s;
-    }
+    HCK(hipMemcpyAsync(&total, T->opt->sumsq, sizeof(double), hipMemcpyDeviceToHost, st));
+    HCK(hipStreamSynchronize(st));
     *norm_out = (float)std::sqrt(total);
     return RH_OK;
 }
