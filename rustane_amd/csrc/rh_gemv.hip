@@ -188,9 +188,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
                     const int oi = __shfl_xor(bi, o, RH_WAVE);
                     if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
                 }
-                if (g == 0 && xvalid) {
-                    a.am_val[(size_t)blockIdx.x * 16 + tok] = bv;
-                    a.am_idx[(size_t)blockIdx.x * 16 + tok] = bi;
+                if (g == 0 && xvalid) {  // token-major, so each token's reduction reads contiguously
+                    a.am_val[(size_t)tok * gridDim.x + blockIdx.x] = bv;
+                    a.am_idx[(size_t)tok * gridDim.x + blockIdx.x] = bi;
                 }
             }
         } else if constexpr (EPI == GV_RESID) {
@@ -222,9 +222,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
     }
 }
 
-// Reduce the per-block (value, index) partials of the logits GEMV; ties ->
-// lowest index.  16 waves: 16/B per token (B <= 16), each strided over the
-// partials with 4 loads in flight, then the token's waves merge through LDS.
+// Reduce the per-block (value, index) partials of the logits GEMV ([B][nblk],
+// token-major); ties -> lowest index.  16 waves: 16/B per token (B <= 16),
+// each strided over its token's partials with 8 coalesced loads of each
+// array in flight, then the token's waves merge through LDS.
 // Writes out[b], next_in[b] and seq_out[state[1] * B + b]; then (advance)
 // state[0] += 1, state[1] += 1.
 __global__ __launch_bounds__(1024) void argmax_final_kernel(const float* pv, const int* pi, int nblk,
@@ -243,18 +244,20 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(const float* pv, con
     if (b < B) {
         const int step = wpt * 64;
         int p = sub * 64 + lane;
-        for (; p + 3 * step < nblk; p += 4 * step) {
-            float v[4];
-            int ix[4];
+        const float* tv = pv + (size_t)b * nblk;
+        const int* ti = pi + (size_t)b * nblk;
+        for (; p + 7 * step < nblk; p += 8 * step) {
+            float v[8];
+            int ix[8];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                v[q] = pv[(size_t)(p + q * step) * 16 + b];
-                ix[q] = pi[(size_t)(p + q * step) * 16 + b];
+            for (int q = 0; q < 8; ++q) {
+                v[q] = tv[p + q * step];
+                ix[q] = ti[p + q * step];
             }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) take(v[q], ix[q]);
+            for (int q = 0; q < 8; ++q) take(v[q], ix[q]);
         }
-        for (; p < nblk; p += step) take(pv[(size_t)p * 16 + b], pi[(size_t)p * 16 + b]);
+        for (; p < nblk; p += step) take(tv[p], ti[p]);
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) take(__shfl_xor(bv, o, RH_WAVE), __shfl_xor(bi, o, RH_WAVE));
         if (lane == 0) { sv[w] = bv; si[w] = bi; }

@@ -111,7 +111,7 @@ struct GemvArgs {
     const float2* rope;
     const int* pos;    // device position
     int D, H, hd, ctx;
-    // GV_F32 only (optional): per-block argmax partials [gemv_argmax_blocks(N)][16]
+    // GV_F32 only (optional): per-block argmax partials [B][gemv_argmax_blocks(N)]
     float* am_val;
     int* am_idx;
     int cfg;           // 0 = default (waves, depth) variant; 1..gemv_num_variants() forces one
