@@ -52,7 +52,15 @@ struct TrainState {
     float* xlast = nullptr;  // residual after the last layer
     f16* xf = nullptr;       // final RMSNorm rows (fragment order)
     // backward workspace
-    f16 *dlh = nullptr, *dlT = nullptr, *H1 = nullptr, *H2 = nullptr, *T1 = nullptr, *T2 = nullptr, *T3 = nullptr;
+    f16 *dlh = nullptr, *dlT = nullptr, *H1 = nullptr, *H2 = nullptr;
+    // Token-inner copies of the weight-gradient GEMMs' operands, one pair per
+    // group of those GEMMs in a layer (0: dW2, 1: dW1 dW3, 2: dWo, 3: dWq dWk
+    // dWv), so a group runs on the side stream while the main stream goes on
+    // to the data gradients and the next group's copies: made[g] (main) says
+    // group g's copies are written, used[g] (side) that its GEMMs have read them.
+    f16* tx[4][2] = {};
+    hipStream_t side = nullptr;
+    hipEvent_t made[4] = {}, used[4] = {};
     f16* dOh = nullptr;
     float *gout = nullptr, *dres = nullptr, *Drow = nullptr, *dgp = nullptr;
     uint32_t* utok = nullptr;
@@ -70,7 +78,17 @@ struct TrainState {
         double* sumsq = nullptr;  // their sum
     };
     Opt* opt = nullptr;
-    ~TrainState() { delete opt; }
+    ~TrainState() {
+        if (side) {
+            (void)hipStreamSynchronize(side);
+            (void)hipStreamDestroy(side);
+        }
+        for (int g = 0; g < 4; ++g) {
+            if (made[g]) (void)hipEventDestroy(made[g]);
+            if (used[g]) (void)hipEventDestroy(used[g]);
+        }
+        delete opt;
+    }
 };
 
 void train_state_free(TrainState* t) { delete t; }
@@ -120,6 +138,13 @@ int ensure_train_static(rh_ctx* ctx) {
     if (T->dembed) return RH_OK;
     const rh_config& c = ctx->cfg;
     const size_t D = c.dim, F = c.hidden, V = c.vocab, Vp = round_up(V, 128);
+    if (!T->side) {  // the weight-gradient GEMMs' stream (default priority, like the context's)
+        HCK(hipStreamCreateWithFlags(&T->side, hipStreamNonBlocking));
+        for (int g = 0; g < 4; ++g) {
+            HCK(hipEventCreateWithFlags(&T->made[g], hipEventDisableTiming));
+            HCK(hipEventCreateWithFlags(&T->used[g], hipEventDisableTiming));
+        }
+    }
     RCK(dalloc(ctx, &T->dembed, V * D));
     RCK(dalloc(ctx, &T->dgf, D));
     T->dlay.resize(c.nlayers);
@@ -154,9 +179,14 @@ int ensure_train_ws(rh_ctx* ctx, int B, int S) {
         for (void* p : ps) dfree(ctx, p);
     }
     {
-        void* ps[] = {T->xlast, T->xf, T->dlh, T->dlT, T->H1, T->H2, T->T1, T->T2, T->T3, T->dOh,
+        void* ps[] = {T->xlast, T->xf, T->dlh, T->dlT, T->H1, T->H2, T->dOh,
                       T->gout, T->dres, T->Drow, T->dgp, T->utok, T->ustart, T->uidx};
         for (void* p : ps) dfree(ctx, p);
+        for (auto& pr : T->tx)
+            for (f16*& p : pr) {
+                dfree(ctx, p);
+                p = nullptr;
+            }
     }
     const rh_config& c = ctx->cfg;
     const size_t D = c.dim, F = c.hidden, V = c.vocab, Vp = round_up(V, 128);
@@ -182,9 +212,9 @@ int ensure_train_ws(rh_ctx* ctx, int B, int S) {
     RCK(dalloc(ctx, &T->dlT, Vp * mp));
     RCK(dalloc(ctx, &T->H1, m16 * D));
     RCK(dalloc(ctx, &T->H2, m16 * wide));
-    RCK(dalloc(ctx, &T->T1, D * mp));
-    RCK(dalloc(ctx, &T->T2, std::max(F, D) * mp));
-    RCK(dalloc(ctx, &T->T3, wide * mp));
+    const size_t txr[4][2] = {{D, F}, {2 * F, D}, {D, D}, {3 * D, D}};  // rows of each copy
+    for (int g = 0; g < 4; ++g)
+        for (int i = 0; i < 2; ++i) RCK(dalloc(ctx, &T->tx[g][i], txr[g][i] * mp));
     RCK(dalloc(ctx, &T->dOh, m * D));
     RCK(dalloc(ctx, &T->gout, m * std::max(F, 4 * D)));  // [M][F] dgate, or da [M][D] + dqkv [M][3D]
     RCK(dalloc(ctx, &T->dres, m * D));
@@ -288,7 +318,10 @@ int gamma_grad(rh_ctx* ctx, int nblk, int D, float kappa, float* dgamma) {
 //                 4-wave 88 | 124, 263 | 278)
 //   32000 x 4096 (tied embedding): 192x256 256 | 364, 694 | 772; at K 8192
 //                 256x128 2079 | 2164
-int grad_gemm(rh_ctx* ctx, const f16* X, const f16* W, int rows, int cols, float kappa, float* out) {
+// On the side stream (st != the context's stream) no stream-K: its workspace
+// belongs to the main stream's GEMMs.
+int grad_gemm(rh_ctx* ctx, const f16* X, const f16* W, int rows, int cols, float kappa, float* out,
+              hipStream_t st) {
     rh::GemmArgs g{};
     g.X = X; g.W = W; g.M = rows; g.N = cols; g.K = ctx->train->Mp;
     g.out_f32 = out; g.ldo = cols; g.alpha = kappa;
@@ -299,8 +332,8 @@ int grad_gemm(rh_ctx* ctx, const f16* X, const f16* W, int rows, int cols, float
         g.force_cfg = long_k ? rh::GCFG_D8_256x128 : rh::GCFG_D8_192x256;
     else
         g.force_cfg = long_k ? rh::GCFG_AUTO : rh::GCFG_D8_256x128;
-    set_sk(ctx, g);
-    LCK(rh::launch_gemm(ctx->train->zero ? rh::EPI_F32 : rh::EPI_RESID, g, ctx->stream));
+    if (st == ctx->stream) set_sk(ctx, g);
+    LCK(rh::launch_gemm(ctx->train->zero ? rh::EPI_F32 : rh::EPI_RESID, g, st));
     return RH_OK;
 }
 
@@ -326,20 +359,41 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
     // CE gradient (internal units), dx_final = dl E, dembed += dl^T x_final
     LCK(rh::launch_ce_backward(ctx->logits, ctx->d_tgt, T->dlh, M, V, Vp, c.softcap, rh::GRAD_UNIT, st));
     RCK(data_gemm(ctx, T->dlh, T->embed_t, M, D, Vp, T->gout));
-    LCK(rh::launch_transpose_frag2(T->dlh, T->dlT, M, Vp, T->xf, T->T1, M, D, Mp, st));
-    RCK(grad_gemm(ctx, T->dlT, T->T1, V, D, kappa, T->dembed));
+    LCK(rh::launch_transpose_frag2(T->dlh, T->dlT, M, Vp, T->xf, T->tx[0][0], M, D, Mp, st));
+    RCK(grad_gemm(ctx, T->dlT, T->tx[0][0], V, D, kappa, T->dembed, st));
     // final RMSNorm backward: dy -> dres, a*dy -> H1 (the last layer's dffn)
     LCK(rh::launch_rms_backward(T->gout, T->xlast, ctx->gfinal, nullptr, T->dres, T->H1, alpha, T->dgp, M, D,
                                 c.rms_eps, st));
     RCK(gamma_grad(ctx, nblk, D, kappa, T->dgf));
+    // The weight-gradient GEMMs of a layer run on the side stream in four
+    // groups, each after the main stream has written its operand copies
+    // (made) and before the main stream rewrites them a layer later (used).
+    hipStream_t sd = T->side;
+    for (int g = 0; g < 4; ++g) HCK(hipEventRecord(T->used[g], sd));  // nothing in use yet
+    auto make = [&](int g) -> int {  // before writing group g's copies
+        HCK(hipStreamWaitEvent(st, T->used[g], 0));
+        return RH_OK;
+    };
+    auto hand_over = [&](int g) -> int {  // group g's copies written: its GEMMs may start
+        HCK(hipEventRecord(T->made[g], st));
+        HCK(hipStreamWaitEvent(sd, T->made[g], 0));
+        return RH_OK;
+    };
     for (int l = c.nlayers - 1; l >= 0; --l) {
         const Layer& W = ctx->L[l];
         const TrainState::Cache& cc = T->c[l];
         const TrainState::WT& wt = T->wt[l];
         float* const* G = T->dlay[l].data();
+        f16* const* X0 = T->tx[0];
+        f16* const* X1 = T->tx[1];
+        f16* const* X2 = T->tx[2];
+        f16* const* X3 = T->tx[3];
         // dW2 += dffn^T gate; dgate = dffn W2; SiLU backward
-        LCK(rh::launch_transpose_frag2(T->H1, T->T1, M, D, cc.gate, T->T2, M, F, Mp, st));
-        RCK(grad_gemm(ctx, T->T1, T->T2, D, F, kappa, G[6]));
+        RCK(make(0));
+        LCK(rh::launch_transpose_frag2(T->H1, X0[0], M, D, cc.gate, X0[1], M, F, Mp, st));
+        RCK(hand_over(0));
+        RCK(grad_gemm(ctx, X0[0], X0[1], D, F, kappa, G[6], sd));
+        HCK(hipEventRecord(T->used[0], sd));
         {  // dgate = dffn W2 with the SiLU-gate backward in the epilogue -> [dh1 | dh3]
             rh::GemmArgs g{};
             g.X = T->H1; g.W = wt.w2t; g.M = M; g.N = F; g.K = D;
@@ -349,17 +403,23 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         }
         // dx_ffn = [dh1 | dh3] [W1 | W3]^T; dW1, dW3 += x2n^T dh
         RCK(data_gemm(ctx, T->H2, wt.w13t, M, D, 2 * F, T->gout));
-        LCK(rh::launch_transpose_frag2(T->H2, T->T3, M, 2 * F, cc.x2n, T->T1, M, D, Mp, st));
-        RCK(grad_gemm(ctx, T->T1, T->T3, D, F, kappa, G[4]));
-        RCK(grad_gemm(ctx, T->T1, T->T3 + (size_t)F * Mp, D, F, kappa, G[5]));
+        RCK(make(1));
+        LCK(rh::launch_transpose_frag2(T->H2, X1[0], M, 2 * F, cc.x2n, X1[1], M, D, Mp, st));
+        RCK(hand_over(1));
+        RCK(grad_gemm(ctx, X1[1], X1[0], D, F, kappa, G[4], sd));
+        RCK(grad_gemm(ctx, X1[1], X1[0] + (size_t)F * Mp, D, F, kappa, G[5], sd));
+        HCK(hipEventRecord(T->used[1], sd));
         // dx2 = RMSNorm2'(dx_ffn) + dy (in place in dres); a*dx2 -> H1
         LCK(rh::launch_rms_backward(T->gout, cc.x2, W.g2, T->dres, T->dres, T->H1, alpha, T->dgp, M, D,
                                     c.rms_eps, st));
         RCK(gamma_grad(ctx, nblk, D, kappa, G[8]));
         // da = (a dx2) Wo^T; dWo += attn^T (a dx2)
         RCK(data_gemm(ctx, T->H1, wt.ot, M, D, D, T->gout));
-        LCK(rh::launch_transpose_frag2(T->H1, T->T1, M, D, cc.attn, T->T2, M, D, Mp, st));
-        RCK(grad_gemm(ctx, T->T2, T->T1, D, D, kappa, G[3]));
+        RCK(make(2));
+        LCK(rh::launch_transpose_frag2(T->H1, X2[0], M, D, cc.attn, X2[1], M, D, Mp, st));
+        RCK(hand_over(2));
+        RCK(grad_gemm(ctx, X2[1], X2[0], D, D, kappa, G[3], sd));
+        HCK(hipEventRecord(T->used[2], sd));
         // attention backward -> dq | dk | dv, RoPE backward, fp16 pack
         float* dqkv = T->gout + (size_t)M * D;  // past da, which the attention kernels read
         LCK(rh::launch_attn_backward(cc.q, cc.k, cc.v, cc.attn, T->gout, cc.lse, T->dOh, T->Drow, dqkv, B, H, S,
@@ -367,13 +427,19 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         LCK(rh::launch_rope_backward_pack(dqkv, ctx->rope, T->H2, M, S, D, hd, st));
         // dxn = dqkv [Wq | Wk | Wv]^T; dWq, dWk, dWv += xn^T d{q,k,v}
         RCK(data_gemm(ctx, T->H2, wt.qkvt, M, D, 3 * D, T->gout));
-        LCK(rh::launch_transpose_frag2(T->H2, T->T3, M, 3 * D, cc.xn, T->T1, M, D, Mp, st));
-        for (int j = 0; j < 3; ++j) RCK(grad_gemm(ctx, T->T1, T->T3 + (size_t)j * D * Mp, D, D, kappa, G[j]));
+        RCK(make(3));
+        LCK(rh::launch_transpose_frag2(T->H2, X3[0], M, 3 * D, cc.xn, X3[1], M, D, Mp, st));
+        RCK(hand_over(3));
+        for (int j = 0; j < 3; ++j)
+            RCK(grad_gemm(ctx, X3[1], X3[0] + (size_t)j * D * Mp, D, D, kappa, G[j], sd));
+        HCK(hipEventRecord(T->used[3], sd));
         // dy' = RMSNorm1'(dxn) + dx2 (in place); a*dy' -> H1 (the next layer's dffn)
         LCK(rh::launch_rms_backward(T->gout, cc.xin, W.g1, T->dres, T->dres, T->H1, alpha, T->dgp, M, D,
                                     c.rms_eps, st));
         RCK(gamma_grad(ctx, nblk, D, kappa, G[7]));
     }
+    // every weight gradient is written before anything after the backward reads them
+    HCK(hipStreamWaitEvent(st, T->used[3], 0));
     LCK(rh::launch_embed_backward(T->dres, T->utok, T->ustart, T->uidx, nuniq, kappa, T->dembed, D, st));
     T->zero = false;
     return RH_OK;
