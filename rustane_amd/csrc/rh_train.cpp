@@ -52,15 +52,19 @@ struct TrainState {
     float* xlast = nullptr;  // residual after the last layer
     f16* xf = nullptr;       // final RMSNorm rows (fragment order)
     // backward workspace
-    f16 *dlh = nullptr, *dlT = nullptr, *H1 = nullptr, *H2 = nullptr;
-    // Token-inner copies of the weight-gradient GEMMs' operands, one pair per
-    // group of those GEMMs in a layer (0: dW2, 1: dW1 dW3, 2: dWo, 3: dWq dWk
-    // dWv), so a group runs on the side stream while the main stream goes on
-    // to the data gradients and the next group's copies: made[g] (main) says
-    // group g's copies are written, used[g] (side) that its GEMMs have read them.
+    // Activation gradients in fp16 fragment order, one buffer per role so each
+    // is rewritten only once per layer: H1 = the layer's output gradient times
+    // alpha (dffn), H1m = alpha * dx2, H2 = [dh1 | dh3], H2q = [dq | dk | dv].
+    f16 *dlh = nullptr, *dlT = nullptr, *H1 = nullptr, *H1m = nullptr, *H2 = nullptr, *H2q = nullptr;
+    // The weight-gradient GEMMs run on the side stream in four groups per
+    // layer (0: dW2, 1: dW1 dW3, 2: dWo, 3: dWq dWk dWv), each after its
+    // token-inner operand copies tx[g] (written on the side stream too, from
+    // the activation gradient above and a forward cache).  ready[g] (main):
+    // group g's activation gradient is written; read[g] (side): the copy has
+    // read it, so the main stream may rewrite that buffer a layer later.
     f16* tx[4][2] = {};
     hipStream_t side = nullptr;
-    hipEvent_t made[4] = {}, used[4] = {};
+    hipEvent_t ready[5] = {}, read[4] = {};  // ready[4]: the logits gradient
     f16* dOh = nullptr;
     float *gout = nullptr, *dres = nullptr, *Drow = nullptr, *dgp = nullptr;
     uint32_t* utok = nullptr;
@@ -83,10 +87,10 @@ struct TrainState {
             (void)hipStreamSynchronize(side);
             (void)hipStreamDestroy(side);
         }
-        for (int g = 0; g < 4; ++g) {
-            if (made[g]) (void)hipEventDestroy(made[g]);
-            if (used[g]) (void)hipEventDestroy(used[g]);
-        }
+        for (hipEvent_t e : ready)
+            if (e) (void)hipEventDestroy(e);
+        for (hipEvent_t e : read)
+            if (e) (void)hipEventDestroy(e);
         delete opt;
     }
 };
@@ -140,10 +144,8 @@ int ensure_train_static(rh_ctx* ctx) {
     const size_t D = c.dim, F = c.hidden, V = c.vocab, Vp = round_up(V, 128);
     if (!T->side) {  // the weight-gradient GEMMs' stream (default priority, like the context's)
         HCK(hipStreamCreateWithFlags(&T->side, hipStreamNonBlocking));
-        for (int g = 0; g < 4; ++g) {
-            HCK(hipEventCreateWithFlags(&T->made[g], hipEventDisableTiming));
-            HCK(hipEventCreateWithFlags(&T->used[g], hipEventDisableTiming));
-        }
+        for (hipEvent_t& e : T->ready) HCK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        for (hipEvent_t& e : T->read) HCK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     }
     RCK(dalloc(ctx, &T->dembed, V * D));
     RCK(dalloc(ctx, &T->dgf, D));
@@ -179,7 +181,7 @@ int ensure_train_ws(rh_ctx* ctx, int B, int S) {
         for (void* p : ps) dfree(ctx, p);
     }
     {
-        void* ps[] = {T->xlast, T->xf, T->dlh, T->dlT, T->H1, T->H2, T->dOh,
+        void* ps[] = {T->xlast, T->xf, T->dlh, T->dlT, T->H1, T->H1m, T->H2, T->H2q, T->dOh,
                       T->gout, T->dres, T->Drow, T->dgp, T->utok, T->ustart, T->uidx};
         for (void* p : ps) dfree(ctx, p);
         for (auto& pr : T->tx)
@@ -205,13 +207,14 @@ int ensure_train_ws(rh_ctx* ctx, int B, int S) {
         RCK(dalloc(ctx, &cc.h13, 2 * m * F));
         RCK(dalloc(ctx, &cc.gate, m16 * F));
     }
-    const size_t wide = std::max(2 * F, 3 * D);
     RCK(dalloc(ctx, &T->xlast, m * D));
     RCK(dalloc(ctx, &T->xf, m16 * D));
     RCK(dalloc(ctx, &T->dlh, m16 * Vp));
     RCK(dalloc(ctx, &T->dlT, Vp * mp));
     RCK(dalloc(ctx, &T->H1, m16 * D));
-    RCK(dalloc(ctx, &T->H2, m16 * wide));
+    RCK(dalloc(ctx, &T->H1m, m16 * D));
+    RCK(dalloc(ctx, &T->H2, m16 * 2 * F));
+    RCK(dalloc(ctx, &T->H2q, m16 * 3 * D));
     const size_t txr[4][2] = {{D, F}, {2 * F, D}, {D, D}, {3 * D, D}};  // rows of each copy
     for (int g = 0; g < 4; ++g)
         for (int i = 0; i < 2; ++i) RCK(dalloc(ctx, &T->tx[g][i], txr[g][i] * mp));
@@ -356,29 +359,32 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
     const float kappa = loss_scale / ((float)S * rh::GRAD_UNIT);
     const int nblk = rh::rms_backward_blocks(M);
     hipStream_t st = ctx->stream;
+    // Main stream: the chain through the data gradients.  Side stream: the
+    // weight gradients, each group from its own copies, after the activation
+    // gradient it reads is written (ready) and before that buffer is rewritten
+    // a layer later (read).  No buffer either stream writes is touched by the
+    // other until the event that orders them.
+    hipStream_t sd = T->side;
+    for (hipEvent_t e : T->read) HCK(hipEventRecord(e, sd));  // nothing read yet
+    auto publish = [&](int g) -> int {  // main -> side: group g's input is written
+        HCK(hipEventRecord(T->ready[g], st));
+        HCK(hipStreamWaitEvent(sd, T->ready[g], 0));
+        return RH_OK;
+    };
+    auto rewrite = [&](int g) -> int {  // main waits: the side has copied group g's input
+        HCK(hipStreamWaitEvent(st, T->read[g], 0));
+        return RH_OK;
+    };
     // CE gradient (internal units), dx_final = dl E, dembed += dl^T x_final
     LCK(rh::launch_ce_backward(ctx->logits, ctx->d_tgt, T->dlh, M, V, Vp, c.softcap, rh::GRAD_UNIT, st));
+    RCK(publish(4));
+    LCK(rh::launch_transpose_frag2(T->dlh, T->dlT, M, Vp, T->xf, T->tx[0][0], M, D, Mp, sd));
+    RCK(grad_gemm(ctx, T->dlT, T->tx[0][0], V, D, kappa, T->dembed, sd));
     RCK(data_gemm(ctx, T->dlh, T->embed_t, M, D, Vp, T->gout));
-    LCK(rh::launch_transpose_frag2(T->dlh, T->dlT, M, Vp, T->xf, T->tx[0][0], M, D, Mp, st));
-    RCK(grad_gemm(ctx, T->dlT, T->tx[0][0], V, D, kappa, T->dembed, st));
     // final RMSNorm backward: dy -> dres, a*dy -> H1 (the last layer's dffn)
     LCK(rh::launch_rms_backward(T->gout, T->xlast, ctx->gfinal, nullptr, T->dres, T->H1, alpha, T->dgp, M, D,
                                 c.rms_eps, st));
     RCK(gamma_grad(ctx, nblk, D, kappa, T->dgf));
-    // The weight-gradient GEMMs of a layer run on the side stream in four
-    // groups, each after the main stream has written its operand copies
-    // (made) and before the main stream rewrites them a layer later (used).
-    hipStream_t sd = T->side;
-    for (int g = 0; g < 4; ++g) HCK(hipEventRecord(T->used[g], sd));  // nothing in use yet
-    auto make = [&](int g) -> int {  // before writing group g's copies
-        HCK(hipStreamWaitEvent(st, T->used[g], 0));
-        return RH_OK;
-    };
-    auto hand_over = [&](int g) -> int {  // group g's copies written: its GEMMs may start
-        HCK(hipEventRecord(T->made[g], st));
-        HCK(hipStreamWaitEvent(sd, T->made[g], 0));
-        return RH_OK;
-    };
     for (int l = c.nlayers - 1; l >= 0; --l) {
         const Layer& W = ctx->L[l];
         const TrainState::Cache& cc = T->c[l];
@@ -388,58 +394,59 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         f16* const* X1 = T->tx[1];
         f16* const* X2 = T->tx[2];
         f16* const* X3 = T->tx[3];
-        // dW2 += dffn^T gate; dgate = dffn W2; SiLU backward
-        RCK(make(0));
-        LCK(rh::launch_transpose_frag2(T->H1, X0[0], M, D, cc.gate, X0[1], M, F, Mp, st));
-        RCK(hand_over(0));
+        // dW2 += dffn^T gate (side); dgate = dffn W2 with the SiLU backward -> [dh1 | dh3]
+        RCK(publish(0));
+        LCK(rh::launch_transpose_frag2(T->H1, X0[0], M, D, cc.gate, X0[1], M, F, Mp, sd));
+        HCK(hipEventRecord(T->read[0], sd));
         RCK(grad_gemm(ctx, X0[0], X0[1], D, F, kappa, G[6], sd));
-        HCK(hipEventRecord(T->used[0], sd));
-        {  // dgate = dffn W2 with the SiLU-gate backward in the epilogue -> [dh1 | dh3]
+        RCK(rewrite(1));
+        {
             rh::GemmArgs g{};
             g.X = T->H1; g.W = wt.w2t; g.M = M; g.N = F; g.K = D;
             g.h13 = cc.h13; g.out_f16 = T->H2; g.ldo = F;
             set_sk(ctx, g);
             LCK(rh::launch_gemm(rh::EPI_SILU_BWD, g, st));
         }
-        // dx_ffn = [dh1 | dh3] [W1 | W3]^T; dW1, dW3 += x2n^T dh
-        RCK(data_gemm(ctx, T->H2, wt.w13t, M, D, 2 * F, T->gout));
-        RCK(make(1));
-        LCK(rh::launch_transpose_frag2(T->H2, X1[0], M, 2 * F, cc.x2n, X1[1], M, D, Mp, st));
-        RCK(hand_over(1));
+        // dx_ffn = [dh1 | dh3] [W1 | W3]^T; dW1, dW3 += x2n^T dh (side)
+        RCK(publish(1));
+        LCK(rh::launch_transpose_frag2(T->H2, X1[0], M, 2 * F, cc.x2n, X1[1], M, D, Mp, sd));
+        HCK(hipEventRecord(T->read[1], sd));
         RCK(grad_gemm(ctx, X1[1], X1[0], D, F, kappa, G[4], sd));
         RCK(grad_gemm(ctx, X1[1], X1[0] + (size_t)F * Mp, D, F, kappa, G[5], sd));
-        HCK(hipEventRecord(T->used[1], sd));
-        // dx2 = RMSNorm2'(dx_ffn) + dy (in place in dres); a*dx2 -> H1
-        LCK(rh::launch_rms_backward(T->gout, cc.x2, W.g2, T->dres, T->dres, T->H1, alpha, T->dgp, M, D,
+        RCK(data_gemm(ctx, T->H2, wt.w13t, M, D, 2 * F, T->gout));
+        // dx2 = RMSNorm2'(dx_ffn) + dy (in place in dres); a*dx2 -> H1m
+        RCK(rewrite(2));
+        LCK(rh::launch_rms_backward(T->gout, cc.x2, W.g2, T->dres, T->dres, T->H1m, alpha, T->dgp, M, D,
                                     c.rms_eps, st));
         RCK(gamma_grad(ctx, nblk, D, kappa, G[8]));
-        // da = (a dx2) Wo^T; dWo += attn^T (a dx2)
-        RCK(data_gemm(ctx, T->H1, wt.ot, M, D, D, T->gout));
-        RCK(make(2));
-        LCK(rh::launch_transpose_frag2(T->H1, X2[0], M, D, cc.attn, X2[1], M, D, Mp, st));
-        RCK(hand_over(2));
+        // da = (a dx2) Wo^T; dWo += attn^T (a dx2) (side)
+        RCK(publish(2));
+        LCK(rh::launch_transpose_frag2(T->H1m, X2[0], M, D, cc.attn, X2[1], M, D, Mp, sd));
+        HCK(hipEventRecord(T->read[2], sd));
         RCK(grad_gemm(ctx, X2[1], X2[0], D, D, kappa, G[3], sd));
-        HCK(hipEventRecord(T->used[2], sd));
+        RCK(data_gemm(ctx, T->H1m, wt.ot, M, D, D, T->gout));
         // attention backward -> dq | dk | dv, RoPE backward, fp16 pack
         float* dqkv = T->gout + (size_t)M * D;  // past da, which the attention kernels read
         LCK(rh::launch_attn_backward(cc.q, cc.k, cc.v, cc.attn, T->gout, cc.lse, T->dOh, T->Drow, dqkv, B, H, S,
                                      hd, st));
-        LCK(rh::launch_rope_backward_pack(dqkv, ctx->rope, T->H2, M, S, D, hd, st));
-        // dxn = dqkv [Wq | Wk | Wv]^T; dWq, dWk, dWv += xn^T d{q,k,v}
-        RCK(data_gemm(ctx, T->H2, wt.qkvt, M, D, 3 * D, T->gout));
-        RCK(make(3));
-        LCK(rh::launch_transpose_frag2(T->H2, X3[0], M, 3 * D, cc.xn, X3[1], M, D, Mp, st));
-        RCK(hand_over(3));
+        RCK(rewrite(3));
+        LCK(rh::launch_rope_backward_pack(dqkv, ctx->rope, T->H2q, M, S, D, hd, st));
+        // dxn = dqkv [Wq | Wk | Wv]^T; dWq, dWk, dWv += xn^T d{q,k,v} (side)
+        RCK(publish(3));
+        LCK(rh::launch_transpose_frag2(T->H2q, X3[0], M, 3 * D, cc.xn, X3[1], M, D, Mp, sd));
+        HCK(hipEventRecord(T->read[3], sd));
         for (int j = 0; j < 3; ++j)
             RCK(grad_gemm(ctx, X3[1], X3[0] + (size_t)j * D * Mp, D, D, kappa, G[j], sd));
-        HCK(hipEventRecord(T->used[3], sd));
+        RCK(data_gemm(ctx, T->H2q, wt.qkvt, M, D, 3 * D, T->gout));
         // dy' = RMSNorm1'(dxn) + dx2 (in place); a*dy' -> H1 (the next layer's dffn)
+        RCK(rewrite(0));
         LCK(rh::launch_rms_backward(T->gout, cc.xin, W.g1, T->dres, T->dres, T->H1, alpha, T->dgp, M, D,
                                     c.rms_eps, st));
         RCK(gamma_grad(ctx, nblk, D, kappa, G[7]));
     }
     // every weight gradient is written before anything after the backward reads them
-    HCK(hipStreamWaitEvent(st, T->used[3], 0));
+    HCK(hipEventRecord(T->ready[4], sd));
+    HCK(hipStreamWaitEvent(st, T->ready[4], 0));
     LCK(rh::launch_embed_backward(T->dres, T->utok, T->ustart, T->uidx, nuniq, kappa, T->dembed, D, st));
     T->zero = false;
     return RH_OK;
