@@ -250,6 +250,25 @@ struct DTile {
     }
 };
 
+// SiLU-gate backward (layer.rs:7083-7104) of the gate gradient g = (v0..v3)
+// of token m, features n..n+3, and the saved a1 = h1, a3 = h3 there:
+// dh3 = g silu(h1), dh1 = g h3 silu'(h1), fp16 in fragment order [M][2N]
+// (dh1 in columns 0..N-1, dh3 in N..2N-1).
+__device__ __forceinline__ void silu_bwd4(const GemmArgs& a, int m, int n, float v0, float v1, float v2, float v3,
+                                          f16x4 a1, f16x4 a3) {
+    const float g[4] = {v0, v1, v2, v3};
+    f16x4 o1, o3;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float h1 = (float)a1[e], h3 = (float)a3[e];
+        const float sig = 1.0f / (1.0f + __expf(-h1));
+        o3[e] = (f16)(g[e] * (h1 * sig));
+        o1[e] = (f16)(g[e] * h3 * (sig * (1.0f + h1 * (1.0f - sig))));
+    }
+    *(f16x4*)(a.out_f16 + frag_off(m, n, 2 * a.ldo)) = o1;
+    *(f16x4*)(a.out_f16 + frag_off(m, a.ldo + n, 2 * a.ldo)) = o3;
+}
+
 // Stores four consecutive output features n..n+3 of token m (every epilogue
 // but SwiGLU, whose lanes hold W1 and W3 rows and store gate features).
 template <int EPI>
@@ -288,22 +307,8 @@ __device__ __forceinline__ void store4(const GemmArgs& a, int m, int n, float v0
             dst = (sec == 1 ? a.kc : a.vc) + (((size_t)b * a.H + h) * a.ctx + pos) * a.hd + d;
         *(f16x4*)dst = f16x4{(f16)v0, (f16)v1, (f16)v2, (f16)v3};
     } else if constexpr (EPI == EPI_SILU_BWD) {
-        // SiLU-gate backward (layer.rs:7083-7104) of the gate gradient g = acc
-        // and the saved h1, h3: dh3 = g silu(h1), dh1 = g h3 silu'(h1), fp16
-        // in fragment order [M][2N] (dh1 in columns 0..N-1, dh3 in N..2N-1)
         const size_t o = (size_t)m * a.ldo + n, plane = (size_t)a.M * a.ldo;
-        const f16x4 a1 = *(const f16x4*)(a.h13 + o), a3 = *(const f16x4*)(a.h13 + plane + o);
-        const float g[4] = {v0, v1, v2, v3};
-        f16x4 o1, o3;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float h1 = (float)a1[e], h3 = (float)a3[e];
-            const float sig = 1.0f / (1.0f + __expf(-h1));
-            o3[e] = (f16)(g[e] * (h1 * sig));
-            o1[e] = (f16)(g[e] * h3 * (sig * (1.0f + h1 * (1.0f - sig))));
-        }
-        *(f16x4*)(a.out_f16 + frag_off(m, n, 2 * a.ldo)) = o1;
-        *(f16x4*)(a.out_f16 + frag_off(m, a.ldo + n, 2 * a.ldo)) = o3;
+        silu_bwd4(a, m, n, v0, v1, v2, v3, *(const f16x4*)(a.h13 + o), *(const f16x4*)(a.h13 + plane + o));
     }
 }
 
@@ -455,8 +460,40 @@ __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long lo
     if constexpr (MODE == MODE_DP) {
         const int t = xcd_remap(blockIdx.x, nbN * nbM);
         const int nb = t / nbM, mb = t - nb * nbM;
-        Tl::run(a, nb * Tl::BN, mb * Tl::BM, 0, KT, acc, sm);
-        run_epilogue<Tl, EPI>(a, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
+        if constexpr (EPI == EPI_SILU_BWD && Tl::kM16 && Tl::NA * Tl::NB <= 12) {
+            // The saved h1, h3 of this lane's outputs are loaded before the k
+            // loop, so they arrive under it instead of stalling the epilogue
+            // (2 * NA * NB registers held through the loop: the larger tiles
+            // would spill).
+            const int nw = Tl::nw(nb * Tl::BN), mw = Tl::mw(mb * Tl::BM), lane = threadIdx.x & 63;
+            const size_t plane = (size_t)a.M * a.ldo;
+            f16x4 p1[Tl::NB][Tl::NA], p3[Tl::NB][Tl::NA];
+#pragma unroll
+            for (int j = 0; j < Tl::NB; ++j)
+#pragma unroll
+                for (int i = 0; i < Tl::NA; ++i) {
+                    const int m = mw + 16 * j + (lane & 15), n = nw + 16 * i + 4 * (lane >> 4);
+                    p1[j][i] = p3[j][i] = f16x4{};
+                    if (m < a.M && n < a.N) {
+                        const size_t o = (size_t)m * a.ldo + n;
+                        p1[j][i] = *(const f16x4*)(a.h13 + o);
+                        p3[j][i] = *(const f16x4*)(a.h13 + plane + o);
+                    }
+                }
+            Tl::run(a, nb * Tl::BN, mb * Tl::BM, 0, KT, acc, sm);
+#pragma unroll
+            for (int j = 0; j < Tl::NB; ++j)
+#pragma unroll
+                for (int i = 0; i < Tl::NA; ++i) {
+                    const int m = mw + 16 * j + (lane & 15), n = nw + 16 * i + 4 * (lane >> 4);
+                    if (m < a.M && n < a.N)
+                        silu_bwd4(a, m, n, acc.v[i][j][0], acc.v[i][j][1], acc.v[i][j][2], acc.v[i][j][3], p1[j][i],
+                                  p3[j][i]);
+                }
+        } else {
+            Tl::run(a, nb * Tl::BN, mb * Tl::BM, 0, KT, acc, sm);
+            run_epilogue<Tl, EPI>(a, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
+        }
     } else if constexpr (MODE == MODE_SPLIT) {
         // the splits of one tile and the tiles of one weight panel land on the
         // same XCD
