@@ -18,8 +18,10 @@
  *    during the call.  Device pointers (the *_dev entry points) must stay
  *    valid until the context's stream has drained (rh_sync).
  *  - A context owns one GPU, one HIP stream and all device memory (fp16
- *    weights, KV cache, workspaces).  A context is driven by one thread at a
- *    time; separate contexts may run concurrently (multistream.rs:54-161).
+ *    weights, KV cache, workspaces); training adds a second stream of its
+ *    own for the weight gradients, joined back into the context stream
+ *    before rh_forward_backward returns.  A context is driven by one thread
+ *    at a time; separate contexts may run concurrently (multistream.rs:54-161).
  *  - Activations are token-major inside the library; the weight tensors come
  *    in and go out in the reference orientation (layer.rs:52-63).
  */
@@ -119,7 +121,8 @@ int rh_forward_dev(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets,
  * (they accumulate across calls, as the reference's ModelGrads do; see
  * rh_zero_grads).  The first call allocates the gradients (the parameter
  * count in fp32), transposed fp16 weight copies and per-layer activation
- * caches.  mean_loss_out nullable [batch].  Needs hidden % 64 == 0. */
+ * caches, and creates the weight-gradient stream.  Synchronises before
+ * returning.  mean_loss_out nullable [batch].  Needs hidden % 64 == 0. */
 int rh_forward_backward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
                         float loss_scale, float* mean_loss_out);
 /* ModelGrads::zero_out: sets every gradient to 0. */
