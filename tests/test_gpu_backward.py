@@ -110,6 +110,26 @@ def test_backward_accumulates_and_is_deterministic(orc):
     assert all(np.abs(t).max() > 0 for t in flat(one))  # every weight group gets a gradient
 
 
+def test_backward_workspace_growth_between_calls(orc):
+    """B 1, then B 2 (the activation caches, operand copies and activation
+    gradients are reallocated while the weight-gradient stream exists), then
+    B 1 again: the accumulated gradients equal the oracle's three calls."""
+    cfg = small_cfg(dim=256, hidden=512, heads=2, hd=128, nlayers=2, vocab=1024, seq=64)
+    w = random_gammas(ModelWeights.normal(cfg, seed=93, std=0.05), 94)
+    t1, g1 = tokens_uniform(95, cfg.vocab, 1, cfg.seq)
+    t2, g2 = tokens_uniform(96, cfg.vocab, 2, cfg.seq)
+    print("[case] backward workspace growth B1 -> B2 -> B1", flush=True)
+    with hb.Context(cfg.to_rh(), 0, 2, 0) as c:
+        c.load_weights(w.embed, w.gamma_final, [lw.tensors() for lw in w.layers])
+        for tok, tgt in ((t1, g1), (t2, g2), (t1, g1)):
+            c.forward_backward(tok, tgt)
+        got = c.read_grads()
+    ow, oc, og = oracle_weights(orc, w), oracle_cfg(orc, cfg), None
+    for tok, tgt in ((t1, g1), (t2, g2), (t1, g1)):
+        og, _ = orc.forward_backward(oc, ow, tok, tgt, grads=og)
+    _check_grads(got, og)
+
+
 def test_backward_weights_reload_rebuilds_transposed_copies(orc):
     """New weights after a backward must be seen by the next backward (the
     data-gradient GEMMs read transposed copies built per weight version)."""
