@@ -175,6 +175,7 @@ int ensure_train_ws(rh_ctx* ctx, int B, int S) {
         return RH_OK;
     }
     HCK(hipStreamSynchronize(ctx->stream));
+    if (T->side) HCK(hipStreamSynchronize(T->side));  // the weight-gradient stream reads some of them
     // free the old per-shape buffers
     for (auto& cc : T->c) {
         void* ps[] = {cc.xin, cc.x2, cc.lse, cc.xn, cc.q, cc.k, cc.v, cc.attn, cc.x2n, cc.h13, cc.gate};
@@ -781,7 +782,13 @@ int rh_forward_backward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* tar
     HCK(hipMemcpyAsync(T->ustart, start.data(), start.size() * sizeof(int), hipMemcpyHostToDevice, st));
     HCK(hipMemcpyAsync(T->uidx, idx.data(), idx.size() * sizeof(int), hipMemcpyHostToDevice, st));
     RCK(enqueue_forward_train(ctx, batch, seq));
-    RCK(enqueue_backward(ctx, batch, seq, loss_scale, (int)utok.size()));
+    {
+        const int rc = enqueue_backward(ctx, batch, seq, loss_scale, (int)utok.size());
+        if (rc != RH_OK) {  // leave no weight-gradient work behind a failed call
+            (void)hipStreamSynchronize(T->side);
+            return rc;
+        }
+    }
     if (mean_loss_out)
         HCK(hipMemcpyAsync(mean_loss_out, ctx->mean, batch * sizeof(float), hipMemcpyDeviceToHost, st));
     HCK(hipStreamSynchronize(st));
