@@ -290,8 +290,10 @@ __device__ __forceinline__ void store4(const GemmArgs& a, int m, int n, float v0
         x[2] = v2 * a.alpha + x[2]; x[3] = v3 * a.alpha + x[3];
         *px = x;
     } else if constexpr (EPI == EPI_QKV) {
-        const int sec = n / a.D, c = n - sec * a.D;
-        const int h = c / a.hd, d = c - h * a.hd;
+        // no integer divisions by run-time values here but the per-row m / S
+        // (hoisted out of the feature loop): n < 3D, hd a power of two
+        const int sec = (n >= a.D) + (n >= 2 * a.D), c = n - sec * a.D;
+        const int h = c >> __builtin_ctz(a.hd), d = c & (a.hd - 1);
         const int b = m / a.S, s = m - b * a.S, pos = a.pos0 + s;
         if (sec < 2) {
             const float2 cs0 = a.rope[(size_t)pos * (a.hd / 2) + d / 2];
@@ -710,7 +712,9 @@ hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st) {
         case EPI_SWIGLU:
             if (a.N % 32 != 0) return hipErrorInvalidValue;
             return launch_epi<EPI_SWIGLU>(a, st);
-        case EPI_QKV: return launch_epi<EPI_QKV>(a, st);
+        case EPI_QKV:
+            if (a.hd <= 0 || (a.hd & (a.hd - 1)) != 0 || a.N != 3 * a.D || a.S <= 0) return hipErrorInvalidValue;
+            return launch_epi<EPI_QKV>(a, st);
         case EPI_SWIGLU_SAVE:
             if (a.N % 32 != 0 || !a.h13) return hipErrorInvalidValue;
             return launch_epi<EPI_SWIGLU_SAVE>(a, st);
