@@ -231,38 +231,76 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const f16* __restric
     }
 }
 
-// dO [M, H*hd] fp32 (token-major GEMM output) -> fp16 [B][H][S][hd], and
-// D[b][h][s] = sum_d dO * O with O the forward's attention output (fragment
-// order).  One wave per (token, head); lane d covers dims d, d + 64.
-__global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const float* __restrict__ dOf, const f16* __restrict__ O,
-                                                            f16* __restrict__ dOh, float* __restrict__ Drow,
-                                                            int B, int H, int S, int HD) {
-    const int lane = threadIdx.x & 63;
-    const long long item = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= (long long)B * S * H) return;
-    const int h = (int)(item % H);
-    const long long m = item / H;  // token row b*S + s
-    const int b = (int)(m / S), s = (int)(m % S);
+// dO [M, H*hd] fp32 (token-major GEMM output, the sum of NS split-K
+// partials split_stride floats apart, added in order) -> fp16 [B][H][S][hd],
+// and D[b][h][s] = sum_d dO * O with O the forward's attention output
+// (fragment order, 8 features of a row contiguous).  One thread per 8
+// features, HD/8 neighbouring lanes per (token, head).
+template <int NS, int HD>
+__global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const float* __restrict__ dOf, size_t split_stride,
+                                                            const f16* __restrict__ O, f16* __restrict__ dOh,
+                                                            float* __restrict__ Drow, int M, int H, int S) {
+    constexpr int LPI = HD / 8;
     const int D = H * HD;
-    float acc = 0.f;
-    for (int d = lane; d < HD; d += 64) {
-        const float v = dOf[m * D + h * HD + d];
-        acc += v * (float)O[frag_off((int)m, h * HD + d, D)];
-        dOh[(((size_t)b * H + h) * S + s) * HD + d] = (f16)v;
+    const long long e = ((long long)blockIdx.x * 256 + threadIdx.x) * 8;
+    // M * D is a multiple of HD, so a (token, head) group is all in or all out
+    if (e >= (long long)M * D) return;
+    const int m = (int)(e / D), c = (int)(e - (long long)m * D);
+    const int h = c / HD, d = c - h * HD;
+    f32x4 p[NS][2];
+#pragma unroll
+    for (int sp = 0; sp < NS; ++sp) {
+        p[sp][0] = *(const f32x4*)(dOf + sp * split_stride + e);
+        p[sp][1] = *(const f32x4*)(dOf + sp * split_stride + e + 4);
     }
-    acc = wave_sum(acc);
-    if (lane == 0) Drow[((size_t)b * H + h) * S + s] = acc;
+    const f16x8 o = *(const f16x8*)(O + frag_off(m, c, D));
+    f32x4 v0 = p[0][0], v1 = p[0][1];
+#pragma unroll
+    for (int sp = 1; sp < NS; ++sp) {
+        v0 += p[sp][0];
+        v1 += p[sp][1];
+    }
+    float acc = 0.f;
+    f16x8 hv;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        acc += v0[q] * (float)o[q];
+        hv[q] = (f16)v0[q];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        acc += v1[q] * (float)o[4 + q];
+        hv[4 + q] = (f16)v1[q];
+    }
+#pragma unroll
+    for (int off = LPI / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, RH_WAVE);
+    const int b = m / S, s = m - b * S;
+    const size_t row = ((size_t)b * H + h) * S + s;
+    *(f16x8*)(dOh + row * HD + d) = hv;
+    if (d == 0) Drow[row] = acc;
 }
 
 }  // namespace
 
 hipError_t launch_attn_backward(const f16* q, const f16* k, const f16* v, const f16* o, const float* dOf,
-                                const float* lse, f16* dOh, float* Drow, float* dqkv, int B, int H, int S, int hd,
-                                hipStream_t st) {
-    if (hd != 128 && hd != 64) return hipErrorInvalidValue;
-    const long long items = (long long)B * S * H;
-    hipLaunchKernelGGL(attn_bwd_prep_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st, dOf, o, dOh, Drow,
-                       B, H, S, hd);
+                                int nsplit, size_t split_stride, const float* lse, f16* dOh, float* Drow,
+                                float* dqkv, int B, int H, int S, int hd, hipStream_t st) {
+    if ((hd != 128 && hd != 64) || nsplit < 1 || nsplit > 8) return hipErrorInvalidValue;
+    const int M = B * S;
+    const unsigned pgrid = (unsigned)(((long long)M * H * hd / 8 + 255) / 256);
+#define RH_PREP(NS_)                                                                                               \
+    case NS_:                                                                                                      \
+        if (hd == 128)                                                                                             \
+            hipLaunchKernelGGL((attn_bwd_prep_kernel<NS_, 128>), dim3(pgrid), dim3(256), 0, st, dOf, split_stride,  \
+                               o, dOh, Drow, M, H, S);                                                             \
+        else                                                                                                       \
+            hipLaunchKernelGGL((attn_bwd_prep_kernel<NS_, 64>), dim3(pgrid), dim3(256), 0, st, dOf, split_stride,   \
+                               o, dOh, Drow, M, H, S);                                                             \
+        break
+    switch (nsplit) {
+        RH_PREP(1); RH_PREP(2); RH_PREP(3); RH_PREP(4); RH_PREP(5); RH_PREP(6); RH_PREP(7); RH_PREP(8);
+    }
+#undef RH_PREP
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const dim3 grid((S + 63) / 64 * H * B);

@@ -497,10 +497,23 @@ __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long lo
             run_epilogue<Tl, EPI>(a, Tl::nw(nb * Tl::BN), Tl::mw(mb * Tl::BM), acc);
         }
     } else if constexpr (MODE == MODE_SPLIT) {
-        // the splits of one tile and the tiles of one weight panel land on the
-        // same XCD
-        const int v = xcd_remap(blockIdx.x, nbN * nbM * P);
-        const int tile = v / P, sp = v - tile * P;
+        // Blocks go round-robin to the 8 XCDs (block b on XCD b % 8).  When P
+        // divides 8 and the tiles share out evenly, XCD x runs split x % P of
+        // its 1/(8/P) of the tiles, panel by panel: each XCD's L2 then fetches
+        // only its k-slice of the activation (which every tile reads) and
+        // each weight slice once for all M-tiles of its panel.  Otherwise the
+        // splits of one tile and the tiles of one weight panel share an XCD.
+        const int tiles = nbN * nbM;
+        int tile, sp;
+        if (8 % P == 0 && tiles % (8 / P) == 0) {
+            const int x = blockIdx.x & 7;
+            sp = x % P;
+            tile = (x / P) * (tiles / (8 / P)) + (blockIdx.x >> 3);
+        } else {
+            const int v = xcd_remap(blockIdx.x, tiles * P);
+            tile = v / P;
+            sp = v - tile * P;
+        }
         const int nb = tile / nbM, mb = tile - nb * nbM;
         const int kb = (int)((long long)sp * KT / P), ke = (int)((long long)(sp + 1) * KT / P);
         Tl::run(a, nb * Tl::BN, mb * Tl::BM, kb, ke, acc, sm);
@@ -677,24 +690,46 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
 
 size_t gemm_sk_part_floats() { return (size_t)SK_P * 2 * 256 * 256; }
 
-hipError_t launch_gemm_resid_norm(const GemmArgs& a, const float* gamma, float eps, f16* xn, hipStream_t st) {
-    if (a.K % 128 != 0 || a.N % 8 != 0 || a.N > 8192 || a.M <= 0 || a.ldo != a.N) return hipErrorInvalidValue;
-    // Split K when the output has too few tiles to fill the CUs: S splits per
-    // tile, at most 8 and at least 8 k-iterations each, within the workspace.
-    const bool wide_k = a.K >= 8192;
-    const int bn = wide_k ? 256 : 128, bm = 128;
+namespace {
+
+// Split K when the output has too few tiles to fill the CUs: S splits per
+// tile, at most 8 and at least 8 k-iterations each, within the workspace;
+// 1 = no split.
+int split_count(const GemmArgs& a) {
+    const int bn = a.K >= 8192 ? 256 : 128, bm = 128;
     const int tiles = ((a.N + bn - 1) / bn) * ((a.M + bm - 1) / bm);
     int S = 1;
     if (a.force_cfg == GCFG_AUTO && a.sk_part && tiles < 160) {
         S = std::min(std::min(SK_P / tiles, 8), a.K / 32 / 8);
         while (S > 1 && (size_t)S * a.M * a.N > a.sk_part_floats) --S;
     }
+    return S;
+}
+
+// K >= 8192 (W2): 256x128 tiles as 8 waves of 16x16x32 (50.3 vs 52.9 us as 4
+// waves of 32x32x16 at 7B, M = 512); otherwise 128x128 (the two forms measure
+// the same there)
+hipError_t launch_split_any(const GemmArgs& a, int S, hipStream_t st) {
+    return a.K >= 8192 ? launch_split<DTile<4, 2, 2, 2, true>>(a, S, st) : launch_split<DTile<2, 2, 2, 2>>(a, S, st);
+}
+
+}  // namespace
+
+hipError_t launch_gemm_partials(const GemmArgs& a, int* nsplit, hipStream_t st) {
+    *nsplit = 0;
+    if (a.K % 128 != 0 || a.N % 8 != 0 || a.M <= 0) return hipErrorInvalidValue;
+    const int S = split_count(a);
+    if (S < 2) return hipSuccess;
+    const hipError_t e = launch_split_any(a, S, st);
+    if (e == hipSuccess) *nsplit = S;
+    return e;
+}
+
+hipError_t launch_gemm_resid_norm(const GemmArgs& a, const float* gamma, float eps, f16* xn, hipStream_t st) {
+    if (a.K % 128 != 0 || a.N % 8 != 0 || a.N > 8192 || a.M <= 0 || a.ldo != a.N) return hipErrorInvalidValue;
+    const int S = split_count(a);
     if (S >= 2) {
-        // K >= 8192 (W2): 256x128 tiles as 8 waves of 16x16x32 (50.3 vs 52.9 us
-        // as 4 waves of 32x32x16 at 7B, M = 512); otherwise 128x128 (the two
-        // forms measure the same there)
-        const hipError_t e = wide_k ? launch_split<DTile<4, 2, 2, 2, true>>(a, S, st)
-                                    : launch_split<DTile<2, 2, 2, 2>>(a, S, st);
+        const hipError_t e = launch_split_any(a, S, st);
         if (e != hipSuccess) return e;
         return launch_resid_norm(a.out_f32, a.sk_part, S, (size_t)a.M * a.N, a.alpha, gamma, eps, xn, a.M,
                                  a.N, st);

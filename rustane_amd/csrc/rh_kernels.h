@@ -78,6 +78,11 @@ hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st);
 // epilogue runs, then the norm.  Needs N % 8 == 0 and N <= 8192.
 hipError_t launch_gemm_resid_norm(const GemmArgs& a, const float* gamma, float eps, f16* xn,
                                   hipStream_t st);
+// X W^T as *nsplit >= 2 fp32 partials [M][N] at a.sk_part + s * M * N, to be
+// summed in split order by the consumer, when the output has too few tiles
+// to fill the CUs (the same split as launch_gemm_resid_norm); otherwise
+// *nsplit = 0 and nothing is launched.  Needs K % 128 == 0, N % 8 == 0.
+hipError_t launch_gemm_partials(const GemmArgs& a, int* nsplit, hipStream_t st);
 
 // ---------------- attention ----------------
 // Causal prefill attention: q [B][H][S][hd], k/v [B][H][ctx][hd] (positions
@@ -172,10 +177,12 @@ hipError_t launch_transpose_frag2(const f16* src0, f16* dst0, int R0, int C0, co
                                   int C1, int Rp, hipStream_t st);
 // RMSNorm backward over M rows: dx = rmsnorm'(x)^T dy (+ dres), optional
 // fp16 fragment-order copy of hscale * dx, per-block dgamma partials
-// [rms_backward_blocks(M)][D].  dx may alias dres.
+// [rms_backward_blocks(M)][D].  dy is the sum of nsplit (1..8) fp32 partials
+// [M][D] split_stride floats apart, added in order.  dx may alias dres.
 int rms_backward_blocks(int M);
-hipError_t launch_rms_backward(const float* dy, const float* x, const float* gamma, const float* dres, float* dx,
-                               f16* outh, float hscale, float* dg_part, int M, int D, float eps, hipStream_t st);
+hipError_t launch_rms_backward(const float* dy, int nsplit, size_t split_stride, const float* x,
+                               const float* gamma, const float* dres, float* dx, f16* outh, float hscale,
+                               float* dg_part, int M, int D, float eps, hipStream_t st);
 // dgamma[d] += kappa * sum_b part[b][d]  (= instead of += when store is set)
 hipError_t launch_dgamma_reduce(const float* part, int nblk, int D, float kappa, float* dgamma, bool store,
                                 hipStream_t st);
@@ -186,12 +193,13 @@ hipError_t launch_rope_backward_pack(const float* dqkv, const float2* rope, f16*
 hipError_t launch_embed_backward(const float* dy, const uint32_t* utok, const int* start, const int* idx, int nuniq,
                                  float kappa, float* dembed, int D, hipStream_t st);
 // Causal attention backward: q, k, v [B][H][S][hd] fp16 (q, k after RoPE), o
-// the forward output (fragment order [B*S][H*hd]), dOf [B*S][H*hd] fp32, lse
-// from the forward.  Workspace dOh (fp16 [B][H][S][hd]) and Drow ([B][H][S]).
+// the forward output (fragment order [B*S][H*hd]), dOf [B*S][H*hd] fp32 as
+// the sum of nsplit (1..8) partials split_stride floats apart, lse from the
+// forward.  Workspace dOh (fp16 [B][H][S][hd]) and Drow ([B][H][S]).
 // Writes dqkv [B*S][3*H*hd] fp32 (dq | dk | dv, before the RoPE backward).
 hipError_t launch_attn_backward(const f16* q, const f16* k, const f16* v, const f16* o, const float* dOf,
-                                const float* lse, f16* dOh, float* Drow, float* dqkv, int B, int H, int S, int hd,
-                                hipStream_t st);
+                                int nsplit, size_t split_stride, const float* lse, f16* dOh, float* Drow,
+                                float* dqkv, int B, int H, int S, int hd, hipStream_t st);
 
 // ---------------- optimizer ----------------
 // One AdamW step (step_fused) with its constants: omb1 = 1 - beta1,

@@ -33,7 +33,9 @@
 namespace rhrt {
 
 struct TrainState {
-    int M = 0, Mp = 0, B = 0, S = 0;  // token capacity; Mp = M rounded up to 128
+    // M: token capacity of the buffers; Mp: this call's token count B * S
+    // rounded up to 128 (the K of the weight-gradient GEMMs, <= capacity's)
+    int M = 0, Mp = 0, B = 0, S = 0;
     uint64_t packs_gen = 0;            // weight version the transposed copies hold
     bool zero = true;  // every gradient is 0: the weight-gradient GEMMs store instead of accumulating
     // fp32 gradients, reference orientation (RSTK order per layer)
@@ -172,6 +174,7 @@ int ensure_train_ws(rh_ctx* ctx, int B, int S) {
     if (M <= T->M) {  // every buffer is indexed with the current B, S: any B*S within capacity fits
         T->B = B;
         T->S = S;
+        T->Mp = (int)round_up((size_t)M, 128);
         return RH_OK;
     }
     HCK(hipStreamSynchronize(ctx->stream));
@@ -342,12 +345,24 @@ int grad_gemm(rh_ctx* ctx, const f16* X, const f16* W, int rows, int cols, float
 }
 
 // out [M][N] fp32 = A W^T with A [M][K] and W [N][K] (fragment order).
-int data_gemm(rh_ctx* ctx, const f16* A, const f16* W, int M, int N, int K, float* out) {
+// As the sum of *nsplit fp32 partials at *parts, M * N floats apart: K split
+// into the stream-K workspace when the output has too few tiles to fill the
+// CUs (the consuming row kernel adds them up, so no fix-up kernel runs),
+// otherwise the whole product in out (*nsplit = 1).
+int data_gemm(rh_ctx* ctx, const f16* A, const f16* W, int M, int N, int K, float* out, const float** parts,
+              int* nsplit) {
     rh::GemmArgs g{};
     g.X = A; g.W = W; g.M = M; g.N = N; g.K = K;
     g.out_f32 = out; g.ldo = N;
     set_sk(ctx, g);
+    LCK(rh::launch_gemm_partials(g, nsplit, ctx->stream));
+    if (*nsplit >= 2) {
+        *parts = ctx->sk_part;
+        return RH_OK;
+    }
     LCK(rh::launch_gemm(rh::EPI_F32, g, ctx->stream));
+    *parts = out;
+    *nsplit = 1;
     return RH_OK;
 }
 
@@ -381,9 +396,12 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
     RCK(publish(4));
     LCK(rh::launch_transpose_frag2(T->dlh, T->dlT, M, Vp, T->xf, T->tx[0][0], M, D, Mp, sd));
     RCK(grad_gemm(ctx, T->dlT, T->tx[0][0], V, D, kappa, T->dembed, sd));
-    RCK(data_gemm(ctx, T->dlh, T->embed_t, M, D, Vp, T->gout));
+    const size_t MD = (size_t)M * D;  // stride of the data-gradient partials
+    const float* dp;
+    int ns;
+    RCK(data_gemm(ctx, T->dlh, T->embed_t, M, D, Vp, T->gout, &dp, &ns));
     // final RMSNorm backward: dy -> dres, a*dy -> H1 (the last layer's dffn)
-    LCK(rh::launch_rms_backward(T->gout, T->xlast, ctx->gfinal, nullptr, T->dres, T->H1, alpha, T->dgp, M, D,
+    LCK(rh::launch_rms_backward(dp, ns, MD, T->xlast, ctx->gfinal, nullptr, T->dres, T->H1, alpha, T->dgp, M, D,
                                 c.rms_eps, st));
     RCK(gamma_grad(ctx, nblk, D, kappa, T->dgf));
     for (int l = c.nlayers - 1; l >= 0; --l) {
@@ -414,10 +432,10 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         HCK(hipEventRecord(T->read[1], sd));
         RCK(grad_gemm(ctx, X1[1], X1[0], D, F, kappa, G[4], sd));
         RCK(grad_gemm(ctx, X1[1], X1[0] + (size_t)F * Mp, D, F, kappa, G[5], sd));
-        RCK(data_gemm(ctx, T->H2, wt.w13t, M, D, 2 * F, T->gout));
+        RCK(data_gemm(ctx, T->H2, wt.w13t, M, D, 2 * F, T->gout, &dp, &ns));
         // dx2 = RMSNorm2'(dx_ffn) + dy (in place in dres); a*dx2 -> H1m
         RCK(rewrite(2));
-        LCK(rh::launch_rms_backward(T->gout, cc.x2, W.g2, T->dres, T->dres, T->H1m, alpha, T->dgp, M, D,
+        LCK(rh::launch_rms_backward(dp, ns, MD, cc.x2, W.g2, T->dres, T->dres, T->H1m, alpha, T->dgp, M, D,
                                     c.rms_eps, st));
         RCK(gamma_grad(ctx, nblk, D, kappa, G[8]));
         // da = (a dx2) Wo^T; dWo += attn^T (a dx2) (side)
@@ -425,11 +443,11 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         LCK(rh::launch_transpose_frag2(T->H1m, X2[0], M, D, cc.attn, X2[1], M, D, Mp, sd));
         HCK(hipEventRecord(T->read[2], sd));
         RCK(grad_gemm(ctx, X2[1], X2[0], D, D, kappa, G[3], sd));
-        RCK(data_gemm(ctx, T->H1m, wt.ot, M, D, D, T->gout));
+        RCK(data_gemm(ctx, T->H1m, wt.ot, M, D, D, T->gout, &dp, &ns));
         // attention backward -> dq | dk | dv, RoPE backward, fp16 pack
-        float* dqkv = T->gout + (size_t)M * D;  // past da, which the attention kernels read
-        LCK(rh::launch_attn_backward(cc.q, cc.k, cc.v, cc.attn, T->gout, cc.lse, T->dOh, T->Drow, dqkv, B, H, S,
-                                     hd, st));
+        float* dqkv = T->gout + MD;  // past da (an unsplit product lands there)
+        LCK(rh::launch_attn_backward(cc.q, cc.k, cc.v, cc.attn, dp, ns, MD, cc.lse, T->dOh, T->Drow, dqkv, B, H,
+                                     S, hd, st));
         RCK(rewrite(3));
         LCK(rh::launch_rope_backward_pack(dqkv, ctx->rope, T->H2q, M, S, D, hd, st));
         // dxn = dqkv [Wq | Wk | Wv]^T; dWq, dWk, dWv += xn^T d{q,k,v} (side)
@@ -438,10 +456,10 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         HCK(hipEventRecord(T->read[3], sd));
         for (int j = 0; j < 3; ++j)
             RCK(grad_gemm(ctx, X3[1], X3[0] + (size_t)j * D * Mp, D, D, kappa, G[j], sd));
-        RCK(data_gemm(ctx, T->H2q, wt.qkvt, M, D, 3 * D, T->gout));
+        RCK(data_gemm(ctx, T->H2q, wt.qkvt, M, D, 3 * D, T->gout, &dp, &ns));
         // dy' = RMSNorm1'(dxn) + dx2 (in place); a*dy' -> H1 (the next layer's dffn)
         RCK(rewrite(0));
-        LCK(rh::launch_rms_backward(T->gout, cc.xin, W.g1, T->dres, T->dres, T->H1, alpha, T->dgp, M, D,
+        LCK(rh::launch_rms_backward(dp, ns, MD, cc.xin, W.g1, T->dres, T->dres, T->H1, alpha, T->dgp, M, D,
                                     c.rms_eps, st));
         RCK(gamma_grad(ctx, nblk, D, kappa, G[7]));
     }

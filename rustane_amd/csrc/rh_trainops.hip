@@ -127,91 +127,120 @@ __global__ __launch_bounds__(256) void transpose_frag_kernel(TransposeJob j0, Tr
 }
 
 // rmsnorm::backward_channel_first (cpu/rmsnorm.rs:185-240) on token-major
-// rows, RB rows per block: r = 1/sqrt(sum(x^2)/D + eps) recomputed from x;
-// x_hat = x*r; dot = sum(dy*g*x_hat)/D; dx = r*(dy*g - x_hat*dot) (+ dres).
-// Writes dx (fp32, may alias dres), optionally hscale*dx as fp16 in fragment
-// order, and this block's dgamma partial sum(dy*x_hat) over its rows.
-constexpr int RB = 2;  // rows per block: M/2 blocks keep enough loads in flight
-__global__ __launch_bounds__(256) void rms_backward_kernel(const float* __restrict__ dy, const float* __restrict__ x,
+// rows: r = 1/sqrt(sum(x^2)/D + eps) recomputed from x; x_hat = x*r;
+// dot = sum(dy*g*x_hat)/D; dx = r*(dy*g - x_hat*dot) (+ dres).  Writes dx
+// (fp32, may alias dres), optionally hscale*dx as fp16 in fragment order,
+// and this block's dgamma partial sum(dy*x_hat) over its rows.  dy is the sum
+// of S split-K partials (split_stride floats apart), added in order.
+// RB = 2 rows per block, one per 256-thread half, so both rows' loads (dres
+// included) are in flight at once; the halves meet only at the barriers of
+// the reductions and for the dgamma partial (second row's terms via LDS).
+// NIT = D / 2048 rounded up: the feature groups of 8 per thread.
+constexpr int RB = 2;
+template <int S, int NIT>
+__global__ __launch_bounds__(512) void rms_backward_kernel(const float* __restrict__ dy, size_t split_stride,
+                                                           const float* __restrict__ x,
                                                            const float* __restrict__ gamma, const float* dres,
                                                            float* dx, f16* __restrict__ outh, float hscale,
                                                            float* __restrict__ dg_part, int M, int D, float eps) {
-    __shared__ float red[4];
-    constexpr int NIT = 4;  // 8 columns x 256 threads x 4 = up to 8192
-    f32x4 gm[NIT][2], dgp[NIT][2];
+    __shared__ float red[2][4];
+    __shared__ __attribute__((aligned(16))) float dgs[NIT * 2048];
+    const int half = threadIdx.x >> 8, t = threadIdx.x & 255, w = t >> 6, lane = t & 63;
+    const int row = blockIdx.x * RB + half;
+    const bool live = row < M;
+    // sum over this half's 4 waves; every thread of the half gets it
+    auto half_sum = [&](float v) {
+        v = wave_sum(v);
+        __syncthreads();
+        if (lane == 0) red[half][w] = v;
+        __syncthreads();
+        return (red[half][0] + red[half][1]) + (red[half][2] + red[half][3]);
+    };
+    const float* xr = x + (size_t)row * D;
+    const float* dr = dy + (size_t)row * D;
+    f32x4 gm[NIT][2], dgp[NIT][2], xv[NIT][2], dv[NIT][2], rv[NIT][2];
+    float ss = 0.f;
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-        const int i = threadIdx.x * 8 + it * 2048;
-        if (i < D) {
-            gm[it][0] = *(const f32x4*)(gamma + i);
-            gm[it][1] = *(const f32x4*)(gamma + i + 4);
-        }
+        const int i = t * 8 + it * 2048;
         dgp[it][0] = dgp[it][1] = f32x4{};
-    }
-    const int rbeg = blockIdx.x * RB, rend = min(M, rbeg + RB);
-    for (int row = rbeg; row < rend; ++row) {
-        const float* xr = x + (size_t)row * D;
-        const float* dr = dy + (size_t)row * D;
-        f32x4 xv[NIT][2], dv[NIT][2];
-        float ss = 0.f;
+        if (live && i < D) {
+            f32x4 p[S][2];
 #pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-            const int i = threadIdx.x * 8 + it * 2048;
-            if (i < D) {
+            for (int sp = 0; sp < S; ++sp)
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    xv[it][hh] = *(const f32x4*)(xr + i + 4 * hh);
-                    dv[it][hh] = *(const f32x4*)(dr + i + 4 * hh);
+                for (int hh = 0; hh < 2; ++hh) p[sp][hh] = *(const f32x4*)(dr + sp * split_stride + i + 4 * hh);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) ss += xv[it][hh][e] * xv[it][hh][e];
-                }
-            }
-        }
-        ss = block_sum_256(ss, red);
-        const float r = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
-        float dot = 0.f;
+            for (int hh = 0; hh < 2; ++hh) {
+                xv[it][hh] = *(const f32x4*)(xr + i + 4 * hh);
+                gm[it][hh] = *(const f32x4*)(gamma + i + 4 * hh);
+                rv[it][hh] = dres ? *(const f32x4*)(dres + (size_t)row * D + i + 4 * hh) : f32x4{};
+                dv[it][hh] = p[0][hh];
 #pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-            const int i = threadIdx.x * 8 + it * 2048;
-            if (i < D) {
+                for (int sp = 1; sp < S; ++sp) dv[it][hh] += p[sp][hh];
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float xh = xv[it][hh][e] * r;
-                        dot += dv[it][hh][e] * gm[it][hh][e] * xh;
-                        dgp[it][hh][e] += dv[it][hh][e] * xh;
-                    }
-            }
-        }
-        dot = block_sum_256(dot, red) * (1.0f / (float)D);
-#pragma unroll
-        for (int it = 0; it < NIT; ++it) {
-            const int i = threadIdx.x * 8 + it * 2048;
-            if (i < D) {
-                f16x8 h;
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    f32x4 o;
-                    const f32x4 rv = dres ? *(const f32x4*)(dres + (size_t)row * D + i + 4 * hh) : f32x4{};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float xh = xv[it][hh][e] * r;
-                        o[e] = r * (dv[it][hh][e] * gm[it][hh][e] - xh * dot) + rv[e];
-                        h[4 * hh + e] = (f16)(o[e] * hscale);
-                    }
-                    *(f32x4*)(dx + (size_t)row * D + i + 4 * hh) = o;
-                }
-                if (outh) *(f16x8*)(outh + frag_off(row, i, D)) = h;
+                for (int e = 0; e < 4; ++e) ss += xv[it][hh][e] * xv[it][hh][e];
             }
         }
     }
+    ss = half_sum(ss);
+    const float r = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
+    float dot = 0.f;
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
-        const int i = threadIdx.x * 8 + it * 2048;
-        if (i < D) {
-            *(f32x4*)(dg_part + (size_t)blockIdx.x * D + i) = dgp[it][0];
-            *(f32x4*)(dg_part + (size_t)blockIdx.x * D + i + 4) = dgp[it][1];
+        const int i = t * 8 + it * 2048;
+        if (live && i < D) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float xh = xv[it][hh][e] * r;
+                    dot += dv[it][hh][e] * gm[it][hh][e] * xh;
+                    dgp[it][hh][e] += dv[it][hh][e] * xh;
+                }
+        }
+    }
+    dot = half_sum(dot) * (1.0f / (float)D);
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int i = t * 8 + it * 2048;
+        if (live && i < D) {
+            f16x8 h;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                f32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float xh = xv[it][hh][e] * r;
+                    o[e] = r * (dv[it][hh][e] * gm[it][hh][e] - xh * dot) + rv[it][hh][e];
+                    h[4 * hh + e] = (f16)(o[e] * hscale);
+                }
+                *(f32x4*)(dx + (size_t)row * D + i + 4 * hh) = o;
+            }
+            if (outh) *(f16x8*)(outh + frag_off(row, i, D)) = h;
+        }
+    }
+    // dgamma partial of the block: first row's terms + second row's (zero
+    // when the second row is past M)
+    if (half == 1) {
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int i = t * 8 + it * 2048;
+            if (i < D) {
+                *(f32x4*)(dgs + i) = dgp[it][0];
+                *(f32x4*)(dgs + i + 4) = dgp[it][1];
+            }
+        }
+    }
+    __syncthreads();
+    if (half == 0) {
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int i = t * 8 + it * 2048;
+            if (i < D) {
+                *(f32x4*)(dg_part + (size_t)blockIdx.x * D + i) = dgp[it][0] + *(const f32x4*)(dgs + i);
+                *(f32x4*)(dg_part + (size_t)blockIdx.x * D + i + 4) = dgp[it][1] + *(const f32x4*)(dgs + i + 4);
+            }
         }
     }
 }
@@ -312,11 +341,23 @@ hipError_t launch_transpose_frag2(const f16* src0, f16* dst0, int R0, int C0, co
 
 int rms_backward_blocks(int M) { return (M + RB - 1) / RB; }
 
-hipError_t launch_rms_backward(const float* dy, const float* x, const float* gamma, const float* dres, float* dx,
-                               f16* outh, float hscale, float* dg_part, int M, int D, float eps, hipStream_t st) {
-    if (D % 8 != 0 || D > 8192) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rms_backward_kernel, dim3(rms_backward_blocks(M)), dim3(256), 0, st, dy, x, gamma, dres, dx,
-                       outh, hscale, dg_part, M, D, eps);
+hipError_t launch_rms_backward(const float* dy, int nsplit, size_t split_stride, const float* x,
+                               const float* gamma, const float* dres, float* dx, f16* outh, float hscale,
+                               float* dg_part, int M, int D, float eps, hipStream_t st) {
+    if (D % 8 != 0 || D > 8192 || nsplit < 1 || nsplit > 8) return hipErrorInvalidValue;
+#define RH_RB(S_)                                                                                             \
+    case S_:                                                                                                  \
+        if (D <= 4096)                                                                                        \
+            hipLaunchKernelGGL((rms_backward_kernel<S_, 2>), dim3(rms_backward_blocks(M)), dim3(512), 0, st,   \
+                               dy, split_stride, x, gamma, dres, dx, outh, hscale, dg_part, M, D, eps);       \
+        else                                                                                                  \
+            hipLaunchKernelGGL((rms_backward_kernel<S_, 4>), dim3(rms_backward_blocks(M)), dim3(512), 0, st,   \
+                               dy, split_stride, x, gamma, dres, dx, outh, hscale, dg_part, M, D, eps);       \
+        break
+    switch (nsplit) {
+        RH_RB(1); RH_RB(2); RH_RB(3); RH_RB(4); RH_RB(5); RH_RB(6); RH_RB(7); RH_RB(8);
+    }
+#undef RH_RB
     return hipGetLastError();
 }
 
