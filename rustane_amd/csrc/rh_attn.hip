@@ -246,16 +246,6 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
 //     group g therefore reads hd 16j + 4(l % 4) .. +3 of key 32c + 8g + 4h +
 //     (l % 16) / 4, and gets V[32c + 8g + 4h + e][16j + l % 16] for e = 0..3:
 //     two reads (h = 0, 1) make the 8-key k slice of the O^T MFMA's A operand.
-__device__ __forceinline__ int swz_k(int row) { return (row & 3) | (((row >> 3) & 3) << 2); }
-__device__ __forceinline__ int swz_v(int row) { return ((row & 3) << 1) | (((row >> 3) & 1) << 3); }
-
-// s_waitcnt vmcnt(n), other counters left at their maximum
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // NG = 2: two groups of 4 waves share the block's 64 queries and split its
 // key blocks (group G takes blocks G, G + 2, ...), each through its own half

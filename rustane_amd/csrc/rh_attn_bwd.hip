@@ -231,6 +231,254 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const f16* __restric
     }
 }
 
+// hd 128: the same two kernels with their operand tiles moved global -> LDS
+// by DMA (global_load_lds_dwordx4, 16 bytes per lane at LDS base + 16 lane)
+// through a two-stage pipeline, so the next tile's loads are in flight while
+// this one is computed and no VGPRs or LDS stores stage them.  Tiles keep
+// their natural [row][hd] order (256-byte rows) with the XOR chunk swizzles
+// of the forward kernel: a tile read as row fragments (an A operand with
+// rows = keys or queries) is stored with swz_k, one read transposed (K^T,
+// Q^T, dO^T) with swz_v and read by ds_read_b64_tr_b16, so K (dq) and Q, dO
+// (dk/dv) are moved twice, once per swizzle.  The MFMA operands and their
+// order are those of the kernels above, so the results are identical.
+//
+// Wave w moves 1 KB units w, w + 4, w + 8, w + 12 of a 64-row tile (unit i
+// holds rows 4i..4i+3; lane L row 4i + L/16 and stored chunk L%16).
+__device__ __forceinline__ void dma_tile(const f16* __restrict__ base, int r0, int S, f16* dst, bool tr) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int i = w + 4 * t, row = 4 * i + (lane >> 4);
+        const int sw = tr ? swz_v(row) : swz_k(row);
+        const f16* src = base + (size_t)min(r0 + row, S - 1) * 128 + 8 * ((lane & 15) ^ sw);
+        __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(dst + i * 512),
+                                         16, 0, 0);
+    }
+}
+
+// Row fragment of a swz_k tile: 8 hd values 32kk + 8g .. +7 of row `row`.
+__device__ __forceinline__ f16x8 tile_row(const f16* t, int row, int kk, int g) {
+    return *(const f16x8*)&t[row * 128 + 8 * ((4 * kk + g) ^ swz_k(row))];
+}
+
+// Transposed fragment of a swz_v tile: element e = T[32c + 8g + e][16j + r]
+// (rows of the tile as the k dimension), from two transposing reads.
+__device__ __forceinline__ f16x8 tile_tr(const f16* t, int c, int j, int lane) {
+    const int g = (lane >> 4) & 3, r = lane & 15, ch = 2 * j + ((lane & 3) >> 1);
+    f16x8 out;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const int row = 32 * c + 8 * g + 4 * hh + (r >> 2);
+        const f16* a = &t[row * 128 + 8 * (ch ^ swz_v(row)) + 4 * (lane & 1)];
+        const f16x4 v = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                      (__attribute__((address_space(3))) s16x4*)a));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[4 * hh + e] = v[e];
+    }
+    return out;
+}
+
+__global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
+                                                              const f16* __restrict__ V, const f16* __restrict__ dO,
+                                                              const float* __restrict__ lse,
+                                                              const float* __restrict__ Drow,
+                                                              float* __restrict__ dqkv, int H, int S,
+                                                              float scale_log2, float scale) {
+    constexpr int HD = 128, KB = 64, NKK = HD / 32, NHT = HD / 16, TILE = KB * HD;
+    // one array per stage and role, so the compiler's wait-count tracking
+    // tells a stage's reads from the DMA filling the other stage
+    __shared__ __attribute__((aligned(1024))) f16 sK0[TILE], sV0[TILE], sKt0[TILE], sK1[TILE], sV1[TILE],
+        sKt1[TILE];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r = lane & 15;
+    const int nqt = (S + 63) / 64;
+    const int t = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int qt = nqt - 1 - t % nqt;  // longest rows first
+    const int h = (t / nqt) % H, b = t / nqt / H;
+    const int q0 = qt * 64, qi = q0 + w * 16 + r, qrow = min(qi, S - 1);
+    const size_t bh = (size_t)b * H + h;
+    const f16* Kb = K + bh * S * HD;
+    const f16* Vb = V + bh * S * HD;
+    f16x8 qf[NKK], df[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+        qf[kk] = *(const f16x8*)(Q + (bh * S + qrow) * HD + 32 * kk + 8 * g);
+        df[kk] = *(const f16x8*)(dO + (bh * S + qrow) * HD + 32 * kk + 8 * g);
+    }
+    const float L = lse[bh * S + qrow], Dq = Drow[bh * S + qrow];
+    f32x4 acc[NHT];
+#pragma unroll
+    for (int j = 0; j < NHT; ++j) acc[j] = f32x4{};
+    const int nkb = (min(S, q0 + 64) + KB - 1) / KB;
+    auto issue = [&](int kb, auto ST) {
+        constexpr int st = decltype(ST)::value;
+        dma_tile(Kb, kb * KB, S, st ? sK1 : sK0, false);
+        dma_tile(Vb, kb * KB, S, st ? sV1 : sV0, false);
+        dma_tile(Kb, kb * KB, S, st ? sKt1 : sKt0, true);
+    };
+    auto step = [&](int kb, auto ST) {
+        constexpr int cur = decltype(ST)::value;
+        const int k0 = kb * KB;
+        // this wave's DMAs of tile kb have landed (nothing else is in flight);
+        // the barrier publishes every wave's and retires every wave's reads of
+        // tile kb - 1, whose stage the next issue refills
+        wait_vm<0>();
+        lds_barrier();
+        if (kb + 1 < nkb) issue(kb + 1, std::integral_constant<int, 1 - cur>{});
+        const f16* sK = cur ? sK1 : sK0;
+        const f16* sV = cur ? sV1 : sV0;
+        const f16* sKt = cur ? sKt1 : sKt0;
+        f32x4 sc[2][2], dp[2][2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                sc[c][u] = f32x4{};
+                dp[c][u] = f32x4{};
+                const int krow = 32 * c + 8 * (r >> 2) + 4 * u + (r & 3);
+#pragma unroll
+                for (int kk = 0; kk < NKK; ++kk) {
+                    sc[c][u] = mfma16(tile_row(sK, krow, kk, g), qf[kk], sc[c][u]);
+                    dp[c][u] = mfma16(tile_row(sV, krow, kk, g), df[kk], dp[c][u]);
+                }
+            }
+        const int lim = qrow - k0 - 8 * g;  // key offsets above lim are masked (or past S)
+        f16x8 dsf[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const bool live = 32 * c + 4 * u + i <= lim;
+                    const float p = live ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[c][u][i], scale_log2, -L)) : 0.f;
+                    dsf[c][4 * u + i] = (f16)(p * (dp[c][u][i] - Dq));
+                }
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int j = 0; j < NHT; ++j) acc[j] = mfma16(tile_tr(sKt, c, j, lane), dsf[c], acc[j]);
+    };
+    issue(0, std::integral_constant<int, 0>{});
+    for (int kb0 = 0; kb0 < nkb; kb0 += 2) {
+        step(kb0, std::integral_constant<int, 0>{});
+        if (kb0 + 1 < nkb) step(kb0 + 1, std::integral_constant<int, 1>{});
+    }
+    if (qi < S) {
+        float* dst = dqkv + (size_t)(b * S + qi) * (3 * H * HD) + h * HD + 4 * g;
+#pragma unroll
+        for (int j = 0; j < NHT; ++j) *(f32x4*)(dst + 16 * j) = acc[j] * scale;
+    }
+}
+
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_dma_kernel(const f16* __restrict__ Q,
+                                                                const f16* __restrict__ K,
+                                                                const f16* __restrict__ V,
+                                                                const f16* __restrict__ dO,
+                                                                const float* __restrict__ lse,
+                                                                const float* __restrict__ Drow,
+                                                                float* __restrict__ dqkv, int H, int S,
+                                                                float scale_log2, float scale) {
+    constexpr int HD = 128, QB = 64, NKK = HD / 32, NHT = HD / 16, TILE = QB * HD;
+    __shared__ __attribute__((aligned(1024))) f16 sQ0[TILE], sO0[TILE], sQt0[TILE], sOt0[TILE], sQ1[TILE],
+        sO1[TILE], sQt1[TILE], sOt1[TILE];
+    __shared__ __attribute__((aligned(256))) float sL0[QB], sD0[QB], sL1[QB], sD1[QB];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, r = lane & 15;
+    const int nkt = (S + 63) / 64;
+    const int t = xcd_remap((int)blockIdx.x, (int)gridDim.x);  // a head's tiles share an XCD's L2
+    const int kt = t % nkt;  // the first key blocks see the most queries: launched first
+    const int h = (t / nkt) % H, b = t / nkt / H;
+    const int k0 = kt * 64, ki = k0 + w * 16 + r, krow = min(ki, S - 1);
+    const size_t bh = (size_t)b * H + h;
+    const f16* Qb = Q + bh * S * HD;
+    const f16* dOb = dO + bh * S * HD;
+    f16x8 kf[NKK], vf[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+        kf[kk] = *(const f16x8*)(K + (bh * S + krow) * HD + 32 * kk + 8 * g);
+        vf[kk] = *(const f16x8*)(V + (bh * S + krow) * HD + 32 * kk + 8 * g);
+    }
+    f32x4 dk[NHT], dv[NHT];
+#pragma unroll
+    for (int j = 0; j < NHT; ++j) dk[j] = dv[j] = f32x4{};
+    const int nqb = (S + QB - 1) / QB;
+    auto issue = [&](int qb, auto ST) {
+        constexpr int st = decltype(ST)::value;
+        const int q0 = qb * QB;
+        dma_tile(Qb, q0, S, st ? sQ1 : sQ0, false);
+        dma_tile(dOb, q0, S, st ? sO1 : sO0, false);
+        dma_tile(Qb, q0, S, st ? sQt1 : sQt0, true);
+        dma_tile(dOb, q0, S, st ? sOt1 : sOt0, true);
+        // the 64 queries' lse and D, 4 bytes per lane (every wave writes the
+        // same values, so each wave's DMA count stays the same)
+        const size_t qv = bh * S + min(q0 + lane, S - 1);
+        __builtin_amdgcn_global_load_lds((const void*)(lse + qv), (__attribute__((address_space(3))) void*)(st ? sL1 : sL0),
+                                         4, 0, 0);
+        __builtin_amdgcn_global_load_lds((const void*)(Drow + qv), (__attribute__((address_space(3))) void*)(st ? sD1 : sD0),
+                                         4, 0, 0);
+    };
+    auto step = [&](int qb, auto ST) {
+        constexpr int cur = decltype(ST)::value;
+        const int q0 = qb * QB;
+        wait_vm<0>();
+        lds_barrier();
+        if (qb + 1 < nqb) issue(qb + 1, std::integral_constant<int, 1 - cur>{});
+        const f16* sQ = cur ? sQ1 : sQ0;
+        const f16* sO = cur ? sO1 : sO0;
+        const f16* sQt = cur ? sQt1 : sQt0;
+        const f16* sOt = cur ? sOt1 : sOt0;
+        const float* sL = cur ? sL1 : sL0;
+        const float* sD = cur ? sD1 : sD0;
+        f32x4 s[2][2], dp[2][2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                s[c][u] = f32x4{};
+                dp[c][u] = f32x4{};
+                const int qr = 32 * c + 8 * (r >> 2) + 4 * u + (r & 3);
+#pragma unroll
+                for (int kk = 0; kk < NKK; ++kk) {
+                    s[c][u] = mfma16(tile_row(sQ, qr, kk, g), kf[kk], s[c][u]);
+                    dp[c][u] = mfma16(tile_row(sO, qr, kk, g), vf[kk], dp[c][u]);
+                }
+            }
+        f16x8 pf[2], dsf[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int qo = 32 * c + 8 * g + 4 * u + i, q = q0 + qo;
+                    const bool live = q >= ki && q < S;
+                    const float p = live ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[c][u][i], scale_log2, -sL[qo])) : 0.f;
+                    pf[c][4 * u + i] = (f16)p;
+                    dsf[c][4 * u + i] = (f16)(p * (dp[c][u][i] - sD[qo]));
+                }
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int j = 0; j < NHT; ++j) {
+                dv[j] = mfma16(tile_tr(sOt, c, j, lane), pf[c], dv[j]);
+                dk[j] = mfma16(tile_tr(sQt, c, j, lane), dsf[c], dk[j]);
+            }
+    };
+    issue(kt, std::integral_constant<int, 0>{});
+    for (int qb0 = kt; qb0 < nqb; qb0 += 2) {
+        step(qb0, std::integral_constant<int, 0>{});
+        if (qb0 + 1 < nqb) step(qb0 + 1, std::integral_constant<int, 1>{});
+    }
+    if (ki < S) {
+        const int D = H * HD;
+        float* dst = dqkv + (size_t)(b * S + ki) * (3 * D) + h * HD + 4 * g;
+#pragma unroll
+        for (int j = 0; j < NHT; ++j) {
+            *(f32x4*)(dst + D + 16 * j) = dk[j] * scale;
+            *(f32x4*)(dst + 2 * D + 16 * j) = dv[j];
+        }
+    }
+}
+
 // dO [M, H*hd] fp32 (token-major GEMM output, the sum of NS split-K
 // partials split_stride floats apart, added in order) -> fp16 [B][H][S][hd],
 // and D[b][h][s] = sum_d dO * O with O the forward's attention output
@@ -306,9 +554,9 @@ hipError_t launch_attn_backward(const f16* q, const f16* k, const f16* v, const 
     const dim3 grid((S + 63) / 64 * H * B);
     const float scale = 1.0f / sqrtf((float)hd), sl2 = scale * 1.4426950408889634f;
     if (hd == 128) {
-        hipLaunchKernelGGL((attn_bwd_dq_kernel<128>), grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S,
-                           sl2, scale);
-        hipLaunchKernelGGL((attn_bwd_dkdv_kernel<128>), grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S,
+        hipLaunchKernelGGL(attn_bwd_dq_dma_kernel, grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S, sl2,
+                           scale);
+        hipLaunchKernelGGL(attn_bwd_dkdv_dma_kernel, grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S,
                            sl2, scale);
     } else {
         hipLaunchKernelGGL((attn_bwd_dq_kernel<64>), grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S,

@@ -73,6 +73,22 @@ __device__ __forceinline__ void lds_barrier() {
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 
+// XOR swizzles of the 16-byte chunks of a 256-byte LDS row (an hd-128 fp16
+// K / V / Q / dO row staged by DMA): chunk c of row k is stored at
+// c ^ swz(k).  swz_k keeps the row-fragment reads of a 16x16x32 A operand
+// (rows 8(r/4) + 4u + r%4, chunk 4kk + g) on distinct banks, swz_v the
+// transposing reads (ds_read_b64_tr_b16) of keys 8g + 4h + r/4.
+__device__ __forceinline__ int swz_k(int row) { return (row & 3) | (((row >> 3) & 3) << 2); }
+__device__ __forceinline__ int swz_v(int row) { return ((row & 3) << 1) | (((row >> 3) & 1) << 3); }
+
+// s_waitcnt vmcnt(n), other counters left at their maximum
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
 // Fragment order of a [N, K] fp16 weight (rows padded to a multiple of 16,
 // K a multiple of 128): 16-row x 128-k chunks, each stored as four 1 KB
 // fragments (k/32 % 4) of 64 lanes x 8 halves, lane = 16 * (k/8 % 4) + row % 16.

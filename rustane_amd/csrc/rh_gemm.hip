@@ -619,6 +619,98 @@ hipError_t launch_split(const GemmArgs& a, int S, hipStream_t st) {
     return hipGetLastError();
 }
 
+// Weight-gradient GEMM (K = the token count, short; fp32 output, as large
+// as the weights): persistent blocks of 8 compute waves running the 8-wave
+// 16x16x32 128x128 DTile k loop and WG_SW store waves.  A tile's
+// accumulators go to an LDS staging tile; the store waves write it out to
+// HBM while the compute waves run the next tile, so the output stores
+// overlap the MFMAs.  The compute waves issue no stores at all: on gfx950
+// stores and the operand DMAs share one in-order vmcnt, so stores in the
+// compute waves would make every later stage wait hold for them.
+//
+// Barriers: every wave of the block executes the same s_barrier sequence.
+// Per tile the compute waves run Tl::run (2 + NS * ceil(KT / NS) barriers),
+// then X (the store waves are done reading the staging tile), write the
+// staging tile, then Y (published).  The store waves mirror that count,
+// storing the previous tile in 16 rounds spread over the k loop's barriers,
+// and the block's last tile after its Y.
+//
+// Tiles: block b runs on XCD b % 8 and takes every (gridDim / 8)-th tile of
+// that XCD's contiguous share; tiles are numbered in groups of 8 M-tiles x all
+// N panels (so 32 tiles in flight on an XCD span 4 panels x 8 M-tiles).
+constexpr int WG_SW = 4;     // store waves
+constexpr int WG_SP = 132;   // staging row pitch in floats (conflict-free b128 access)
+template <class Tl, bool ACC>
+__global__ __launch_bounds__(Tl::NT + 64 * WG_SW) void gemm_wgrad_kernel(GemmArgs a) {
+    static_assert(Tl::kM16 && Tl::BN == 128 && Tl::BM == 128 && Tl::NWAVE == 8, "8-wave 128x128 tile");
+    __shared__ __attribute__((aligned(16))) float stg[128 * WG_SP];
+    typename Tl::Smem sm;
+    const int nbN = (a.N + 127) / 128, nbM = (a.M + 127) / 128, T = nbN * nbM;
+    const int KT = a.K / Tl::KI;
+    const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3, per = gridDim.x >> 3;
+    const int t0 = (int)((long long)xcd * T / 8), t1 = (int)((long long)(xcd + 1) * T / 8);
+    const int mine = (t1 - t0 > k) ? (t1 - t0 - k + per - 1) / per : 0;
+    const int nbar = 2 + Tl::NS * ((KT + Tl::NS - 1) / Tl::NS);  // barriers of one Tl::run
+    auto tile_at = [&](int i, int& n0, int& m0) {
+        const int t = t0 + k + i * per;
+        const int mg = t / (nbN * 8), rem = t - mg * nbN * 8, gsz = min(8, nbM - mg * 8);
+        n0 = (rem / gsz) * 128;
+        m0 = (mg * 8 + rem % gsz) * 128;
+    };
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wv < Tl::NWAVE) {
+        typename Tl::Acc acc;
+        for (int i = 0; i < mine; ++i) {
+            int n0, m0;
+            tile_at(i, n0, m0);
+            Tl::run(a, n0, m0, 0, KT, acc, sm);
+            __builtin_amdgcn_s_barrier();  // X
+            const int nl = Tl::nw(n0) - n0, ml = Tl::mw(m0) - m0;
+#pragma unroll
+            for (int i2 = 0; i2 < Tl::NA; ++i2)
+#pragma unroll
+                for (int j = 0; j < Tl::NB; ++j)
+                    *(f32x4*)&stg[(ml + 16 * j + (lane & 15)) * WG_SP + nl + 16 * i2 + 4 * (lane >> 4)] = acc.v[i2][j];
+            lds_barrier();  // Y
+        }
+    } else {
+        const int sw = wv - Tl::NWAVE;
+        int pn0 = 0, pm0 = 0;  // the staged tile
+        // round r: rows 2 (4r + sw) + lane / 32 of the staged tile, 4 columns per lane
+        auto store_round = [&](int r) {
+            const int ml = 2 * (WG_SW * r + sw) + (lane >> 5), nl = 4 * (lane & 31);
+            const int m = pm0 + ml, n = pn0 + nl;
+            if (m < a.M && n < a.N) {
+                f32x4 v = *(const f32x4*)&stg[ml * WG_SP + nl];
+                float* po = a.out_f32 + (size_t)m * a.ldo + n;
+                if constexpr (ACC) {
+                    f32x4 x = *(const f32x4*)po;
+                    x[0] = v[0] * a.alpha + x[0]; x[1] = v[1] * a.alpha + x[1];
+                    x[2] = v[2] * a.alpha + x[2]; x[3] = v[3] * a.alpha + x[3];
+                    v = x;
+                } else if (a.alpha != 0.f) {
+                    v[0] *= a.alpha; v[1] *= a.alpha; v[2] *= a.alpha; v[3] *= a.alpha;
+                }
+                *(f32x4*)po = v;
+            }
+        };
+        constexpr int NR = 128 / (2 * WG_SW);  // rounds per tile
+        for (int i = 0; i < mine; ++i) {
+            for (int bar = 0; bar < nbar; ++bar) {
+                __builtin_amdgcn_s_barrier();
+                if (i > 0)
+                    for (int r = bar * NR / nbar; r < (bar + 1) * NR / nbar; ++r) store_round(r);
+            }
+            __builtin_amdgcn_s_waitcnt(Tl::vm_lgkm_wait(63));  // staging reads done before X
+            __builtin_amdgcn_s_barrier();  // X
+            __builtin_amdgcn_s_barrier();  // Y
+            tile_at(i, pn0, pm0);
+        }
+        if (mine > 0)
+            for (int r = 0; r < NR; ++r) store_round(r);
+    }
+}
+
 template <int EPI>
 hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
     int cfg = a.force_cfg;
@@ -689,6 +781,17 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
 }  // namespace
 
 size_t gemm_sk_part_floats() { return (size_t)SK_P * 2 * 256 * 256; }
+
+hipError_t launch_gemm_wgrad(const GemmArgs& a, bool accumulate, hipStream_t st) {
+    if (a.K % 128 != 0 || a.N % 4 != 0 || a.M <= 0 || a.N <= 0 || a.ldo < a.N || !a.out_f32)
+        return hipErrorInvalidValue;
+    using Tl = DTile<2, 4, 2, 1, true>;
+    if (accumulate)
+        hipLaunchKernelGGL((gemm_wgrad_kernel<Tl, true>), dim3(SK_P), dim3(Tl::NT + 64 * WG_SW), 0, st, a);
+    else
+        hipLaunchKernelGGL((gemm_wgrad_kernel<Tl, false>), dim3(SK_P), dim3(Tl::NT + 64 * WG_SW), 0, st, a);
+    return hipGetLastError();
+}
 
 namespace {
 

@@ -164,4 +164,29 @@ int rhh_gemm_resid_norm(int cfg, const uint16_t* wf, const uint16_t* xf, int M, 
     return 0;
 }
 
+// Weight-gradient GEMM (launch_gemm_wgrad): io_f32 [M][N] = alpha * (X W^T)
+// (alpha 0: unscaled), or io_f32 += alpha * (X W^T) when accumulate.
+int rhh_gemm_wgrad(const uint16_t* wf, const uint16_t* xf, int M, int N, int K, float alpha, int accumulate,
+                   float* io_f32) {
+    if (M <= 0 || N <= 0 || K <= 0 || !wf || !xf || !io_f32) return -1;
+    Dev d;
+    const size_t wn = (size_t)up16(N) * K, xn = (size_t)up16(M) * K;
+    f16* W = d.alloc<f16>(wn);
+    f16* X = d.alloc<f16>(xn);
+    float* of = d.alloc<float>((size_t)M * N);
+    if (!W || !X || !of) return -1;
+    if (hipMemcpy(W, wf, wn * 2, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(X, xf, xn * 2, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(of, io_f32, (size_t)M * N * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return -1;
+    rh::GemmArgs a{};
+    a.W = W; a.X = X; a.M = M; a.N = N; a.K = K;
+    a.out_f32 = of; a.ldo = N; a.alpha = alpha;
+    hipError_t e = rh::launch_gemm_wgrad(a, accumulate != 0, nullptr);
+    if (e != hipSuccess) return (int)e;
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return (int)e;
+    if (hipMemcpy(io_f32, of, (size_t)M * N * 4, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    return 0;
+}
+
 }  // extern "C"

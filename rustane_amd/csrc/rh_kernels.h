@@ -83,6 +83,11 @@ hipError_t launch_gemm_resid_norm(const GemmArgs& a, const float* gamma, float e
 // to fill the CUs (the same split as launch_gemm_resid_norm); otherwise
 // *nsplit = 0 and nothing is launched.  Needs K % 128 == 0, N % 8 == 0.
 hipError_t launch_gemm_partials(const GemmArgs& a, int* nsplit, hipStream_t st);
+// Weight-gradient GEMM for a short K (the token count): out [M][ldo] fp32 =
+// alpha * X W^T (alpha 0: unscaled), or += when accumulate; persistent blocks
+// whose store waves write each 128x128 tile while the next one is computed.
+// Needs K % 128 == 0, N % 4 == 0.
+hipError_t launch_gemm_wgrad(const GemmArgs& a, bool accumulate, hipStream_t st);
 
 // ---------------- attention ----------------
 // Causal prefill attention: q [B][H][S][hd], k/v [B][H][ctx][hd] (positions

@@ -333,6 +333,10 @@ int grad_gemm(rh_ctx* ctx, const f16* X, const f16* W, int rows, int cols, float
     g.X = X; g.W = W; g.M = rows; g.N = cols; g.K = ctx->train->Mp;
     g.out_f32 = out; g.ldo = cols; g.alpha = kappa;
     const bool long_k = g.K >= 8192;
+    if (ctx->train->zero && g.K <= 1024 && (size_t)rows * cols > (size_t)4096 * 4096) {
+        LCK(rh::launch_gemm_wgrad(g, false, st));
+        return RH_OK;
+    }
     if (cols > 4096)
         g.force_cfg = rh::GCFG_D8_192x256;
     else if (rows > 4096)

@@ -44,6 +44,8 @@ def lib():
     h.rhh_gemm.restype = i
     h.rhh_gemm_resid_norm.argtypes = [i, p, p, i, i, i, f, p, p, f, p]
     h.rhh_gemm_resid_norm.restype = i
+    h.rhh_gemm_wgrad.argtypes = [p, p, i, i, i, f, i, p]
+    h.rhh_gemm_wgrad.restype = i
     return h
 
 
@@ -228,3 +230,24 @@ def test_residual_then_rmsnorm(lib, cfg, K):
     close(io, x1, 1e-5, "residual")
     xn_ref = x1 / np.sqrt((x1 * x1).mean(1, keepdims=True) + eps) * gamma
     close(frag_unpack(xn, M, N), xn_ref, 2e-3, "rmsnorm output")
+
+
+# Weight-gradient GEMM (persistent blocks, store waves draining an LDS-staged
+# tile): few tiles (XCDs without a tile), ragged edges, more tiles than blocks
+# (several per block), K from 128 to 2048 (the token count), store with and
+# without a scale and accumulate.
+@pytest.mark.parametrize("M,N,K", [(100, 60, 128), (300, 1000, 384), (1100, 2060, 512), (4096, 1100, 640),
+                                   (640, 384, 2048)])
+def test_weight_gradient_gemm(lib, M, N, K):
+    x, w, y = operands(11, M, N, K)
+    xf, wf = frag_pack(x), frag_pack(w)
+    out = np.full((M, N), np.nan, np.float32)  # every element must be written
+    assert lib.rhh_gemm_wgrad(ptr(wf), ptr(xf), M, N, K, 0.0, 0, ptr(out)) == 0
+    close(out, y, 1e-5, "store")
+    out = np.zeros((M, N), np.float32)
+    assert lib.rhh_gemm_wgrad(ptr(wf), ptr(xf), M, N, K, 0.25, 0, ptr(out)) == 0
+    close(out, 0.25 * y, 1e-5, "scaled store")
+    x0 = np.random.default_rng(12).standard_normal((M, N)).astype(np.float32)
+    io = x0.copy()
+    assert lib.rhh_gemm_wgrad(ptr(wf), ptr(xf), M, N, K, 0.5, 1, ptr(io)) == 0
+    close(io, x0.astype(np.float64) + 0.5 * y, 1e-5, "accumulate")
