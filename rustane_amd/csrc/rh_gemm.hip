@@ -284,8 +284,9 @@ __device__ __forceinline__ void store4(const GemmArgs& a, int m, int n, float v0
         }
         *(f32x4*)(a.out_f32 + (size_t)m * a.ldo + n) = f32x4{v0, v1, v2, v3};
     } else if constexpr (EPI == EPI_RESID) {
-        f32x4* px = (f32x4*)(a.out_f32 + (size_t)m * a.ldo + n);
-        f32x4 x = *px;
+        const size_t o = (size_t)m * a.ldo + n;
+        f32x4* px = (f32x4*)(a.out_f32 + o);
+        f32x4 x = *(const f32x4*)((a.resid_in ? a.resid_in : a.out_f32) + o);
         x[0] = v0 * a.alpha + x[0]; x[1] = v1 * a.alpha + x[1];
         x[2] = v2 * a.alpha + x[2]; x[3] = v3 * a.alpha + x[3];
         *px = x;
@@ -834,8 +835,8 @@ hipError_t launch_gemm_resid_norm(const GemmArgs& a, const float* gamma, float e
     if (S >= 2) {
         const hipError_t e = launch_split_any(a, S, st);
         if (e != hipSuccess) return e;
-        return launch_resid_norm(a.out_f32, a.sk_part, S, (size_t)a.M * a.N, a.alpha, gamma, eps, xn, a.M,
-                                 a.N, st);
+        return launch_resid_norm(a.resid_in ? a.resid_in : a.out_f32, a.out_f32, a.sk_part, S, (size_t)a.M * a.N,
+                                 a.alpha, gamma, eps, xn, a.M, a.N, st);
     }
     const hipError_t e = launch_epi<EPI_RESID>(a, st);
     if (e != hipSuccess || !gamma) return e;

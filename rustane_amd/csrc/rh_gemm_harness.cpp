@@ -130,29 +130,33 @@ int rhh_gemm(int epi, int cfg, const uint16_t* wf, const uint16_t* xf, int M, in
 
 // Residual GEMM + RMSNorm as the forward runs it after Wo and W2: x += alpha *
 // (X W^T), then xn = RMSNorm(x) * gamma in fragment order ([ceil(M/16)*16][N]
-// halves).  cfg 0 takes the split-K path when the output has few tiles.
+// halves).  With xin set the residual is read from there (out of place, as
+// the training forward runs it) and x only written.  cfg 0 takes the split-K
+// path when the output has few tiles.
 int rhh_gemm_resid_norm(int cfg, const uint16_t* wf, const uint16_t* xf, int M, int N, int K, float alpha,
-                        float* x, const float* gamma, float eps, uint16_t* xn_out) {
+                        const float* xin, float* x, const float* gamma, float eps, uint16_t* xn_out) {
     if (M <= 0 || N <= 0 || K <= 0 || !wf || !xf || !x || !gamma || !xn_out) return -1;
     Dev d;
     const size_t wn = (size_t)up16(N) * K, xn = (size_t)up16(M) * K, on = (size_t)up16(M) * N;
     f16* W = d.alloc<f16>(wn);
     f16* X = d.alloc<f16>(xn);
     float* dx = d.alloc<float>((size_t)M * N);
+    float* dxin = xin ? d.alloc<float>((size_t)M * N) : nullptr;
     float* dg = d.alloc<float>(N);
     f16* dxn = d.alloc<f16>(on);
     const size_t skf = rh::gemm_sk_part_floats();
     float* sk = d.alloc<float>(skf);
-    if (!W || !X || !dx || !dg || !dxn || !sk) return -1;
+    if (!W || !X || !dx || !dg || !dxn || !sk || (xin && !dxin)) return -1;
     if (hipMemcpy(W, wf, wn * 2, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(X, xf, xn * 2, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(dx, x, (size_t)M * N * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        (xin && hipMemcpy(dxin, xin, (size_t)M * N * 4, hipMemcpyHostToDevice) != hipSuccess) ||
         hipMemcpy(dg, gamma, (size_t)N * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemset(dxn, 0, on * 2) != hipSuccess)
         return -1;
     rh::GemmArgs a{};
     a.W = W; a.X = X; a.M = M; a.N = N; a.K = K;
-    a.out_f32 = dx; a.ldo = N; a.alpha = alpha;
+    a.resid_in = dxin; a.out_f32 = dx; a.ldo = N; a.alpha = alpha;
     a.sk_part = sk; a.sk_part_floats = skf;
     a.force_cfg = cfg;
     hipError_t e = rh::launch_gemm_resid_norm(a, dg, eps, dxn, nullptr);

@@ -21,6 +21,7 @@ struct GemmArgs {
     f16* out_f16;    // EPI_SWIGLU: gate [M, ldo] in fragment order
     int ldo;
     float alpha;     // EPI_RESID: x += alpha * acc; EPI_F32: out = alpha * acc (0 = unscaled)
+    const float* resid_in;  // EPI_RESID: the residual read, [M, ldo] (null: out_f32, in place)
     float softcap;   // EPI_F32: c * tanh(acc / c) when c > 0
     // EPI_QKV: N = 3*D rows ordered q | k | v; RoPE on q and k.
     f16* q;          // [B][H][S][hd]
@@ -69,7 +70,8 @@ enum GemmCfg {
 size_t gemm_sk_part_floats();
 hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t st);
 // Residual projection followed by the next RMSNorm:
-//   x [M, N] += alpha * (X W^T)            (a.out_f32 = x, a.ldo = N)
+//   x [M, N] += alpha * (X W^T)            (a.out_f32 = x, a.ldo = N; with
+//                                           a.resid_in set, x = resid_in + ...)
 //   xn = rmsnorm(x) * gamma, fp16 in fragment order (skipped when gamma is null).
 // With few output tiles (narrow N, small M) K is split: every split writes an
 // fp32 partial into a.sk_part and one row kernel sums the partials in split
@@ -154,11 +156,12 @@ hipError_t launch_rmsnorm(const float* x, const float* gamma, f16* out, int rows
 // rmsnorm of rows x[(r*stride + offset)] -> out[r]  (last-position gather)
 hipError_t launch_rmsnorm_strided(const float* x, const float* gamma, f16* out, int rows, int D,
                                   float eps, int stride_rows, int offset_rows, hipStream_t st);
-// x [rows, D] += alpha * sum_s part[s*split_stride + row*D ...] (s = 0..S-1 in
-// order), then out = rmsnorm(x) * gamma in fragment order when gamma is set.
-// D % 8 == 0, D <= 8192.
-hipError_t launch_resid_norm(float* x, const float* part, int S, size_t split_stride, float alpha,
-                             const float* gamma, float eps, f16* out, int rows, int D, hipStream_t st);
+// x [rows, D] = xin + alpha * sum_s part[s*split_stride + row*D ...] (s =
+// 0..S-1 in order; xin may be x), then out = rmsnorm(x) * gamma in fragment
+// order when gamma is set.  D % 8 == 0, D <= 8192.
+hipError_t launch_resid_norm(const float* xin, float* x, const float* part, int S, size_t split_stride,
+                             float alpha, const float* gamma, float eps, f16* out, int rows, int D,
+                             hipStream_t st);
 hipError_t launch_cross_entropy(const float* logits, const uint32_t* targets, float* loss,
                                 int rows, int V, int* err, hipStream_t st);
 hipError_t launch_mean_rows(const float* loss, float* mean, int B, int S, hipStream_t st);

@@ -80,7 +80,8 @@ __global__ __launch_bounds__(256) void rmsnorm_frag_kernel(const float* x, const
     }
 }
 
-// Split-K reduction + residual + RMSNorm: one block per row; each thread
+// Split-K reduction + residual + RMSNorm (x = xin + alpha * sum, xin may be
+// x itself): one block per row; each thread
 // owns 8 consecutive columns per 2048-column pass (up to 4 passes), keeps the
 // updated values in registers between the sum of squares and the normalised
 // 16-byte fragment-order writes.  S (the split count) is a template argument
@@ -88,12 +89,14 @@ __global__ __launch_bounds__(256) void rmsnorm_frag_kernel(const float* x, const
 // are summed in split order.  (Nontemporal loads of the partials, which the
 // split GEMM has just written, measured slower: 11.9 -> 14.2 us for W2.)
 template <int S>
-__global__ __launch_bounds__(256) void resid_norm_kernel(float* x, const float* part, size_t split_stride,
+__global__ __launch_bounds__(256) void resid_norm_kernel(const float* xin, float* x, const float* part,
+                                                         size_t split_stride,
                                                          float alpha, const float* gamma, float eps, f16* out,
                                                          int D) {
     __shared__ float red[4];
     const int row = blockIdx.x;
     float* xr = x + (size_t)row * D;
+    const float* xir = xin + (size_t)row * D;
     const float* pr = part + (size_t)row * D;
     f32x4 v[4][2];
     float ss = 0.f;
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(float* x, const float* 
                 p0[sp] = *(const f32x4*)(pr + sp * split_stride + i);
                 p1[sp] = *(const f32x4*)(pr + sp * split_stride + i + 4);
             }
-            f32x4 x0 = *(const f32x4*)(xr + i), x1 = *(const f32x4*)(xr + i + 4);
+            f32x4 x0 = *(const f32x4*)(xir + i), x1 = *(const f32x4*)(xir + i + 4);
             f32x4 a0 = {}, a1 = {};
 #pragma unroll
             for (int sp = 0; sp < S; ++sp) {
@@ -312,12 +315,13 @@ hipError_t launch_rmsnorm_strided(const float* x, const float* gamma, f16* out, 
                        stride_rows, offset_rows);
     return hipGetLastError();
 }
-hipError_t launch_resid_norm(float* x, const float* part, int S, size_t split_stride, float alpha,
-                             const float* gamma, float eps, f16* out, int rows, int D, hipStream_t st) {
+hipError_t launch_resid_norm(const float* xin, float* x, const float* part, int S, size_t split_stride,
+                             float alpha, const float* gamma, float eps, f16* out, int rows, int D,
+                             hipStream_t st) {
     if (D % 8 != 0 || D > 8192 || S < 0 || S > 8 || (S > 0 && !part)) return hipErrorInvalidValue;
 #define RH_RN(S_)                                                                                          \
     case S_:                                                                                               \
-        hipLaunchKernelGGL(resid_norm_kernel<S_>, dim3(rows), dim3(256), 0, st, x, part, split_stride, alpha, \
+        hipLaunchKernelGGL(resid_norm_kernel<S_>, dim3(rows), dim3(256), 0, st, xin, x, part, split_stride, alpha, \
                            gamma, eps, out, D);                                                            \
         break
     switch (S) {

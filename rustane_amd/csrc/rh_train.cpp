@@ -264,12 +264,13 @@ int enqueue_forward_train(rh_ctx* ctx, int B, int S) {
     const int M = B * S, D = c.dim, F = c.hidden;
     const float alpha = 1.0f / std::sqrt(2.0f * (float)c.nlayers);
     hipStream_t st = ctx->stream;
-    LCK(rh::launch_embed(ctx->d_tok, ctx->embed, ctx->x, M, D, c.vocab, ctx->d_err, st));
-    LCK(rh::launch_rmsnorm(ctx->x, ctx->L[0].g1, T->c[0].xn, M, D, c.rms_eps, st, true));
+    // The residual stream moves out of place through the per-layer caches the
+    // backward reads: xin[l] -> (Wo) x2[l] -> (W2) xin[l + 1] ... -> xlast.
+    LCK(rh::launch_embed(ctx->d_tok, ctx->embed, T->c[0].xin, M, D, c.vocab, ctx->d_err, st));
+    LCK(rh::launch_rmsnorm(T->c[0].xin, ctx->L[0].g1, T->c[0].xn, M, D, c.rms_eps, st, true));
     for (int l = 0; l < c.nlayers; ++l) {
         const Layer& W = ctx->L[l];
         const TrainState::Cache& cc = T->c[l];
-        HCK(hipMemcpyAsync(cc.xin, ctx->x, (size_t)M * D * sizeof(float), hipMemcpyDeviceToDevice, st));
         rh::GemmArgs g{};
         g.W = W.wqkv; g.X = cc.xn; g.M = M; g.N = 3 * D; g.K = D;
         g.q = cc.q; g.kc = cc.k; g.vc = cc.v; g.rope = ctx->rope;
@@ -281,10 +282,9 @@ int enqueue_forward_train(rh_ctx* ctx, int B, int S) {
         }));
         g = rh::GemmArgs{};
         g.W = W.wo; g.X = cc.attn; g.M = M; g.N = D; g.K = D;
-        g.out_f32 = ctx->x; g.ldo = D; g.alpha = alpha;
+        g.resid_in = cc.xin; g.out_f32 = cc.x2; g.ldo = D; g.alpha = alpha;
         set_sk(ctx, g);
         RCK(timed(ctx, RH_K_GEMM_WO, [&] { return rh::launch_gemm_resid_norm(g, W.g2, c.rms_eps, cc.x2n, st); }));
-        HCK(hipMemcpyAsync(cc.x2, ctx->x, (size_t)M * D * sizeof(float), hipMemcpyDeviceToDevice, st));
         g = rh::GemmArgs{};
         g.W = W.w13; g.X = cc.x2n; g.M = M; g.N = 2 * F; g.K = D;
         g.out_f16 = cc.gate; g.ldo = F; g.h13 = cc.h13;
@@ -296,13 +296,12 @@ int enqueue_forward_train(rh_ctx* ctx, int B, int S) {
         const bool last = l + 1 == c.nlayers;
         g = rh::GemmArgs{};
         g.W = W.w2; g.X = cc.gate; g.M = M; g.N = D; g.K = F;
-        g.out_f32 = ctx->x; g.ldo = D; g.alpha = alpha;
+        g.resid_in = cc.x2; g.out_f32 = last ? T->xlast : T->c[l + 1].xin; g.ldo = D; g.alpha = alpha;
         set_sk(ctx, g);
         const float* ng = last ? ctx->gfinal : ctx->L[l + 1].g1;
         f16* nxn = last ? T->xf : T->c[l + 1].xn;
         RCK(timed(ctx, RH_K_GEMM_W2, [&] { return rh::launch_gemm_resid_norm(g, ng, c.rms_eps, nxn, st); }));
     }
-    HCK(hipMemcpyAsync(T->xlast, ctx->x, (size_t)M * D * sizeof(float), hipMemcpyDeviceToDevice, st));
     return enqueue_tail(ctx, B, S, true, T->xf);
 }
 

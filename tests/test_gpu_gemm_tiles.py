@@ -42,7 +42,7 @@ def lib():
     f, i, p = ctypes.c_float, ctypes.c_int, ctypes.c_void_p
     h.rhh_gemm.argtypes = [i, i, p, p, i, i, i, f, f, p, p, p, i, i, i, i, i, i, p, p, p, p]
     h.rhh_gemm.restype = i
-    h.rhh_gemm_resid_norm.argtypes = [i, p, p, i, i, i, f, p, p, f, p]
+    h.rhh_gemm_resid_norm.argtypes = [i, p, p, i, i, i, f, p, p, p, f, p]
     h.rhh_gemm_resid_norm.restype = i
     h.rhh_gemm_wgrad.argtypes = [p, p, i, i, i, f, i, p]
     h.rhh_gemm_wgrad.restype = i
@@ -211,20 +211,24 @@ def test_qkv_rope_scatter(lib, name):
     assert not v[:, :, :pos0].any() and not v[:, :, pos0 + S:].any()
 
 
+@pytest.mark.parametrize("out_of_place", [False, True])
 @pytest.mark.parametrize("cfg,K", [(0, 1024), (0, 8192), (16, 1024), (9, 1024)])
-def test_residual_then_rmsnorm(lib, cfg, K):
+def test_residual_then_rmsnorm(lib, cfg, K, out_of_place):
     """cfg 0 at these shapes takes split-K (K 1024: 128x128 tiles, K 8192:
     256x128) with the summing row kernel; 16 / 9 are one block per tile and
-    stream-K followed by the plain RMSNorm kernel."""
+    stream-K followed by the plain RMSNorm kernel.  Out of place the residual
+    is read from its own buffer and the output buffer starts as garbage."""
     M, N, eps, alpha = 300, 1024, 1e-5, 0.25
     x, w, y = operands(7, M, N, K)
     rng = np.random.default_rng(8)
     x0 = rng.standard_normal((M, N)).astype(np.float32)
     gamma = rng.uniform(0.5, 1.5, N).astype(np.float32)
     xf, wf = frag_pack(x), frag_pack(w)
-    io = x0.copy()
+    xin = x0.copy() if out_of_place else None
+    io = np.full_like(x0, np.nan) if out_of_place else x0.copy()
     xn = np.zeros(up16(M) * N, np.float16)
-    rc = lib.rhh_gemm_resid_norm(cfg, ptr(wf), ptr(xf), M, N, K, alpha, ptr(io), ptr(gamma), eps, ptr(xn))
+    rc = lib.rhh_gemm_resid_norm(cfg, ptr(wf), ptr(xf), M, N, K, alpha, ptr(xin), ptr(io), ptr(gamma), eps,
+                                 ptr(xn))
     assert rc == 0, f"rhh_gemm_resid_norm cfg {cfg}: error {rc}"
     x1 = x0.astype(np.float64) + alpha * y
     close(io, x1, 1e-5, "residual")
