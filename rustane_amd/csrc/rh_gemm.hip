@@ -734,7 +734,11 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         const bool sk_ok = a.sk_part && (size_t)SK_P * 2 * 256 * 256 <= a.sk_part_floats;
         if (sk_ok && a.K >= 8192 && t256x128 < 160 && t256x128 * KT >= 2 * SK_P) {
             cfg = GCFG_D8_256x128_SK;
-        } else if (sk_ok && t128 < 160 && t128 * KT >= 2 * SK_P) {
+        } else if (sk_ok && t128 < 160 && t128 * KT >= 2 * SK_P && KT * (SK_P - t128) >= 28 * SK_P) {
+            // stream-K saves the idle CUs' share of one tile's k loop (about
+            // 0.36 us per 32-k step) but pays a fix-up launch (about 9 us): at
+            // 600M, M = 512, QKV (144 tiles, K 1536) one round of whole tiles is
+            // faster (15.3 + 8.5 us stream-K + fix-up against one 17.5 us round)
             cfg = GCFG_D8_128x128_SK;
         } else {
             float best = 3.0e38f;
