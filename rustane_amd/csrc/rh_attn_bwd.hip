@@ -33,6 +33,25 @@ namespace {
 
 typedef f16 f16x2 __attribute__((ext_vector_type(2)));
 
+// Four consecutive dims d..d+3 (d % 4 == 0) of head h of token row `row`
+// (sequence position pos) of the q (sec 0), k (1) or v (2) gradient, written
+// as fp16 into the fragment-order operand [M][3D] of the dX GEMM; q and k
+// first get the RoPE backward (rope_backward_inplace, layer.rs:7389-7407):
+// the transposed rotation of the pairs (d, d+1), (d+2, d+3).
+template <int HD>
+__device__ __forceinline__ void store_dqkv4(f16* __restrict__ out, const float2* __restrict__ rope, int row,
+                                            int pos, int sec, int D, int h, int d, f32x4 v) {
+    if (sec < 2) {
+        const float2 c0 = rope[(size_t)pos * (HD / 2) + d / 2], c1 = rope[(size_t)pos * (HD / 2) + d / 2 + 1];
+        const float a0 = v[0], a1 = v[1], a2 = v[2], a3 = v[3];
+        v[0] = c0.x * a0 + c0.y * a1;
+        v[1] = -c0.y * a0 + c0.x * a1;
+        v[2] = c1.x * a2 + c1.y * a3;
+        v[3] = -c1.y * a2 + c1.x * a3;
+    }
+    *(f16x4*)(out + frag_off(row, sec * D + h * HD + d, 3 * D)) = f16x4{(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+}
+
 // Stages rows r0..r0+63 (clamped to S - 1) of a [S][HD] fp16 matrix into
 // LDS: row-major (ld HD + 8) when rm is set, and transposed [HD][64] (ld 72)
 // when tr is set, two rows per 32-bit LDS store.
@@ -63,7 +82,8 @@ template <int HD>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const f16* __restrict__ Q, const f16* __restrict__ K,
                                                           const f16* __restrict__ V, const f16* __restrict__ dO,
                                                           const float* __restrict__ lse,
-                                                          const float* __restrict__ Drow, float* __restrict__ dqkv,
+                                                          const float* __restrict__ Drow, f16* __restrict__ dqkv,
+                                                          const float2* __restrict__ rope,
                                                           int H, int S, float scale_log2, float scale) {
     constexpr int KB = 64, LD = HD + 8, LT = KB + 8, NKK = HD / 32, NHT = HD / 16;
     __shared__ __attribute__((aligned(16))) f16 sK[KB * LD];
@@ -133,9 +153,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const f16* __restrict_
                 acc[j] = mfma16(*(const f16x8*)&sKt[(16 * j + r) * LT + 32 * c + 8 * g], dsf[c], acc[j]);
     }
     if (qi < S) {
-        float* dst = dqkv + (size_t)(b * S + qi) * (3 * H * HD) + h * HD + 4 * g;
 #pragma unroll
-        for (int j = 0; j < NHT; ++j) *(f32x4*)(dst + 16 * j) = acc[j] * scale;
+        for (int j = 0; j < NHT; ++j)
+            store_dqkv4<HD>(dqkv, rope, b * S + qi, qi, 0, H * HD, h, 16 * j + 4 * g, acc[j] * scale);
     }
 }
 
@@ -144,7 +164,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const f16* __restric
                                                             const f16* __restrict__ V, const f16* __restrict__ dO,
                                                             const float* __restrict__ lse,
                                                             const float* __restrict__ Drow,
-                                                            float* __restrict__ dqkv, int H, int S,
+                                                            f16* __restrict__ dqkv, const float2* __restrict__ rope,
+                                                            int H, int S,
                                                             float scale_log2, float scale) {
     constexpr int QB = 64, LD = HD + 8, LT = QB + 8, NKK = HD / 32, NHT = HD / 16;
     __shared__ __attribute__((aligned(16))) f16 sQ[QB * LD];
@@ -222,11 +243,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const f16* __restric
     }
     if (ki < S) {
         const int D = H * HD;
-        float* dst = dqkv + (size_t)(b * S + ki) * (3 * D) + h * HD + 4 * g;
 #pragma unroll
         for (int j = 0; j < NHT; ++j) {
-            *(f32x4*)(dst + D + 16 * j) = dk[j] * scale;
-            *(f32x4*)(dst + 2 * D + 16 * j) = dv[j];
+            store_dqkv4<HD>(dqkv, rope, b * S + ki, ki, 1, D, h, 16 * j + 4 * g, dk[j] * scale);
+            store_dqkv4<HD>(dqkv, rope, b * S + ki, ki, 2, D, h, 16 * j + 4 * g, dv[j]);
         }
     }
 }
@@ -282,8 +302,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const f16* __restr
                                                               const f16* __restrict__ V, const f16* __restrict__ dO,
                                                               const float* __restrict__ lse,
                                                               const float* __restrict__ Drow,
-                                                              float* __restrict__ dqkv, int H, int S,
-                                                              float scale_log2, float scale) {
+                                                              f16* __restrict__ dqkv, const float2* __restrict__ rope,
+                                                              int H, int S, float scale_log2, float scale) {
     constexpr int HD = 128, KB = 64, NKK = HD / 32, NHT = HD / 16, TILE = KB * HD;
     // one array per stage and role, so the compiler's wait-count tracking
     // tells a stage's reads from the DMA filling the other stage
@@ -364,9 +384,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_dma_kernel(const f16* __restr
         if (kb0 + 1 < nkb) step(kb0 + 1, std::integral_constant<int, 1>{});
     }
     if (qi < S) {
-        float* dst = dqkv + (size_t)(b * S + qi) * (3 * H * HD) + h * HD + 4 * g;
 #pragma unroll
-        for (int j = 0; j < NHT; ++j) *(f32x4*)(dst + 16 * j) = acc[j] * scale;
+        for (int j = 0; j < NHT; ++j)
+            store_dqkv4<HD>(dqkv, rope, b * S + qi, qi, 0, H * HD, h, 16 * j + 4 * g, acc[j] * scale);
     }
 }
 
@@ -376,7 +396,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_dma_kernel(const f16* __res
                                                                 const f16* __restrict__ dO,
                                                                 const float* __restrict__ lse,
                                                                 const float* __restrict__ Drow,
-                                                                float* __restrict__ dqkv, int H, int S,
+                                                                f16* __restrict__ dqkv, const float2* __restrict__ rope,
+                                                            int H, int S,
                                                                 float scale_log2, float scale) {
     constexpr int HD = 128, QB = 64, NKK = HD / 32, NHT = HD / 16, TILE = QB * HD;
     __shared__ __attribute__((aligned(1024))) f16 sQ0[TILE], sO0[TILE], sQt0[TILE], sOt0[TILE], sQ1[TILE],
@@ -470,11 +491,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_dma_kernel(const f16* __res
     }
     if (ki < S) {
         const int D = H * HD;
-        float* dst = dqkv + (size_t)(b * S + ki) * (3 * D) + h * HD + 4 * g;
 #pragma unroll
         for (int j = 0; j < NHT; ++j) {
-            *(f32x4*)(dst + D + 16 * j) = dk[j] * scale;
-            *(f32x4*)(dst + 2 * D + 16 * j) = dv[j];
+            store_dqkv4<HD>(dqkv, rope, b * S + ki, ki, 1, D, h, 16 * j + 4 * g, dk[j] * scale);
+            store_dqkv4<HD>(dqkv, rope, b * S + ki, ki, 2, D, h, 16 * j + 4 * g, dv[j]);
         }
     }
 }
@@ -532,7 +552,7 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_kernel(const float* __restr
 
 hipError_t launch_attn_backward(const f16* q, const f16* k, const f16* v, const f16* o, const float* dOf,
                                 int nsplit, size_t split_stride, const float* lse, f16* dOh, float* Drow,
-                                float* dqkv, int B, int H, int S, int hd, hipStream_t st) {
+                                f16* dqkv, const float2* rope, int B, int H, int S, int hd, hipStream_t st) {
     if ((hd != 128 && hd != 64) || nsplit < 1 || nsplit > 8) return hipErrorInvalidValue;
     const int M = B * S;
     const unsigned pgrid = (unsigned)(((long long)M * H * hd / 8 + 255) / 256);
@@ -554,14 +574,14 @@ hipError_t launch_attn_backward(const f16* q, const f16* k, const f16* v, const 
     const dim3 grid((S + 63) / 64 * H * B);
     const float scale = 1.0f / sqrtf((float)hd), sl2 = scale * 1.4426950408889634f;
     if (hd == 128) {
-        hipLaunchKernelGGL(attn_bwd_dq_dma_kernel, grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S, sl2,
+        hipLaunchKernelGGL(attn_bwd_dq_dma_kernel, grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, rope, H, S, sl2,
                            scale);
-        hipLaunchKernelGGL(attn_bwd_dkdv_dma_kernel, grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S,
+        hipLaunchKernelGGL(attn_bwd_dkdv_dma_kernel, grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, rope, H, S,
                            sl2, scale);
     } else {
-        hipLaunchKernelGGL((attn_bwd_dq_kernel<64>), grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S,
+        hipLaunchKernelGGL((attn_bwd_dq_kernel<64>), grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, rope, H, S,
                            sl2, scale);
-        hipLaunchKernelGGL((attn_bwd_dkdv_kernel<64>), grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, H, S,
+        hipLaunchKernelGGL((attn_bwd_dkdv_kernel<64>), grid, dim3(256), 0, st, q, k, v, dOh, lse, Drow, dqkv, rope, H, S,
                            sl2, scale);
     }
     return hipGetLastError();

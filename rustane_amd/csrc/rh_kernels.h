@@ -194,9 +194,6 @@ hipError_t launch_rms_backward(const float* dy, int nsplit, size_t split_stride,
 // dgamma[d] += kappa * sum_b part[b][d]  (= instead of += when store is set)
 hipError_t launch_dgamma_reduce(const float* part, int nblk, int D, float kappa, float* dgamma, bool store,
                                 hipStream_t st);
-// RoPE backward on the q, k sections of dqkv [M][3D] fp32, out fp16 fragment order.
-hipError_t launch_rope_backward_pack(const float* dqkv, const float2* rope, f16* out, int M, int S, int D, int hd,
-                                     hipStream_t st);
 // dembed[utok[u]] += kappa * dy[idx[j]] for j in [start[u], start[u+1]).
 hipError_t launch_embed_backward(const float* dy, const uint32_t* utok, const int* start, const int* idx, int nuniq,
                                  float kappa, float* dembed, int D, hipStream_t st);
@@ -204,10 +201,12 @@ hipError_t launch_embed_backward(const float* dy, const uint32_t* utok, const in
 // the forward output (fragment order [B*S][H*hd]), dOf [B*S][H*hd] fp32 as
 // the sum of nsplit (1..8) partials split_stride floats apart, lse from the
 // forward.  Workspace dOh (fp16 [B][H][S][hd]) and Drow ([B][H][S]).
-// Writes dqkv [B*S][3*H*hd] fp32 (dq | dk | dv, before the RoPE backward).
+// Writes dqkv, the dX GEMM's operand: fp16 in fragment order [B*S][3*H*hd]
+// (dq | dk | dv, the RoPE backward applied to dq and dk with the table rope
+// [S][hd/2]).
 hipError_t launch_attn_backward(const f16* q, const f16* k, const f16* v, const f16* o, const float* dOf,
                                 int nsplit, size_t split_stride, const float* lse, f16* dOh, float* Drow,
-                                float* dqkv, int B, int H, int S, int hd, hipStream_t st);
+                                f16* dqkv, const float2* rope, int B, int H, int S, int hd, hipStream_t st);
 
 // ---------------- optimizer ----------------
 // One AdamW step (step_fused) with its constants: omb1 = 1 - beta1,

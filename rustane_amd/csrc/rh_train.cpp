@@ -223,7 +223,7 @@ int ensure_train_ws(rh_ctx* ctx, int B, int S) {
     for (int g = 0; g < 4; ++g)
         for (int i = 0; i < 2; ++i) RCK(dalloc(ctx, &T->tx[g][i], txr[g][i] * mp));
     RCK(dalloc(ctx, &T->dOh, m * D));
-    RCK(dalloc(ctx, &T->gout, m * std::max(F, 4 * D)));  // [M][F] dgate, or da [M][D] + dqkv [M][3D]
+    RCK(dalloc(ctx, &T->gout, m * D));  // an unsplit data-gradient product [M][D]
     RCK(dalloc(ctx, &T->dres, m * D));
     RCK(dalloc(ctx, &T->Drow, (size_t)M * c.heads));
     RCK(dalloc(ctx, &T->dgp, (size_t)rh::rms_backward_blocks(M) * D));
@@ -447,12 +447,11 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         HCK(hipEventRecord(T->read[2], sd));
         RCK(grad_gemm(ctx, X2[1], X2[0], D, D, kappa, G[3], sd));
         RCK(data_gemm(ctx, T->H1m, wt.ot, M, D, D, T->gout, &dp, &ns));
-        // attention backward -> dq | dk | dv, RoPE backward, fp16 pack
-        float* dqkv = T->gout + MD;  // past da (an unsplit product lands there)
-        LCK(rh::launch_attn_backward(cc.q, cc.k, cc.v, cc.attn, dp, ns, MD, cc.lse, T->dOh, T->Drow, dqkv, B, H,
-                                     S, hd, st));
+        // attention backward -> dq | dk | dv with the RoPE backward, as the fp16
+        // operand H2q (rewritten: the side stream has copied the previous layer's)
         RCK(rewrite(3));
-        LCK(rh::launch_rope_backward_pack(dqkv, ctx->rope, T->H2q, M, S, D, hd, st));
+        LCK(rh::launch_attn_backward(cc.q, cc.k, cc.v, cc.attn, dp, ns, MD, cc.lse, T->dOh, T->Drow, T->H2q,
+                                     ctx->rope, B, H, S, hd, st));
         // dxn = dqkv [Wq | Wk | Wv]^T; dWq, dWk, dWv += xn^T d{q,k,v} (side)
         RCK(publish(3));
         LCK(rh::launch_transpose_frag2(T->H2q, X3[0], M, 3 * D, cc.xn, X3[1], M, D, Mp, sd));

@@ -267,36 +267,6 @@ __global__ __launch_bounds__(256) void dgamma_reduce_kernel(const float* __restr
     }
 }
 
-// RoPE backward (rope_backward_inplace, layer.rs:7389-7407) on the q and k
-// sections of dqkv [M][3D] fp32 (token m at position m % S), then fp16 in
-// fragment order [M][3D] for the dX GEMM.
-__global__ __launch_bounds__(256) void rope_backward_pack_kernel(const float* __restrict__ dqkv,
-                                                                 const float2* __restrict__ rope,
-                                                                 f16* __restrict__ out, int M, int S, int D, int hd) {
-    const int N = 3 * D;
-    const size_t n8 = (size_t)M * N / 8;
-    for (size_t t = blockIdx.x * (size_t)blockDim.x + threadIdx.x; t < n8; t += (size_t)gridDim.x * blockDim.x) {
-        const size_t base = t * 8;
-        const int m = (int)(base / N), c = (int)(base % N);
-        const f32x4 a0 = *(const f32x4*)(dqkv + base), a1 = *(const f32x4*)(dqkv + base + 4);
-        float v[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-        if (c < 2 * D) {
-            const int d = (c % D) % hd, pos = m % S;
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const float2 cs = rope[(size_t)pos * (hd / 2) + d / 2 + p];
-                const float d0 = v[2 * p], d1 = v[2 * p + 1];
-                v[2 * p] = cs.x * d0 + cs.y * d1;
-                v[2 * p + 1] = -cs.y * d0 + cs.x * d1;
-            }
-        }
-        f16x8 o;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = (f16)v[e];
-        *(f16x8*)(out + frag_off(m, c, N)) = o;
-    }
-}
-
 // embedding::backward_channel_first (cpu/embedding.rs:34-44): dembed[tok] +=
 // kappa * dy[pos] for the positions of each distinct token in increasing
 // order (one block per distinct token; idx/start a CSR built on the host).
@@ -365,14 +335,6 @@ hipError_t launch_dgamma_reduce(const float* part, int nblk, int D, float kappa,
                                 hipStream_t st) {
     hipLaunchKernelGGL(dgamma_reduce_kernel, dim3((D + 15) / 16), dim3(256), 0, st, part, nblk, D, kappa, dgamma,
                        (int)store);
-    return hipGetLastError();
-}
-
-hipError_t launch_rope_backward_pack(const float* dqkv, const float2* rope, f16* out, int M, int S, int D, int hd,
-                                     hipStream_t st) {
-    if (D % 8 != 0 || hd % 8 != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rope_backward_pack_kernel, dim3(grid_for((size_t)M * 3 * D / 8, 256)), dim3(256), 0, st, dqkv,
-                       rope, out, M, S, D, hd);
     return hipGetLastError();
 }
 
