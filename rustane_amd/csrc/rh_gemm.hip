@@ -282,14 +282,17 @@ __device__ __forceinline__ void store4(const GemmArgs& a, int m, int n, float v0
             v0 = tanhf(v0 * ic) * c; v1 = tanhf(v1 * ic) * c;
             v2 = tanhf(v2 * ic) * c; v3 = tanhf(v3 * ic) * c;
         }
-        *(f32x4*)(a.out_f32 + (size_t)m * a.ldo + n) = f32x4{v0, v1, v2, v3};
+        f32x4* po = (f32x4*)(a.out_f32 + (size_t)m * a.ldo + n);
+        if (a.nt_out) __builtin_nontemporal_store(f32x4{v0, v1, v2, v3}, po);
+        else *po = f32x4{v0, v1, v2, v3};
     } else if constexpr (EPI == EPI_RESID) {
         const size_t o = (size_t)m * a.ldo + n;
         f32x4* px = (f32x4*)(a.out_f32 + o);
         f32x4 x = *(const f32x4*)((a.resid_in ? a.resid_in : a.out_f32) + o);
         x[0] = v0 * a.alpha + x[0]; x[1] = v1 * a.alpha + x[1];
         x[2] = v2 * a.alpha + x[2]; x[3] = v3 * a.alpha + x[3];
-        *px = x;
+        if (a.nt_out) __builtin_nontemporal_store(x, px);
+        else *px = x;
     } else if constexpr (EPI == EPI_QKV) {
         // no integer divisions by run-time values here but the per-row m / S
         // (hoisted out of the feature loop): n < 3D, hd a power of two
@@ -692,7 +695,9 @@ __global__ __launch_bounds__(Tl::NT + 64 * WG_SW) void gemm_wgrad_kernel(GemmArg
                 } else if (a.alpha != 0.f) {
                     v[0] *= a.alpha; v[1] *= a.alpha; v[2] *= a.alpha; v[3] *= a.alpha;
                 }
-                *(f32x4*)po = v;
+                // the gradients are read only by the optimizer: streaming stores
+                // keep them from evicting the other stream's operands
+                __builtin_nontemporal_store(v, (f32x4*)po);
             }
         };
         constexpr int NR = 128 / (2 * WG_SW);  // rounds per tile

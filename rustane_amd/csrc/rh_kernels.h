@@ -36,6 +36,7 @@ struct GemmArgs {
     float* sk_part;
     size_t sk_part_floats;
     int force_cfg;  // 0 = heuristic; otherwise a GemmCfg value (tuning)
+    bool nt_out;    // EPI_F32 / EPI_RESID: nontemporal output stores (data read much later)
     // Optional timing: stamped at the kernel's own start and end by the
     // one-block-per-tile launch (hipExtLaunchKernelGGL), recorded around the
     // launches otherwise.

@@ -331,6 +331,7 @@ int grad_gemm(rh_ctx* ctx, const f16* X, const f16* W, int rows, int cols, float
     rh::GemmArgs g{};
     g.X = X; g.W = W; g.M = rows; g.N = cols; g.K = ctx->train->Mp;
     g.out_f32 = out; g.ldo = cols; g.alpha = kappa;
+    g.nt_out = true;  // read only by the optimizer
     const bool long_k = g.K >= 8192;
     if (ctx->train->zero && g.K <= 1024 && (size_t)rows * cols >= (size_t)4096 * 4096) {
         LCK(rh::launch_gemm_wgrad(g, false, st));
