@@ -40,7 +40,7 @@ def test_noalloc_step_matches_decode_step():
     try:
         for c in (ref, noa):
             c.load_weights(w.embed, w.gamma_final, tensors)
-        for call, (B, P) in enumerate([(8, 100), (2, 37)]):
+        for call, (B, P) in enumerate([(8, 140), (2, 37)]):
             print(f"[case] noalloc call {call}: batch {B}, prompt {P}", flush=True)
             prompt, _ = tokens_uniform(93 + call, cfg.vocab, B, P)
             n_ref, _ = ref.prefill(prompt)
