@@ -32,25 +32,37 @@ __global__ void embed_kernel(const uint32_t* tok, const f16* E, float* x, int D,
     }
 }
 
+// One block per row; NIT = ceil(D / 1024) groups of 4 features per thread.
+// The row and gamma are loaded once, every load issued before the first use
+// (one memory round trip instead of one per group and pass); each thread
+// sums its groups in ascending feature order, as the fused GEMV norm does.
+template <int NIT>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const float* gamma, f16* out,
                                                       int D, float eps, int stride_rows,
                                                       int offset_rows) {
     __shared__ float red[4];
     const int row = blockIdx.x;
     const float* xr = x + ((size_t)row * stride_rows + offset_rows) * D;
-    float ss = 0.f;
-    for (int i = threadIdx.x * 4; i < D; i += 1024) {
-        const f32x4 v = *(const f32x4*)(xr + i);
-        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    f32x4 v[NIT], gm[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int i = threadIdx.x * 4 + it * 1024;
+        v[it] = i < D ? *(const f32x4*)(xr + i) : f32x4{};
+        gm[it] = i < D ? *(const f32x4*)(gamma + i) : f32x4{};
     }
+    float ss = 0.f;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it)
+        ss += v[it][0] * v[it][0] + v[it][1] * v[it][1] + v[it][2] * v[it][2] + v[it][3] * v[it][3];
     ss = block_sum_256(ss, red);
     const float r = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
     f16* o = out + (size_t)row * D;
-    for (int i = threadIdx.x * 4; i < D; i += 1024) {
-        const f32x4 v = *(const f32x4*)(xr + i);
-        const f32x4 gm = *(const f32x4*)(gamma + i);
-        *(f16x4*)(o + i) = f16x4{(f16)(v[0] * r * gm[0]), (f16)(v[1] * r * gm[1]),
-                                 (f16)(v[2] * r * gm[2]), (f16)(v[3] * r * gm[3])};
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int i = threadIdx.x * 4 + it * 1024;
+        if (i < D)
+            *(f16x4*)(o + i) = f16x4{(f16)(v[it][0] * r * gm[it][0]), (f16)(v[it][1] * r * gm[it][1]),
+                                     (f16)(v[it][2] * r * gm[it][2]), (f16)(v[it][3] * r * gm[it][3])};
     }
 }
 
@@ -301,19 +313,28 @@ hipError_t launch_embed(const uint32_t* tok, const f16* E, float* x, int rows, i
     hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(256), 0, st, tok, E, x, D, V, err);
     return hipGetLastError();
 }
-hipError_t launch_rmsnorm(const float* x, const float* gamma, f16* out, int rows, int D, float eps,
-                          hipStream_t st, bool frag) {
-    if (frag)
-        hipLaunchKernelGGL(rmsnorm_frag_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps);
-    else
-        hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps, 1, 0);
-    return hipGetLastError();
-}
 hipError_t launch_rmsnorm_strided(const float* x, const float* gamma, f16* out, int rows, int D,
                                   float eps, int stride_rows, int offset_rows, hipStream_t st) {
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps,
-                       stride_rows, offset_rows);
+    if (D % 4 != 0 || D > 8192) return hipErrorInvalidValue;
+#define RH_RMS(N_)                                                                                          \
+    case N_:                                                                                                \
+        hipLaunchKernelGGL(rmsnorm_kernel<N_>, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps, stride_rows, \
+                           offset_rows);                                                                    \
+        break
+    switch ((D + 1023) / 1024) {
+        RH_RMS(1); RH_RMS(2); RH_RMS(3); RH_RMS(4); RH_RMS(5); RH_RMS(6); RH_RMS(7); RH_RMS(8);
+        default: return hipErrorInvalidValue;
+    }
+#undef RH_RMS
     return hipGetLastError();
+}
+hipError_t launch_rmsnorm(const float* x, const float* gamma, f16* out, int rows, int D, float eps,
+                          hipStream_t st, bool frag) {
+    if (frag) {
+        hipLaunchKernelGGL(rmsnorm_frag_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps);
+        return hipGetLastError();
+    }
+    return launch_rmsnorm_strided(x, gamma, out, rows, D, eps, 1, 0, st);
 }
 hipError_t launch_resid_norm(const float* xin, float* x, const float* part, int S, size_t split_stride,
                              float alpha, const float* gamma, float eps, f16* out, int rows, int D,
