@@ -253,8 +253,18 @@ __global__ __launch_bounds__(256) void dgamma_reduce_kernel(const float* __restr
     __shared__ float red[16][17];
     const int c = threadIdx.x & 15, q = threadIdx.x >> 4, d = blockIdx.x * 16 + c;
     float s = 0.f;
-    if (d < D)
-        for (int b = q; b < nblk; b += 16) s += part[(size_t)b * D + d];
+    if (d < D) {
+        // eight loads in flight per round, added in the same (ascending) order
+        int b = q;
+        for (; b + 7 * 16 < nblk; b += 8 * 16) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = part[(size_t)(b + 16 * u) * D + d];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += v[u];
+        }
+        for (; b < nblk; b += 16) s += part[(size_t)b * D + d];
+    }
     red[q][c] = s;
     __syncthreads();
     for (int h = 8; h > 0; h >>= 1) {
