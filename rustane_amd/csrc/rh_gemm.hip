@@ -55,7 +55,8 @@ struct Frag16 {
 // ---------------------------------------------------------------------------
 // Tile policy (DTile): operands go global -> LDS by DMA
 // (global_load_lds_dwordx4: 16 bytes per lane land at LDS base + 16 * lane),
-// so no registers stage them and NS = 4 stages of 32 k are in flight.  A
+// so no registers stage them and NS = 4 stages of 32 k are in flight (5 for
+// the 192x256 tile: its long-K and 5120-token shapes gain from the depth).  A
 // stage holds BN/16 weight fragments and BM/16 activation fragments of 1 KB
 // each; both operands are stored in fragment order in HBM (the activations by
 // the kernels that produce them), so every DMA instruction reads 1 KB
@@ -73,12 +74,13 @@ struct Frag16 {
 // fragment itself (lane l: row l%16, k 8(l/16)..+7), so each operand is one
 // 1 KB fragment read as is; same tile sizes, operand bytes and accumulator
 // registers, a different output layout (epilogue16).
-template <int WGN, int WGM, int TN, int TM, bool M16 = false>
+template <int WGN, int WGM, int TN, int TM, bool M16 = false, int NS_ = 4>
 struct DTile {
+    static_assert(NS_ == 4 || NS_ == 5, "4 or 5 stages");
     static constexpr bool kM16 = M16;
     static constexpr int NA = 2 * TN, NB = 2 * TM;  // 16-wide A / B tiles per wave (M16)
     static constexpr int BN = 32 * TN * WGN, BM = 32 * TM * WGM, NT = 64 * WGN * WGM;
-    static constexpr int FTN = TN, FTM = TM, KI = 32, NS = 4;
+    static constexpr int FTN = TN, FTM = TM, KI = 32, NS = NS_;
     static constexpr int NWF = BN / 16, NXF = BM / 16, NWAVE = WGN * WGM;
     // DMA instructions per wave per stage; when the fragments do not split
     // evenly, surplus slots repeat the last fragment (identical bytes to the
@@ -96,6 +98,11 @@ struct DTile {
 
     __device__ static void run(const GemmArgs& a, int n0, int m0, int kb, int ke, Acc& acc, Smem&) {
         __shared__ __attribute__((aligned(1024))) f16 st0[SH], st1[SH], st2[SH], st3[SH];
+        f16* st4 = st3;
+        if constexpr (NS > 4) {
+            __shared__ __attribute__((aligned(1024))) f16 st4s[SH];
+            st4 = st4s;
+        }
         const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
         const int wn = wv % WGN, wm = wv / WGN;
         const int K = a.K;
@@ -132,7 +139,7 @@ struct DTile {
             for (int j = 0; j < TM; ++j)
                 bo[j] = (NWF + ((wm * 32 * TM + 32 * j) >> 4) + (r >> 4)) * 512 + 128 * h + 8 * (r & 15);
         }
-        auto buf = [&](int s) -> f16* { return s == 0 ? st0 : s == 1 ? st1 : s == 2 ? st2 : st3; };
+        auto buf = [&](int s) -> f16* { return s == 0 ? st0 : s == 1 ? st1 : s == 2 ? st2 : s == 3 ? st3 : st4; };
         auto issue = [&](int kt, f16* st) {
 #pragma unroll
             for (int q = 0; q < LPS; ++q)
@@ -233,17 +240,44 @@ struct DTile {
         // more group of predicated steps.  Every step issues LPS DMAs, so the
         // vmcnt bookkeeping stays uniform.
         int t0 = 0;
-        for (; t0 + NS <= n; t0 += NS) {
-            step_il(t0, f0, f1, buf(0), buf(1));
-            step_il(t0 + 1, f1, f0, buf(1), buf(2));
-            step_il(t0 + 2, f0, f1, buf(2), buf(3));
-            step_il(t0 + 3, f1, f0, buf(3), buf(0));
-        }
-        if (t0 < n) {
-            step(t0, f0, f1, buf(0), buf(1));
-            step(t0 + 1, f1, f0, buf(1), buf(2));
-            step(t0 + 2, f0, f1, buf(2), buf(3));
-            step(t0 + 3, f1, f0, buf(3), buf(0));
+        if constexpr (NS == 4) {
+            for (; t0 + NS <= n; t0 += NS) {
+                step_il(t0, f0, f1, buf(0), buf(1));
+                step_il(t0 + 1, f1, f0, buf(1), buf(2));
+                step_il(t0 + 2, f0, f1, buf(2), buf(3));
+                step_il(t0 + 3, f1, f0, buf(3), buf(0));
+            }
+            if (t0 < n) {
+                step(t0, f0, f1, buf(0), buf(1));
+                step(t0 + 1, f1, f0, buf(1), buf(2));
+                step(t0 + 2, f0, f1, buf(2), buf(3));
+                step(t0 + 3, f1, f0, buf(3), buf(0));
+            }
+        } else {  // 5 stages: groups of 10 steps bring both the buffers and the fragment sets back around
+            for (; t0 + 10 <= n; t0 += 10) {
+                step_il(t0, f0, f1, buf(0), buf(1));
+                step_il(t0 + 1, f1, f0, buf(1), buf(2));
+                step_il(t0 + 2, f0, f1, buf(2), buf(3));
+                step_il(t0 + 3, f1, f0, buf(3), buf(4));
+                step_il(t0 + 4, f0, f1, buf(4), buf(0));
+                step_il(t0 + 5, f1, f0, buf(0), buf(1));
+                step_il(t0 + 6, f0, f1, buf(1), buf(2));
+                step_il(t0 + 7, f1, f0, buf(2), buf(3));
+                step_il(t0 + 8, f0, f1, buf(3), buf(4));
+                step_il(t0 + 9, f1, f0, buf(4), buf(0));
+            }
+            if (t0 < n) {
+                step(t0, f0, f1, buf(0), buf(1));
+                step(t0 + 1, f1, f0, buf(1), buf(2));
+                step(t0 + 2, f0, f1, buf(2), buf(3));
+                step(t0 + 3, f1, f0, buf(3), buf(4));
+                step(t0 + 4, f0, f1, buf(4), buf(0));
+                step(t0 + 5, f1, f0, buf(0), buf(1));
+                step(t0 + 6, f0, f1, buf(1), buf(2));
+                step(t0 + 7, f1, f0, buf(2), buf(3));
+                step(t0 + 8, f0, f1, buf(3), buf(4));
+                step(t0 + 9, f1, f0, buf(4), buf(0));
+            }
         }
         // the trailing (unused) stage loads must land before the LDS is reused
         __builtin_amdgcn_s_waitcnt(vm_wait(0));
@@ -780,8 +814,8 @@ hipError_t launch_epi(const GemmArgs& a, hipStream_t st) {
         case GCFG_D8_128x128: return launch_tile<DTile<2, 4, 2, 1, true>, EPI>(a, false, st);
         case GCFG_D8_128x128_SK: return launch_tile<DTile<2, 4, 2, 1, true>, EPI>(a, true, st);
         case GCFG_D4_192x128_SK: return launch_tile<DTile<2, 2, 3, 2>, EPI>(a, true, st);
-        case GCFG_D8_192x256: return launch_tile<DTile<2, 4, 3, 2, true>, EPI>(a, false, st);
-        case GCFG_D8_192x256_SK: return launch_tile<DTile<2, 4, 3, 2, true>, EPI>(a, true, st);
+        case GCFG_D8_192x256: return launch_tile<DTile<2, 4, 3, 2, true, 5>, EPI>(a, false, st);
+        case GCFG_D8_192x256_SK: return launch_tile<DTile<2, 4, 3, 2, true, 5>, EPI>(a, true, st);
         case GCFG_D4_192x256: return launch_tile<DTile<2, 2, 3, 4>, EPI>(a, false, st);
         case GCFG_D4_192x256_SK: return launch_tile<DTile<2, 2, 3, 4>, EPI>(a, true, st);
     }
