@@ -98,6 +98,9 @@ struct DTile {
 
     __device__ static void run(const GemmArgs& a, int n0, int m0, int kb, int ke, Acc& acc, Smem&) {
         __shared__ __attribute__((aligned(1024))) f16 st0[SH], st1[SH], st2[SH], st3[SH];
+        // The fifth stage exists only in five-stage tiles, so the four-stage
+        // ones keep their LDS size (two blocks per CU where they fit); there
+        // buf(4) is never used and st4 merely names st3.
         f16* st4 = st3;
         if constexpr (NS > 4) {
             __shared__ __attribute__((aligned(1024))) f16 st4s[SH];
