@@ -121,6 +121,19 @@ def test_fp32_store_scale_softcap(lib, name):
     close(out2, 15.0 * np.tanh(0.5 * y / 15.0), 1e-5, f"{name} alpha+softcap")
 
 
+@pytest.mark.parametrize("K", [128, 640, 1152])
+@pytest.mark.parametrize("name", ["D8_192x256", "D8_192x256_SK", "D8_256x128", "D8_128x128"])
+def test_k_step_counts(lib, name, K):
+    """k loops of 4, 20 and 36 steps: the five-stage tile (192x256) runs
+    groups of 10 steps and a predicated remainder, the four-stage ones
+    groups of 4, so these cover a remainder only, whole groups only, and
+    both."""
+    x, w, y = operands(11, 200, 700, K)
+    out = np.zeros((200, 700), np.float32)
+    run(lib, EPI_F32, CFGS[name], x, w, io=out)
+    close(out, y, 1e-5, f"{name} K {K}")
+
+
 @pytest.mark.parametrize("name", list(CFGS))
 def test_residual(lib, name):
     x, w, y = operands(2, 300, 1000, 384)
