@@ -12,9 +12,10 @@
 // which makes the RoPE pairs (2i, 2i+1) and 16-byte fp32 stores lane-local.
 //
 // Tile policy: DTile (below) -- both operands in fragment order in HBM, moved
-// global -> LDS by DMA through a 4-stage pipeline of 32-wide k slices,
+// global -> LDS by DMA through a 4-stage (192x256: 5-stage) pipeline of 32-wide k slices,
 // 32x32x16 MFMA (16x16x32 for the 8-wave tiles but 256x256) on fragments
-// double-buffered in registers.  Instantiated as
+// double-buffered in registers (256x256 keeps 32x32x16: its 16x16x32 form
+// spills).  Instantiated as
 // 256x256 (8 waves of 128x64, or 4 waves of 128x128 with AGPR accumulators),
 // 256x128, 192x256, 192x128 and 128x128; a cost model picks one per shape.
 // Out-of-range rows are clamped, not predicated (they only feed accumulator
