@@ -63,7 +63,11 @@ int ensure_rope(rh_ctx* ctx, int npos) {
     return RH_OK;
 }
 
+// Destroys every captured graph, after the stream has drained any replay of
+// them still in flight.
 void drop_graphs(rh_ctx* ctx) {
+    if (!ctx->dgraph && ctx->fgraphs.empty()) return;
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->dgraph) (void)hipGraphExecDestroy(ctx->dgraph);
     ctx->dgraph = nullptr;
     ctx->dgraph_B = 0;
@@ -217,6 +221,7 @@ int run_forward(rh_ctx* ctx, int B, int S, bool with_loss) {
                            [&](const FwdGraph& g) { return g.B == B && g.S == S && g.loss == with_loss; });
     if (it == gs.end()) {
         if (gs.size() >= kMaxFwdGraphs) {
+            HCK(hipStreamSynchronize(ctx->stream));  // the evicted graph may still be replaying
             (void)hipGraphExecDestroy(gs.front().exec);
             gs.erase(gs.begin());
         }
