@@ -10,6 +10,8 @@
   graph reading the old table.
 * rh_train_step leaves the context's own softcap as it was.
 * Decode calls whose batch differs from the prefill batch are refused.
+* Forward graphs evicted from the per-shape cache while earlier replays are
+  still queued leave every result intact.
 """
 import numpy as np
 import pytest
@@ -163,3 +165,29 @@ def test_decode_refuses_other_batch():
         assert c.pos == 8
         out, _ = c.decode_step(np.ones(3, np.uint32))
         assert out.shape == (3,) and c.pos == 9
+
+
+def test_forward_graph_eviction_with_replays_in_flight():
+    """More (batch, seq) shapes than the forward-graph cache holds, enqueued
+    back to back with rh_forward_dev (no synchronisation between calls): each
+    new shape evicts the oldest graph while earlier replays may still be
+    queued.  Every call's per-token losses must equal the synchronous
+    host-pointer forward of the same tokens."""
+    from rustane_amd import hip_rt
+    cfg = small_cfg(seq=96)
+    w = ModelWeights.normal(cfg, seed=71)
+    shapes = [(1, 96)] + [(1 + i % 2, 40 + 4 * i) for i in range(10)] * 2
+    print(f"[case] forward graph eviction: {len(shapes)} async forwards over 10 shapes", flush=True)
+    with hb.Context(cfg.to_rh(), 0, 2, 0) as c:
+        _load(c, w)
+        keep, want = [], []
+        for k, (B, S) in enumerate(shapes):
+            tok, tgt = tokens_uniform(500 + k, cfg.vocab, B, S)
+            want.append(c.forward(tok, tgt, want_logits=False).token_losses)
+            keep.append((hip_rt.DeviceArray.from_numpy(tok), hip_rt.DeviceArray.from_numpy(tgt),
+                         hip_rt.DeviceArray((B, S), np.float32)))
+        for (B, S), (dt, dg, dl) in zip(shapes, keep):
+            c.forward_dev(dt.ptr, dg.ptr, B, S, None, dl.ptr, None)
+        c.sync()
+        for k, (_, _, dl) in enumerate(keep):
+            assert np.array_equal(dl.numpy(), want[k]), k
