@@ -68,6 +68,7 @@ struct rh_ctx {
     float *dx = nullptr, *dlogits = nullptr, *pm = nullptr, *pl = nullptr, *po = nullptr;
     f16 *dxn = nullptr, *dq = nullptr, *dattn = nullptr, *dgate = nullptr;
     int* dstate = nullptr;
+    float* dssq = nullptr;  // [D/16][16] sums of squares from the residual GEMVs (B > fused-norm limit)
     uint32_t *dtok = nullptr, *dout = nullptr, *dseq = nullptr;
     float* dam_v = nullptr;  // [argmax blocks][16] argmax partials of the logits GEMV
     int* dam_i = nullptr;
@@ -208,6 +209,7 @@ struct DecodeBufs {
     f16* dgate;                // [B][F]
     float* dlogits;            // [B][V]
     float *pm, *pl, *po;       // [B][H][chunks] (m, l), [B][H][chunks][hd] o
+    float* ssq;                // [D/16][16] per-block sums of squares of x (norm without a row kernel)
     float* am_v;               // [gemv_argmax_blocks(V)][16]
     int* am_i;
     int* state;                // [2]: position, step

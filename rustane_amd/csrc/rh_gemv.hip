@@ -17,6 +17,12 @@
 // RoPE + KV-cache append, residual, SwiGLU, logits (+ per-block argmax
 // partials for greedy decode).
 //
+// Larger batches (the normalised rows exceed the LDS budget): the residual
+// GEMV that updates x also writes fp16(x * gamma_next) and per-block sums of
+// x^2 per token; the next GEMV sums those partials in a fixed order, takes
+// x * gamma as its fp16 input and scales its accumulators by each token's
+// 1/rms -- the RMSNorm with no launch of its own (rs_part / ssq_out).
+//
 // NORM: the input is the fp32 residual stream and the block applies the
 // RMSNorm itself (rmsnorm::forward_channel_first, cpu/rmsnorm.rs:149-183)
 // into LDS while its first weight chunks are in flight, in the same
@@ -85,6 +91,23 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
             for (int t = 0; t < RT; ++t) acc[t] = mfma16(wr[t][u], xv, acc[t]);
         }
     };
+    // rs_part: token t's sum of squares over the producer's rs_n (<= 512)
+    // blocks, as 16 strided slices summed in order and then the slices in
+    // order.  Loaded ahead of the weight prefetch and reduced after the k
+    // loop: only the epilogue needs 1/rms, so the loads' latency and the
+    // reduction stay off the weight stream.
+    constexpr bool RS = !NORM && EPI != GV_RESID;
+    float pv[RS ? 32 : 1];
+    if constexpr (RS) {
+        if (a.rs_part && tid < 256) {
+            const int t = tid & 15, q = tid >> 4;
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                const int i = q + 16 * k;
+                pv[k] = i < a.rs_n ? a.rs_part[i * 16 + t] : 0.f;
+            }
+        }
+    }
 #pragma unroll
     for (int s = 0; s < DEPTH; ++s) {
         wload(s, wb[s]);
@@ -142,6 +165,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
 
 #pragma unroll
     for (int t = 0; t < RT; ++t) sred[w][t][lane] = acc[t];
+    __shared__ float s_sq[RS ? 16 : 1][16];
+    if constexpr (RS) {
+        if (a.rs_part && tid < 256) {
+            float ss = 0.f;
+#pragma unroll
+            for (int k = 0; k < 32; ++k) ss += pv[k];
+            s_sq[tid >> 4][tid & 15] = ss;
+        }
+    }
     __syncthreads();
     if (w != 0) return;
 #pragma unroll
@@ -150,6 +182,16 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int v = 1; v < NW; ++v) s += sred[v][t][lane];
         acc[t] = s;
+    }
+    if constexpr (RS) {
+        if (a.rs_part) {
+            float ss = 0.f;  // token r's slices, in order
+#pragma unroll
+            for (int q = 0; q < 16; ++q) ss += s_sq[q][r];
+            const float rs = 1.0f / sqrtf(ss * (1.0f / (float)K) + a.eps);
+#pragma unroll
+            for (int t = 0; t < RT; ++t) acc[t] *= rs;
+        }
     }
     const int tok = r;
     // lane holds rows rows[t] + 4g + (0..3) for token `tok`
@@ -194,12 +236,26 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
                 }
             }
         } else if constexpr (EPI == GV_RESID) {
-            if (!xvalid || n >= N) return;
-            f32x4* px = (f32x4*)(a.out_f32 + (size_t)tok * a.ldo + n);
-            f32x4 x = *px;
-            x[0] = v0 * a.alpha + x[0]; x[1] = v1 * a.alpha + x[1];
-            x[2] = v2 * a.alpha + x[2]; x[3] = v3 * a.alpha + x[3];
-            *px = x;
+            const bool live = xvalid && n < N;
+            f32x4 x = f32x4{};
+            if (live) {
+                f32x4* px = (f32x4*)(a.out_f32 + (size_t)tok * a.ldo + n);
+                x = *px;
+                x[0] = v0 * a.alpha + x[0]; x[1] = v1 * a.alpha + x[1];
+                x[2] = v2 * a.alpha + x[2]; x[3] = v3 * a.alpha + x[3];
+                *px = x;
+            }
+            if (a.ssq_out) {  // the next RMSNorm's input and partial sums (all 64 lanes)
+                if (live) {
+                    const f32x4 gm = *(const f32x4*)(a.gnext + n);
+                    *(f16x4*)(a.xg_out + (size_t)tok * N + n) =
+                        f16x4{(f16)(x[0] * gm[0]), (f16)(x[1] * gm[1]), (f16)(x[2] * gm[2]), (f16)(x[3] * gm[3])};
+                }
+                float ss = (x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]);
+                ss += __shfl_xor(ss, 16, RH_WAVE);  // the token's 4 lane groups, in a fixed order
+                ss += __shfl_xor(ss, 32, RH_WAVE);
+                if (g == 0) a.ssq_out[(size_t)blockIdx.x * 16 + r] = ss;
+            }
         } else {  // GV_QKV
             if (!xvalid || n >= N) return;
             const int pos = *a.pos;
@@ -331,6 +387,8 @@ hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t st) {
     if (a.K % 128 != 0 || a.B < 1 || a.B > 16 || a.N % 4 != 0) return hipErrorInvalidValue;
     if (a.am_val && (epi != GV_F32 || !a.am_idx)) return hipErrorInvalidValue;
     if (a.xres && (epi == GV_RESID || !a.gamma || !gemv_norm_fits(a.B, a.K))) return hipErrorInvalidValue;
+    if (a.ssq_out && (epi != GV_RESID || !a.xg_out || !a.gnext)) return hipErrorInvalidValue;
+    if (a.rs_part && (epi == GV_RESID || a.xres || a.rs_n < 1 || a.rs_n > 512)) return hipErrorInvalidValue;
     const int v = a.cfg > 0 ? a.cfg : pick_variant(epi, a);
     if (v > kNumVariants) return hipErrorInvalidValue;
     const int nblk = (a.N + 15) / 16;

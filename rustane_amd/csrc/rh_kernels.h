@@ -133,6 +133,17 @@ struct GemvArgs {
     const float* xres;
     const float* gamma;
     float eps;
+    // Optional, GV_RESID: also write the next RMSNorm's input as
+    // xg_out [B, N] = fp16(x_new * gnext) and this block's per-token sum of
+    // x_new^2 over its 16 rows, ssq_out[blockIdx * 16 + token].
+    f16* xg_out;
+    const float* gnext;
+    float* ssq_out;
+    // Optional, not GV_RESID: X holds such fp16(x * gamma) rows; each
+    // token's 1/rms comes from rs_n blocks of ssq partials (rs_part) and eps,
+    // and scales the accumulators before the epilogue.
+    const float* rs_part;
+    int rs_n;
 };
 // W is fp16 [N, K] in fragment order (frag_off), rows padded to a multiple of 16.
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t st);

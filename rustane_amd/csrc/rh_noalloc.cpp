@@ -61,6 +61,7 @@ size_t layout(const rh_ctx* ctx, int B, bool own_logits, unsigned char* base, rh
     b->am_v = (float*)take(am * 4);
     b->am_i = (int*)take(am * 4);
     b->state = (int*)take(2 * 4);
+    b->ssq = (float*)take(D * 4);
     return off;
 }
 

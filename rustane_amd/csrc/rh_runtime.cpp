@@ -260,15 +260,26 @@ int rhrt::enqueue_decode_step(rh_ctx* ctx, int B, const DecodeBufs& b) {
     const float alpha = 1.0f / std::sqrt(2.0f * (float)c.nlayers);
     const bool fuse_norm = rh::gemv_norm_fits(B, D);
     hipStream_t st = ctx->stream;
-    // input of a normed GEMV: fused (xres + gamma) or via the row kernel (X)
+    // Input of a normed GEMV.  Small B: the GEMV normalises x itself (xres +
+    // gamma).  Larger B: the residual GEMV before it left fp16(x * gamma) in
+    // dxn and per-block sums of squares in ssq, and the GEMV scales by 1/rms
+    // (xg); the first norm of the step, after the embedding, is a row kernel.
+    bool xg = false;
     auto normed = [&](rh::GemvArgs& g, const float* gamma) -> int {
         if (fuse_norm) {
             g.xres = b.dx; g.gamma = gamma; g.eps = c.rms_eps;
+        } else if (xg) {
+            g.X = b.dxn; g.rs_part = b.ssq; g.rs_n = D / 16; g.eps = c.rms_eps;
         } else {
             LCK(rh::launch_rmsnorm(b.dx, gamma, b.dxn, B, D, c.rms_eps, st));
             g.X = b.dxn;
         }
         return RH_OK;
+    };
+    auto produce = [&](rh::GemvArgs& g, const float* gnext) {
+        if (fuse_norm || !b.ssq) return;
+        g.xg_out = b.dxn; g.gnext = gnext; g.ssq_out = b.ssq;
+        xg = true;
     };
     LCK(rh::launch_embed(b.tok_in, ctx->embed, b.dx, B, D, c.vocab, ctx->d_err, st));
     for (int l = 0; l < c.nlayers; ++l) {
@@ -288,6 +299,7 @@ int rhrt::enqueue_decode_step(rh_ctx* ctx, int B, const DecodeBufs& b) {
         g = rh::GemvArgs{};
         g.W = W.wo; g.X = b.dattn; g.B = B; g.N = D; g.K = D;
         g.out_f32 = b.dx; g.ldo = D; g.alpha = alpha;
+        produce(g, W.g2);
         RCK(timed(ctx, RH_K_GEMV_WO, [&] { return rh::launch_gemv(rh::GV_RESID, g, st); }));
         g = rh::GemvArgs{};
         RCK(normed(g, W.g2));
@@ -297,6 +309,7 @@ int rhrt::enqueue_decode_step(rh_ctx* ctx, int B, const DecodeBufs& b) {
         g = rh::GemvArgs{};
         g.W = W.w2; g.X = b.dgate; g.B = B; g.N = D; g.K = F;
         g.out_f32 = b.dx; g.ldo = D; g.alpha = alpha;
+        produce(g, l + 1 < c.nlayers ? ctx->L[l + 1].g1 : ctx->gfinal);
         RCK(timed(ctx, RH_K_GEMV_W2, [&] { return rh::launch_gemv(rh::GV_RESID, g, st); }));
     }
     rh::GemvArgs g{};
@@ -314,7 +327,7 @@ rhrt::DecodeBufs rhrt::ctx_decode_bufs(rh_ctx* ctx) {
     DecodeBufs b{};
     b.dx = ctx->dx; b.dxn = ctx->dxn; b.dq = ctx->dq; b.dattn = ctx->dattn; b.dgate = ctx->dgate;
     b.dlogits = ctx->dlogits; b.pm = ctx->pm; b.pl = ctx->pl; b.po = ctx->po;
-    b.am_v = ctx->dam_v; b.am_i = ctx->dam_i; b.state = ctx->dstate;
+    b.am_v = ctx->dam_v; b.am_i = ctx->dam_i; b.state = ctx->dstate; b.ssq = ctx->dssq;
     b.tok_in = ctx->dtok; b.tok_out = ctx->dout; b.next_in = ctx->dtok; b.seq = ctx->dseq;
     return b;
 }
@@ -491,6 +504,7 @@ int rh_create(const rh_config* cfg, int device, int max_batch, int max_ctx, rh_c
             (rc = dalloc(ctx, &ctx->pl, (size_t)Bd * c.heads * nch)) ||
             (rc = dalloc(ctx, &ctx->po, (size_t)Bd * c.heads * nch * c.head_dim)) ||
             (rc = dalloc(ctx, &ctx->dstate, 2)) || (rc = dalloc(ctx, &ctx->dtok, 16)) ||
+            (rc = dalloc(ctx, &ctx->dssq, D)) ||
             (rc = dalloc(ctx, &ctx->dout, 16)) || (rc = dalloc(ctx, &ctx->dseq, (size_t)max_ctx * 16)) ||
             (rc = dalloc(ctx, &ctx->dam_v, (size_t)rh::gemv_argmax_blocks(c.vocab) * 16)) ||
             (rc = dalloc(ctx, &ctx->dam_i, (size_t)rh::gemv_argmax_blocks(c.vocab) * 16)))

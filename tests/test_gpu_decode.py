@@ -121,11 +121,13 @@ def test_decode_batch16_long_context_hd128(orc):
             assert err <= LOGIT_ATOL, (p, err)
 
 
-@pytest.mark.parametrize("dim,batch", [(256, 2), (2048, 16)])
+@pytest.mark.parametrize("dim,batch", [(256, 2), (2048, 9), (2048, 16)])
 def test_decode_nonunit_gammas(orc, dim, batch):
     """Random gammas through the decode norms: at dim 256 the RMSNorm is fused
-    into the GEMV (the normalised rows fit in LDS), at dim 2048 x 16 rows it
-    runs as its own kernel."""
+    into the GEMV (the normalised rows fit in LDS); at dim 2048 x 9 or 16 rows
+    the first norm of a step is a row kernel and the others come from the
+    residual GEMVs (x * gamma and sums of squares) with 1/rms applied by the
+    next GEMV (9: seven padded token rows in the MFMA tiles)."""
     cfg = small_cfg(dim=dim, hidden=1024, heads=dim // 128, hd=128, nlayers=2, vocab=1024, seq=40)
     w = random_gammas(ModelWeights.normal(cfg, seed=53), seed=54)
     tok, tgt = tokens_uniform(55, cfg.vocab, batch, cfg.seq)
