@@ -104,7 +104,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int k = 0; k < 32; ++k) {
                 const int i = q + 16 * k;
-                pv[k] = i < a.rs_n ? a.rs_part[i * 16 + t] : 0.f;
+                pv[k] = i < a.rs_n && t < a.B ? a.rs_part[i * 16 + t] : 0.f;
             }
         }
     }
