@@ -489,6 +489,23 @@ __global__ __launch_bounds__(256 * NG) void attn_prefill_dma_kernel(const f16* _
     }
 }
 
+// Sum over the N (8 or 16) consecutive lanes of a DPP row, in every one of
+// them: quad pairs, quad halves, then the mirrored halves of 8 and of 16.
+// Each step adds a lane's value to its partner's, so partners hold equal sums
+// (addition commutes) and the N lanes end bitwise equal.  DPP moves stay in
+// the VALU; __shfl_xor goes through the LDS crossbar (ds_bpermute).
+#define RH_DPP_STEP(v, ctrl) \
+    ((v) + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, true)))
+template <int N>
+__device__ __forceinline__ float row_sum_dpp(float v) {
+    static_assert(N == 8 || N == 16, "8 or 16 lanes");
+    v = RH_DPP_STEP(v, 0xB1);   // quad_perm [1, 0, 3, 2]
+    v = RH_DPP_STEP(v, 0x4E);   // quad_perm [2, 3, 0, 1]
+    v = RH_DPP_STEP(v, 0x141);  // row_half_mirror: lane i <-> 7 - i within 8
+    if constexpr (N == 16) v = RH_DPP_STEP(v, 0x140);  // row_mirror: lane i <-> 15 - i
+    return v;
+}
+
 // Decode attention: one block per (chunk, head, sequence), 4 waves.  A chunk
 // covers `per` consecutive positions (0: ceil(positions / chunks), computed
 // on the device from the current position), split evenly over the 4 waves.
@@ -556,8 +573,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict_
             float d = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) d += (float)qv[e] * (float)kr[i][e];
-#pragma unroll
-            for (int x = LPP / 2; x > 0; x >>= 1) d += __shfl_xor(d, x, RH_WAVE);
+            d = row_sum_dpp<LPP>(d);
             sc[i] = tb + i * SL < w1 ? d * scale : -INFINITY;
             mloc = fmaxf(mloc, sc[i]);
         }
