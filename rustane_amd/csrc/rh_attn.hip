@@ -505,6 +505,7 @@ __device__ __forceinline__ float row_sum_dpp(float v) {
     if constexpr (N == 16) v = RH_DPP_STEP(v, 0x140);  // row_mirror: lane i <-> 15 - i
     return v;
 }
+#undef RH_DPP_STEP
 
 // Decode attention: one block per (chunk, head, sequence), 4 waves.  A chunk
 // covers `per` consecutive positions (0: ceil(positions / chunks), computed

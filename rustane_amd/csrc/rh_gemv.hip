@@ -21,7 +21,10 @@
 // GEMV that updates x also writes fp16(x * gamma_next) and per-block sums of
 // x^2 per token; the next GEMV sums those partials in a fixed order, takes
 // x * gamma as its fp16 input and scales its accumulators by each token's
-// 1/rms -- the RMSNorm with no launch of its own (rs_part / ssq_out).
+// 1/rms -- the RMSNorm (rmsnorm::forward_channel_first, cpu/rmsnorm.rs:149-183)
+// with no launch of its own (rs_part / ssq_out): rmsnorm(x) * gamma . W =
+// (1/rms) * ((x * gamma) . W), rounded to fp16 before instead of after the
+// 1/rms factor.
 //
 // NORM: the input is the fp32 residual stream and the block applies the
 // RMSNorm itself (rmsnorm::forward_channel_first, cpu/rmsnorm.rs:149-183)
