@@ -74,13 +74,28 @@ int rh_context_info(const rh_ctx* ctx, rh_config* cfg_out, int* max_batch_out, i
  * nlayers*9 pointers in RSTK order (bin/train.rs:238-345):
  *   wq[D,D] wk[D,D] wv[D,D] wo[D,D] w1[D,F] w3[D,F] w2[D,F] gamma1[D] gamma2[D]
  * (wq/wk/wv/wo/w1/w3 are in x out; w2 is out x in, used transposed).
- * The fp32 matrices are also kept on the device as the optimizer's master
- * weights (allocated by the first load, 4 bytes per parameter), so
- * rh_read_weights_f32 returns them exactly and training resumes from them;
- * any optimizer moments restart from zero (ModelOptState::zeros after
- * load_checkpoint, bin/train.rs:444-449). */
+ * Each matrix passes through a device staging buffer the size of the
+ * largest tensor.  When the context keeps fp32 master weights
+ * (rh_set_fp32_masters, or once an optimizer state exists) the matrices
+ * land in them instead, so rh_read_weights_f32 returns them exactly and
+ * training continues from the exact values; any optimizer moments restart
+ * from zero (ModelOptState::zeros after load_checkpoint,
+ * bin/train.rs:444-449). */
 int rh_load_weights_f32(rh_ctx* ctx, const float* embed, const float* gamma_final,
                         const float* const* layer_tensors);
+
+/* Whether the context keeps fp32 master weights on the device (4 bytes per
+ * parameter: 26.4 GB at 7B, twice the fp16 weights).  Off by default, so
+ * forward-only and decode contexts hold the fp16 weights alone.  keep = 1
+ * allocates them now (holding the current weights widened from fp16) and
+ * makes later fp32 loads write through them; a training run calls it right
+ * after rh_create, where the reference compiles its kernels before
+ * load_checkpoint / ModelWeights::random (bin/train.rs:427-448), so the
+ * optimizer starts from the exact fp32 weights.  keep = 0 frees them
+ * (RH_ESTATE once the optimizer state exists, which owns them).  Without
+ * masters, the first rh_update_weights creates them from the fp16 device
+ * weights.  No counterpart in the reference, whose weights are host fp32. */
+int rh_set_fp32_masters(rh_ctx* ctx, int keep);
 
 /* Downloads the weights in the reference orientation: the fp32 masters when
  * they hold the current weights (after an fp32 load or an optimizer step),
@@ -125,6 +140,29 @@ int rh_forward_dev(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets,
  * returning.  mean_loss_out nullable [batch].  Needs hidden % 64 == 0. */
 int rh_forward_backward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
                         float loss_scale, float* mean_loss_out);
+/* The same pass in two calls, for callers of full_model::forward ->
+ * ForwardResult (full_model.rs:120-129, 915-991) followed by
+ * full_model::backward(&fwd, tokens, softcap, loss_scale, grads)
+ * (full_model.rs:996-1010), e.g. crates/engine/tests/phase4_training.rs:61-72.
+ * rh_forward_train runs the training forward with logit softcap `softcap`
+ * (mean_loss_out nullable [batch]) and keeps its caches on the device; *out
+ * receives a handle to them (free it with rh_forward_result_free).
+ * rh_backward adds loss_scale times the gradient of that forward to the
+ * gradients (as rh_forward_backward does: forward then backward gives the
+ * same gradients bit for bit) and, when grad_norm_out is not NULL, writes
+ * the L2 norm of the accumulated gradients (rh_grad_norm), the reference
+ * backward's return value.  tokens (the forward's input tokens) and softcap
+ * must equal the forward's (RH_EINVAL otherwise).  The caches live in the
+ * context: any later call that runs a forward on it (rh_forward*,
+ * rh_prefill, rh_validate, rh_forward_backward, another rh_forward_train)
+ * makes the handle stale and rh_backward returns RH_ESTATE.  A handle may
+ * be consumed more than once, each backward accumulating again. */
+typedef struct rh_forward_result rh_forward_result;
+int rh_forward_train(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
+                     float softcap, float* mean_loss_out, rh_forward_result** out);
+int rh_backward(rh_ctx* ctx, const rh_forward_result* fwd, const uint32_t* tokens, float softcap, float loss_scale,
+                float* grad_norm_out);
+void rh_forward_result_free(rh_forward_result* fwd);
 /* ModelGrads::zero_out: sets every gradient to 0. */
 int rh_zero_grads(rh_ctx* ctx);
 /* Copies the gradients to host fp32 arrays in the orientation and RSTK order
@@ -152,14 +190,22 @@ int rh_decode_step(rh_ctx* ctx, int batch, const uint32_t* in_tok, uint32_t* out
  * For callers that cannot allocate device memory or runtime objects (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  in_tok [batch], out_tok [batch] and logits_out (nullable
- * [batch, vocab]) are DEVICE pointers; batch must equal the prefill batch.
- * The step is enqueued on the context stream without synchronising (rh_sync
- * waits and reports clamped out-of-range ids) and the position advances by
- * one.  Its scratch (activations, attention partials, argmax partials,
- * position state; the logits too when logits_out is NULL) lives in a fixed
- * 64 MiB device array per GPU, shared by every call on that GPU: calls whose
- * work overlaps on one GPU race.  RH_ERANGE when the batch and model need
- * more scratch than that (7B at batch 16 needs about 4 MiB). */
+ * [batch, vocab]) are DEVICE pointers (in_tok may equal out_tok: each step
+ * then feeds its argmax to the next); batch must equal the prefill batch.
+ * The step is enqueued on the context stream (rh_stream) without
+ * synchronising; rh_sync waits and reports clamped out-of-range ids.  The
+ * step reads and advances the context's device-side position, so a step
+ * captured into a graph (on the context stream) moves forward on every
+ * replay; the next rh_decode_step, rh_decode or rh_decode_pos re-reads that
+ * position.  A replay at a full cache writes nothing to it and its outputs
+ * are undefined (rh_sync then returns RH_ERANGE).  Its scratch
+ * (activations, attention and argmax partials; the logits too when
+ * logits_out is NULL) lives in a fixed 64 MiB device array per GPU, cut
+ * into four 16 MiB slots: a context takes one at its first call and keeps
+ * it until rh_destroy, so up to four contexts per GPU use this entry point
+ * at once (RH_ERANGE for a fifth), and no two share scratch.  RH_ERANGE
+ * when the batch and model need more than a slot (7B at batch 16 needs
+ * about 4 MiB). */
 int rh_decode_step_noalloc(rh_ctx* ctx, int batch, const uint32_t* in_tok, uint32_t* out_tok,
                            float* logits_out);
 
@@ -278,12 +324,13 @@ int rh_grad_norm(rh_ctx* ctx, float* norm_out);
  * multiplied by grad_scale: the embedding at lr * embed_lr_scale and the
  * gammas at lr without weight decay, the seven matrices per layer at
  * lr * matrix_lr_scale with weight_decay.  The first call allocates the
- * optimizer state: first and second moments (zero) and, unless an fp32
- * load made them, the fp32 master weights (read from the fp16 device
- * weights).  rh_load_weights_f32 and rh_load_checkpoint write the masters
- * exactly, rh_init_weights_normal leaves them to be re-read from the fp16
- * copy; every weight write restarts the moments from zero.  After an update
- * rh_read_weights_f32 (and rh_save_checkpoint) return the fp32 masters. */
+ * optimizer state: first and second moments (zero) and, unless
+ * rh_set_fp32_masters made them, the fp32 master weights (read from the
+ * fp16 device weights).  With masters, rh_load_weights_f32 and
+ * rh_load_checkpoint write them exactly, rh_init_weights_normal leaves them
+ * to be re-read from the fp16 copy; every weight write restarts the moments
+ * from zero.  After an update rh_read_weights_f32 (and rh_save_checkpoint)
+ * return the fp32 masters. */
 int rh_update_weights(rh_ctx* ctx, uint32_t t, float lr, const rh_train_config* tc, float grad_scale);
 /* train_step / train_step_with_options (full_model.rs:1488-1600): zero the
  * gradients; accum_steps sequences of the context's seq from `data` at

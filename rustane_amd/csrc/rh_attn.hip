@@ -538,7 +538,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict_
     const int j = lane % LPP, slot = lane / LPP;
     const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int nch = gridDim.x;
-    const int nctx = *pos + 1;
+    const int nctx = min(*pos + 1, ctx);  // a position past the cache attends over the whole cache
     const int per = per_fixed > 0 ? per_fixed : (nctx + nch - 1) / nch;
     const int t0 = min(chunk * per, nctx), t1 = min(nctx, t0 + per);
     const size_t bh = (size_t)b * H + h;

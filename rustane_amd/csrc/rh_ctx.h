@@ -52,8 +52,11 @@ struct rh_ctx {
     float2* rope = nullptr;
     int rope_len = 0;
 
-    // forward / prefill workspace (grow-only, sized for M = B*S rows)
+    // forward / prefill workspace (grow-only, sized for M = B*S rows);
+    // work_epoch counts the calls that write it (a kept training forward is
+    // valid while the count is unchanged)
     int ws_M = 0;
+    uint64_t work_epoch = 0;
     float *x = nullptr, *logits = nullptr, *tok_loss = nullptr, *mean = nullptr;
     f16 *xn = nullptr, *q = nullptr, *kbuf = nullptr, *vbuf = nullptr, *attn = nullptr, *gate = nullptr;
     uint32_t *d_tok = nullptr, *d_tgt = nullptr;
@@ -73,6 +76,9 @@ struct rh_ctx {
     float* dam_v = nullptr;  // [argmax blocks][16] argmax partials of the logits GEMV
     int* dam_i = nullptr;
     int dec_B = 0, host_pos = 0;
+    // an allocation-free step ran since the prefill (a captured one may be
+    // replayed any time): host-side calls re-read the position from dstate
+    bool pos_on_device = false;
     bool have_prefill = false;
     bool use_graphs = true;
     hipGraphExec_t dgraph = nullptr;
@@ -180,9 +186,13 @@ TensorMap layer_map(rh_ctx* ctx, int l, int j);
 // embedding) kept by the optimizer, or null when there is none or the
 // device weights changed since it was written.
 const float* train_master(const rh_ctx* ctx, int l, int j);
-// The fp32 master of weight tensor j of layer l (j = -1: the embedding),
-// allocating the masters on first use; a weight load writes through it.
-int master_for_load(rh_ctx* ctx, int l, int j, float** out);
+// The fp32 master weights: whether they exist, where tensor j of layer l
+// (j = -1: the embedding) lives among them, their allocation (all or none)
+// and their release (refused while optimizer moments exist).
+bool have_masters(const rh_ctx* ctx);
+float* master_ptr(rh_ctx* ctx, int l, int j);
+int ensure_masters(rh_ctx* ctx);
+int drop_masters(rh_ctx* ctx);
 // After a weight write (wgen already bumped): the masters hold the new
 // weights when masters_hold_them is set (an fp32 load), otherwise they are
 // stale; the moments restart from zero (ModelOptState::zeros).
@@ -196,8 +206,8 @@ int ensure_workspace(rh_ctx* ctx, int M);
 int check_tokens(rh_ctx* ctx, const uint32_t* t, size_t n);
 int check_err_flag(rh_ctx* ctx);
 // Logits (+ CE loss rows and per-sequence means) from the final-norm rows in
-// ctx->xn, or in xf when given.
-int enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss, const f16* xf = nullptr);
+// ctx->xn, or in xf when given; softcap < 0: the context's.
+int enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss, const f16* xf = nullptr, float softcap = -1.f);
 
 // Device buffers one greedy decode step uses besides the weights and the KV
 // cache: the residual rows, normalised rows, q, attention output and gate of
@@ -226,5 +236,7 @@ int enqueue_decode_step(rh_ctx* ctx, int B, const DecodeBufs& b);
 // rh_decode_step_noalloc on ctx->device (once per device; the device must be
 // current).  Called by rh_create.
 int noalloc_init(rh_ctx* ctx);
+// Frees the context's scratch slot (rh_destroy).
+void noalloc_release(const rh_ctx* ctx);
 
 }  // namespace rhrt

@@ -261,12 +261,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
             }
         } else {  // GV_QKV
             if (!xvalid || n >= N) return;
-            const int pos = *a.pos;
+            // a position past the cache (a captured step replayed too often):
+            // RoPE at the last slot, no K/V write
+            const int pos = *a.pos, pr = min(pos, a.ctx - 1);
             const int sec = n / a.D, cc = n - sec * a.D;
             const int h = cc / a.hd, d = cc - h * a.hd;
+            if (sec > 0 && pos >= a.ctx) return;
             if (sec < 2) {
-                const float2 cs0 = a.rope[(size_t)pos * (a.hd / 2) + d / 2];
-                const float2 cs1 = a.rope[(size_t)pos * (a.hd / 2) + d / 2 + 1];
+                const float2 cs0 = a.rope[(size_t)pr * (a.hd / 2) + d / 2];
+                const float2 cs1 = a.rope[(size_t)pr * (a.hd / 2) + d / 2 + 1];
                 const float r0 = v0 * cs0.x + (-v1) * cs0.y, r1 = v1 * cs0.x + v0 * cs0.y;
                 const float r2 = v2 * cs1.x + (-v3) * cs1.y, r3 = v3 * cs1.x + v2 * cs1.y;
                 v0 = r0; v1 = r1; v2 = r2; v3 = r3;
@@ -286,10 +289,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
 // each strided over its token's partials with 8 coalesced loads of each
 // array in flight, then the token's waves merge through LDS.
 // Writes out[b], next_in[b] and seq_out[state[1] * B + b]; then (advance)
-// state[0] += 1, state[1] += 1.
+// state[0] += 1, state[1] += 1 while the position is inside the cache
+// (state[0] < limit); a step run at a position past it (a captured step
+// replayed too often) wrote nothing to the cache and sets ERR_PAST_CACHE in
+// *err instead.
 __global__ __launch_bounds__(1024) void argmax_final_kernel(const float* pv, const int* pi, int nblk,
                                                             int B, uint32_t* out, uint32_t* next_in,
-                                                            uint32_t* seq_out, int* state, int advance) {
+                                                            uint32_t* seq_out, int* state, int advance,
+                                                            int limit, int* err) {
     __shared__ float sv[16];
     __shared__ int si[16];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -331,7 +338,14 @@ __global__ __launch_bounds__(1024) void argmax_final_kernel(const float* pv, con
     }
     if (!advance) return;
     __syncthreads();  // every token's writer has read state[1]
-    if (threadIdx.x == 0) { state[0] += 1; state[1] += 1; }
+    if (threadIdx.x == 0) {
+        if (state[0] < limit) {
+            state[0] += 1;
+            state[1] += 1;
+        } else if (err) {
+            atomicOr(err, ERR_PAST_CACHE);
+        }
+    }
 }
 
 // (NW, DEPTH) variants selectable through GemvArgs::cfg (1-based).
@@ -413,11 +427,11 @@ hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t st) {
 int gemv_argmax_blocks(int N) { return (N + 15) / 16; }
 
 hipError_t launch_argmax_final(const float* pv, const int* pi, int nblk, int B, uint32_t* out,
-                               uint32_t* next_in, uint32_t* seq_out, int* state, bool advance,
-                               hipStream_t st) {
+                               uint32_t* next_in, uint32_t* seq_out, int* state, bool advance, int limit,
+                               int* err, hipStream_t st) {
     if (B < 1 || B > 16 || nblk < 1) return hipErrorInvalidValue;
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(1024), 0, st, pv, pi, nblk, B, out, next_in,
-                       seq_out, state, advance ? 1 : 0);
+                       seq_out, state, advance ? 1 : 0, limit, err);
     return hipGetLastError();
 }
 

@@ -153,10 +153,14 @@ bool gemv_norm_fits(int B, int K);
 int gemv_argmax_blocks(int N);
 // Greedy token from the logits GEMV's argmax partials (ties -> lowest id):
 // writes out[b], next_in[b] (nullable), seq_out[state[1]*B + b] (nullable),
-// then state[0] += 1, state[1] += 1 when advance is set.
+// then state[0] += 1, state[1] += 1 when advance is set and state[0] < limit
+// (else ERR_PAST_CACHE is or-ed into *err, when err is not null).
 hipError_t launch_argmax_final(const float* pv, const int* pi, int nblk, int B, uint32_t* out,
-                               uint32_t* next_in, uint32_t* seq_out, int* state, bool advance,
-                               hipStream_t st);
+                               uint32_t* next_in, uint32_t* seq_out, int* state, bool advance, int limit,
+                               int* err, hipStream_t st);
+// Bit of the context's device error word: a decode step ran at a position
+// past the KV cache (its other bits count clamped token ids).
+constexpr int ERR_PAST_CACHE = 1 << 30;
 
 // ---------------- row ops ----------------
 hipError_t launch_embed(const uint32_t* tok, const f16* E, float* x, int rows, int D, int V,

@@ -76,6 +76,7 @@ void drop_graphs(rh_ctx* ctx) {
 }
 
 int ensure_workspace(rh_ctx* ctx, int M) {
+    ctx->work_epoch += 1;  // every caller writes the workspace next
     if (M <= ctx->ws_M) return RH_OK;
     HCK(hipStreamSynchronize(ctx->stream));
     drop_graphs(ctx);  // captured forwards hold the old buffers' addresses
@@ -182,13 +183,13 @@ int enqueue_body(rh_ctx* ctx, int B, int S, bool to_cache, bool final_norm) {
 // the final RMSNorm of every row.
 }  // namespace
 
-int rhrt::enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss, const f16* xf) {
+int rhrt::enqueue_tail(rh_ctx* ctx, int B, int S, bool with_loss, const f16* xf, float softcap) {
     const rh_config& c = ctx->cfg;
     const int M = B * S, D = c.dim;
     hipStream_t st = ctx->stream;
     rh::GemmArgs g{};
     g.W = ctx->embed; g.X = xf ? xf : ctx->xn; g.M = M; g.N = c.vocab; g.K = D;
-    g.out_f32 = ctx->logits; g.ldo = c.vocab; g.softcap = c.softcap;
+    g.out_f32 = ctx->logits; g.ldo = c.vocab; g.softcap = softcap < 0.f ? c.softcap : softcap;
     set_sk(ctx, g);
     RCK(timed(ctx, RH_K_GEMM_LOGITS, [&] { return rh::launch_gemm(rh::EPI_F32, g, st); }));
     if (with_loss) {
@@ -319,7 +320,7 @@ int rhrt::enqueue_decode_step(rh_ctx* ctx, int B, const DecodeBufs& b) {
     g.am_val = b.am_v; g.am_idx = b.am_i;
     RCK(timed(ctx, RH_K_GEMV_LOGITS, [&] { return rh::launch_gemv(rh::GV_F32, g, st); }));
     LCK(rh::launch_argmax_final(b.am_v, b.am_i, rh::gemv_argmax_blocks(c.vocab), B, b.tok_out, b.next_in, b.seq,
-                                b.state, true, st));
+                                b.state, true, ctx->max_ctx, ctx->d_err, st));
     return RH_OK;
 }
 
@@ -386,6 +387,8 @@ int rhrt::check_err_flag(rh_ctx* ctx) {
     if (h != 0) {
         const int z = 0;
         HCK(hipMemcpy(ctx->d_err, &z, sizeof(int), hipMemcpyHostToDevice));
+        if (h & rh::ERR_PAST_CACHE)
+            return fail(ctx, RH_ERANGE, "a decode step ran past the end of the KV cache; its outputs are undefined");
         return fail(ctx, RH_ERANGE, std::to_string(h) + " token id(s) >= vocab were clamped to 0");
     }
     return RH_OK;
@@ -420,6 +423,19 @@ int unpack_to_staging(rh_ctx* ctx, const TensorMap& m) {
     return RH_OK;
 }
 
+// Re-reads the decode position from the device once allocation-free steps
+// have run since the prefill: a captured one may be replayed at any time,
+// so the device's copy stays the authority until the next prefill.
+int sync_pos(rh_ctx* ctx) {
+    if (!ctx->pos_on_device) return RH_OK;
+    HCK(hipSetDevice(ctx->device));
+    int st[2] = {0, 0};
+    HCK(hipMemcpyAsync(st, ctx->dstate, sizeof st, hipMemcpyDeviceToHost, ctx->stream));
+    HCK(hipStreamSynchronize(ctx->stream));
+    ctx->host_pos = st[0];
+    return RH_OK;
+}
+
 void destroy_ctx(rh_ctx* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
@@ -428,6 +444,7 @@ void destroy_ctx(rh_ctx* ctx) {
     for (auto& p : ctx->prof)
         for (auto& e : p.ev) { (void)hipEventDestroy(e.first); (void)hipEventDestroy(e.second); }
     rhrt::train_state_free(ctx->train);
+    rhrt::noalloc_release(ctx);
     for (void* p : ctx->allocs) (void)hipFree(p);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -528,12 +545,14 @@ int rh_load_weights_f32(rh_ctx* ctx, const float* embed, const float* gamma_fina
     const size_t D = c.dim, F = c.hidden, V = c.vocab;
     for (int i = 0; i < 9 * c.nlayers; ++i)
         if (!layer_tensors[i]) return fail(ctx, RH_EINVAL, "null layer tensor " + std::to_string(i));
-    // Each matrix lands in its fp32 master copy (kept for the optimizer and
-    // rh_read_weights_f32, so training resumes from the exact values), which
-    // is then packed to the fp16 device layout.
+    // With fp32 masters (rh_set_fp32_masters, or an optimizer state) each
+    // matrix lands in its master copy, which is then packed to the fp16
+    // device layout; otherwise it passes through a staging buffer the size
+    // of the largest tensor.
+    const bool masters = have_masters(ctx);
+    if (!masters) RCK(ensure_staging(ctx, std::max({V * D, D * F, D * D})));
     hipStream_t st = ctx->stream;
-    float* mst = nullptr;
-    RCK(master_for_load(ctx, 0, -1, &mst));
+    float* mst = masters ? master_ptr(ctx, 0, -1) : ctx->staging;
     HCK(hipMemcpyAsync(mst, embed, V * D * sizeof(float), hipMemcpyHostToDevice, st));
     LCK(rh::launch_pack_rows(mst, ctx->embed, (int)V, (int)D, st));
     HCK(hipMemcpyAsync(ctx->gfinal, gamma_final, D * sizeof(float), hipMemcpyHostToDevice, st));
@@ -541,7 +560,7 @@ int rh_load_weights_f32(rh_ctx* ctx, const float* embed, const float* gamma_fina
         const float* const* t = layer_tensors + 9 * l;
         for (int j = 0; j < 7; ++j) {
             const TensorMap m = layer_map(ctx, l, j);
-            RCK(master_for_load(ctx, l, j, &mst));
+            mst = masters ? master_ptr(ctx, l, j) : ctx->staging;
             HCK(hipMemcpyAsync(mst, t[j], (size_t)m.R * m.C * sizeof(float), hipMemcpyHostToDevice, st));
             RCK(pack_from(ctx, mst, m));
         }
@@ -550,9 +569,31 @@ int rh_load_weights_f32(rh_ctx* ctx, const float* embed, const float* gamma_fina
     }
     HCK(hipStreamSynchronize(st));
     ++ctx->wgen;
-    RCK(weights_written(ctx, true));
-    (void)F;
+    RCK(weights_written(ctx, masters));
     return RH_OK;
+}
+
+int rh_set_fp32_masters(rh_ctx* ctx, int keep) {
+    if (!ctx) return RH_EINVAL;
+    HCK(hipSetDevice(ctx->device));
+    if (!keep) return drop_masters(ctx);
+    if (have_masters(ctx)) return RH_OK;
+    RCK(ensure_masters(ctx));
+    // until the next fp32 load they hold the current fp16 device weights
+    const rh_config& c = ctx->cfg;
+    hipStream_t st = ctx->stream;
+    LCK(rh::launch_unpack_rows(ctx->embed, master_ptr(ctx, 0, -1), c.vocab, c.dim, st));
+    for (int l = 0; l < c.nlayers; ++l)
+        for (int j = 0; j < 7; ++j) {
+            const TensorMap m = layer_map(ctx, l, j);
+            if (m.map < 0) {
+                LCK(rh::launch_unpack_rows(m.dst, master_ptr(ctx, l, j), m.R, m.C, st));
+            } else {
+                LCK(rh::launch_unpack_transpose(m.dst, master_ptr(ctx, l, j), m.R, m.C, m.ldd, m.map, m.row_off, st));
+            }
+        }
+    HCK(hipStreamSynchronize(st));
+    return weights_written(ctx, true);
 }
 
 int rh_read_weights_f32(rh_ctx* ctx, float* embed, float* gamma_final, float* const* layer_tensors) {
@@ -697,7 +738,7 @@ int rh_prefill(rh_ctx* ctx, const uint32_t* tokens, int batch, int len, uint32_t
     RCK(timed(ctx, RH_K_GEMV_LOGITS, [&] { return rh::launch_gemv(rh::GV_F32, g, st); }));
     LCK(rh::launch_set_state(ctx->dstate, len, 0, st));
     LCK(rh::launch_argmax_final(ctx->dam_v, ctx->dam_i, rh::gemv_argmax_blocks(c.vocab), batch, ctx->dout,
-                                ctx->dtok, nullptr, ctx->dstate, false, st));
+                                ctx->dtok, nullptr, ctx->dstate, false, ctx->max_ctx, nullptr, st));
     if (next_tok_out) HCK(hipMemcpyAsync(next_tok_out, ctx->dout, batch * sizeof(uint32_t), hipMemcpyDeviceToHost, st));
     if (last_logits_out)
         HCK(hipMemcpyAsync(last_logits_out, ctx->dlogits, (size_t)batch * c.vocab * sizeof(float),
@@ -705,6 +746,7 @@ int rh_prefill(rh_ctx* ctx, const uint32_t* tokens, int batch, int len, uint32_t
     HCK(hipStreamSynchronize(st));
     ctx->dec_B = batch;
     ctx->host_pos = len;
+    ctx->pos_on_device = false;
     ctx->have_prefill = true;
     return check_err_flag(ctx);
 }
@@ -712,6 +754,7 @@ int rh_prefill(rh_ctx* ctx, const uint32_t* tokens, int batch, int len, uint32_t
 int rh_decode_step(rh_ctx* ctx, int batch, const uint32_t* in_tok, uint32_t* out_tok, float* logits_out) {
     if (!ctx || !in_tok) return fail(ctx, RH_EINVAL, "null argument");
     if (!ctx->have_prefill) return fail(ctx, RH_ESTATE, "rh_decode_step before rh_prefill");
+    RCK(sync_pos(ctx));
     if (batch != ctx->dec_B)
         return fail(ctx, RH_EINVAL, "batch " + std::to_string(batch) + " differs from the prefill batch " +
                                         std::to_string(ctx->dec_B));
@@ -735,6 +778,7 @@ int rh_decode_step(rh_ctx* ctx, int batch, const uint32_t* in_tok, uint32_t* out
 int rh_decode(rh_ctx* ctx, int batch, const uint32_t* in_tok, int nsteps, uint32_t* out_tokens) {
     if (!ctx || !in_tok || !out_tokens) return fail(ctx, RH_EINVAL, "null argument");
     if (!ctx->have_prefill) return fail(ctx, RH_ESTATE, "rh_decode before rh_prefill");
+    RCK(sync_pos(ctx));
     if (batch != ctx->dec_B)
         return fail(ctx, RH_EINVAL, "batch " + std::to_string(batch) + " differs from the prefill batch " +
                                         std::to_string(ctx->dec_B));
@@ -763,6 +807,7 @@ int rh_set_softcap(rh_ctx* ctx, float softcap) {
 
 int rh_decode_pos(rh_ctx* ctx, int* pos_out) {
     if (!ctx || !pos_out) return RH_EINVAL;
+    RCK(sync_pos(ctx));
     *pos_out = ctx->host_pos;
     return RH_OK;
 }

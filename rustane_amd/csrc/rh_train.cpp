@@ -80,10 +80,19 @@ struct TrainState {
         bool moments = false;                  // moments and norm partials allocated
         float *emb_m = nullptr, *emb_v = nullptr, *gf_m = nullptr, *gf_v = nullptr;
         std::vector<std::array<float*, 9>> m, v;
-        float* part = nullptr;  // sum-of-squares partials of the gradient norm
-        double* sumsq = nullptr;  // their sum
     };
     Opt* opt = nullptr;
+    // gradient norm: per-block sums of squares of every gradient tensor, their sum
+    float* norm_part = nullptr;
+    double* norm_sum = nullptr;
+    // The kept forward (ForwardResult, full_model.rs:120-129): the caches
+    // above, ctx->logits and ctx->d_tgt hold the forward of fwd_B sequences of
+    // fwd_S tokens run at ctx->work_epoch == fwd_epoch with logit softcap
+    // fwd_softcap; utok/ustart/uidx hold the embedding backward's index.
+    uint64_t fwd_epoch = 0, fwd_id = 0;
+    int fwd_B = 0, fwd_S = 0, fwd_nuniq = 0;
+    float fwd_softcap = 0.f;
+    std::vector<uint32_t> fwd_tokens;
     ~TrainState() {
         if (side) {
             (void)hipStreamSynchronize(side);
@@ -99,14 +108,7 @@ struct TrainState {
 
 void train_state_free(TrainState* t) { delete t; }
 
-int ensure_masters(rh_ctx* ctx);
 int zero_moments(rh_ctx* ctx);
-
-int master_for_load(rh_ctx* ctx, int l, int j, float** out) {
-    RCK(ensure_masters(ctx));
-    *out = j < 0 ? ctx->train->opt->emb : ctx->train->opt->w[l][j];
-    return RH_OK;
-}
 
 int weights_written(rh_ctx* ctx, bool masters_hold_them) {
     TrainState* T = ctx->train;
@@ -153,8 +155,14 @@ int ensure_train_static(rh_ctx* ctx) {
     RCK(dalloc(ctx, &T->dgf, D));
     T->dlay.resize(c.nlayers);
     const size_t sz[9] = {D * D, D * D, D * D, D * D, D * F, D * F, D * F, D, D};
+    size_t nparts = rh::sumsq_blocks(V * D) + rh::sumsq_blocks(D);
     for (auto& g : T->dlay)
-        for (int j = 0; j < 9; ++j) RCK(dalloc(ctx, &g[j], sz[j]));
+        for (int j = 0; j < 9; ++j) {
+            RCK(dalloc(ctx, &g[j], sz[j]));
+            nparts += rh::sumsq_blocks(sz[j]);
+        }
+    RCK(dalloc(ctx, &T->norm_part, nparts));
+    RCK(dalloc(ctx, &T->norm_sum, 1));
     RCK(dalloc(ctx, &T->embed_t, D * Vp));
     T->wt.resize(c.nlayers);
     for (auto& w : T->wt) {
@@ -302,7 +310,7 @@ int enqueue_forward_train(rh_ctx* ctx, int B, int S) {
         f16* nxn = last ? T->xf : T->c[l + 1].xn;
         RCK(timed(ctx, RH_K_GEMM_W2, [&] { return rh::launch_gemm_resid_norm(g, ng, c.rms_eps, nxn, st); }));
     }
-    return enqueue_tail(ctx, B, S, true, T->xf);
+    return enqueue_tail(ctx, B, S, true, T->xf, T->fwd_softcap);
 }
 
 // dgamma (+)= kappa * the partial sums of rms_backward (stores while the
@@ -396,7 +404,7 @@ int enqueue_backward(rh_ctx* ctx, int B, int S, float loss_scale, int nuniq) {
         return RH_OK;
     };
     // CE gradient (internal units), dx_final = dl E, dembed += dl^T x_final
-    LCK(rh::launch_ce_backward(ctx->logits, ctx->d_tgt, T->dlh, M, V, Vp, c.softcap, rh::GRAD_UNIT, st));
+    LCK(rh::launch_ce_backward(ctx->logits, ctx->d_tgt, T->dlh, M, V, Vp, T->fwd_softcap, rh::GRAD_UNIT, st));
     RCK(publish(4));
     LCK(rh::launch_transpose_frag2(T->dlh, T->dlT, M, Vp, T->xf, T->tx[0][0], M, D, Mp, sd));
     RCK(grad_gemm(ctx, T->dlT, T->tx[0][0], V, D, kappa, T->dembed, sd));
@@ -483,7 +491,10 @@ const size_t* tensor_sizes(const rh_config& c, size_t out[9]) {
 
 }  // namespace
 
-// fp32 master weights (reference orientation): allocated once.
+// fp32 master weights (reference orientation), allocated together: the
+// tensors are published only once every allocation has succeeded, so a
+// failed call leaves no partial set behind for a later call to mistake for
+// a complete one.
 int rhrt::ensure_masters(rh_ctx* ctx) {
     RCK(ensure_train_host(ctx));
     TrainState* T = ctx->train;
@@ -496,10 +507,42 @@ int rhrt::ensure_masters(rh_ctx* ctx) {
     const rh_config& c = ctx->cfg;
     size_t sz[9];
     tensor_sizes(c, sz);
-    RCK(dalloc(ctx, &o->emb, (size_t)c.vocab * c.dim));
-    o->w.resize(c.nlayers);
-    for (int l = 0; l < c.nlayers; ++l)
-        for (int j = 0; j < 7; ++j) RCK(dalloc(ctx, &o->w[l][j], sz[j]));
+    float* emb = nullptr;
+    std::vector<std::array<float*, 7>> w(c.nlayers);
+    for (auto& a : w) a.fill(nullptr);
+    int rc = dalloc(ctx, &emb, (size_t)c.vocab * c.dim);
+    for (int l = 0; l < c.nlayers && rc == RH_OK; ++l)
+        for (int j = 0; j < 7 && rc == RH_OK; ++j) rc = dalloc(ctx, &w[l][j], sz[j]);
+    if (rc != RH_OK) {
+        dfree(ctx, emb);
+        for (auto& a : w)
+            for (float* p : a) dfree(ctx, p);
+        return rc;
+    }
+    o->w = std::move(w);
+    o->emb = emb;
+    o->synced = 0;  // nothing written yet
+    return RH_OK;
+}
+
+bool rhrt::have_masters(const rh_ctx* ctx) { return ctx->train && ctx->train->opt && ctx->train->opt->emb; }
+
+float* rhrt::master_ptr(rh_ctx* ctx, int l, int j) {
+    return j < 0 ? ctx->train->opt->emb : ctx->train->opt->w[l][j];
+}
+
+// Frees the masters (no optimizer moments may exist: they belong together).
+int rhrt::drop_masters(rh_ctx* ctx) {
+    if (!have_masters(ctx)) return RH_OK;
+    auto* o = ctx->train->opt;
+    if (o->moments) return fail(ctx, RH_ESTATE, "the optimizer state holds the fp32 masters");
+    HCK(hipStreamSynchronize(ctx->stream));
+    dfree(ctx, o->emb);
+    o->emb = nullptr;
+    for (auto& a : o->w)
+        for (float* p : a) dfree(ctx, p);
+    o->w.clear();
+    o->synced = 0;
     return RH_OK;
 }
 
@@ -545,15 +588,11 @@ int ensure_opt(rh_ctx* ctx) {
         RCK(dalloc(ctx, &o->gf_v, D));
         o->m.resize(c.nlayers);
         o->v.resize(c.nlayers);
-        size_t nparts = rh::sumsq_blocks(V * D) + rh::sumsq_blocks(D);
         for (int l = 0; l < c.nlayers; ++l)
             for (int j = 0; j < 9; ++j) {
                 RCK(dalloc(ctx, &o->m[l][j], sz[j]));
                 RCK(dalloc(ctx, &o->v[l][j], sz[j]));
-                nparts += rh::sumsq_blocks(sz[j]);
             }
-        RCK(dalloc(ctx, &o->part, nparts));
-        RCK(dalloc(ctx, &o->sumsq, 1));
         o->moments = true;
         RCK(zero_moments(ctx));
     }
@@ -608,7 +647,6 @@ int rh_grad_norm(rh_ctx* ctx, float* norm_out) {
         return RH_OK;
     }
     HCK(hipSetDevice(ctx->device));
-    RCK(ensure_opt(ctx));
     const rh_config& c = ctx->cfg;
     size_t sz[9];
     tensor_sizes(c, sz);
@@ -620,12 +658,12 @@ int rh_grad_norm(rh_ctx* ctx, float* norm_out) {
     // per-block partials of every tensor, then their sum in double on the device
     size_t off = 0;
     for (auto& t : ts) {
-        LCK(rh::launch_sumsq(t.first, t.second, T->opt->part + off, st));
+        LCK(rh::launch_sumsq(t.first, t.second, T->norm_part + off, st));
         off += rh::sumsq_blocks(t.second);
     }
-    LCK(rh::launch_sum_parts(T->opt->part, off, T->opt->sumsq, st));
+    LCK(rh::launch_sum_parts(T->norm_part, off, T->norm_sum, st));
     double total = 0.0;
-    HCK(hipMemcpyAsync(&total, T->opt->sumsq, sizeof(double), hipMemcpyDeviceToHost, st));
+    HCK(hipMemcpyAsync(&total, T->norm_sum, sizeof(double), hipMemcpyDeviceToHost, st));
     HCK(hipStreamSynchronize(st));
     *norm_out = (float)std::sqrt(total);
     return RH_OK;
@@ -694,6 +732,8 @@ int rh_update_weights(rh_ctx* ctx, uint32_t t, float lr, const rh_train_config* 
 namespace {
 int train_step_body(rh_ctx* ctx, const rh_tokens* data, uint32_t step, const rh_train_config* tc,
                     uint64_t max_pos, float* loss_out, float* grad_norm_out);
+int forward_backward_impl(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
+                          float softcap, float loss_scale, float* mean_loss_out);
 }  // namespace
 
 extern "C" {
@@ -708,11 +748,8 @@ int rh_train_step(rh_ctx* ctx, const rh_tokens* data, uint32_t step, const rh_tr
     if (n < (int64_t)S + 2) return fail(ctx, RH_ERANGE, "token data shorter than seq + 2");
     const uint64_t max_pos = (uint64_t)(n - S - 1);
     // The training forward uses tc->softcap; the context's own softcap (the
-    // one later forwards and decodes use) is restored on every exit.
-    const float saved_softcap = ctx->cfg.softcap;
-    RCK(rh_set_softcap(ctx, tc->softcap));
+    // one forwards and decodes use) is not touched.
     const int rc = train_step_body(ctx, data, step, tc, max_pos, loss_out, grad_norm_out);
-    RCK(rh_set_softcap(ctx, saved_softcap));
     return rc;
 }
 
@@ -739,7 +776,7 @@ int train_step_body(rh_ctx* ctx, const rh_tokens* data, uint32_t step, const rh_
             std::memcpy(&tok[(size_t)j * S], buf.data(), (size_t)S * 4);
             std::memcpy(&tgt[(size_t)j * S], buf.data() + 1, (size_t)S * 4);
         }
-        RCK(rh_forward_backward(ctx, tok.data(), tgt.data(), nb, S, tc->loss_scale, losses.data()));
+        RCK(forward_backward_impl(ctx, tok.data(), tgt.data(), nb, S, tc->softcap, tc->loss_scale, losses.data()));
         for (int j = 0; j < nb; ++j) total += losses[j];
     }
     const float gsc = 1.0f / ((float)tc->accum_steps * tc->loss_scale);
@@ -768,12 +805,23 @@ int rh_zero_grads(rh_ctx* ctx) {
     return RH_OK;
 }
 
-int rh_forward_backward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
-                        float loss_scale, float* mean_loss_out) {
+}  // extern "C"
+
+namespace {
+
+// Host-built index of the embedding backward: every distinct token and its
+// positions, in increasing order.
+struct TokenIndex {
+    std::vector<uint32_t> utok;
+    std::vector<int> start{0}, idx;
+};
+
+// Checks a training forward's arguments and sizes every buffer it needs.
+int prepare_train(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq, float softcap) {
     if (!ctx || !tokens || !targets) return fail(ctx, RH_EINVAL, "null argument");
     if (batch <= 0 || seq <= 0 || batch > ctx->max_batch)
         return fail(ctx, RH_ERANGE, "batch must be in [1, max_batch] and seq >= 1");
-    if (!(loss_scale > 0.f) || !std::isfinite(loss_scale)) return fail(ctx, RH_EINVAL, "loss_scale must be > 0");
+    if (!(softcap >= 0.f) || !std::isfinite(softcap)) return fail(ctx, RH_EINVAL, "softcap must be >= 0");
     const rh_config& c = ctx->cfg;
     if (c.hidden % 64 != 0) return fail(ctx, RH_EINVAL, "the backward pass needs hidden % 64 == 0");
     const size_t M = (size_t)batch * seq;
@@ -785,36 +833,122 @@ int rh_forward_backward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* tar
     RCK(ensure_train_static(ctx));
     RCK(ensure_train_ws(ctx, batch, seq));
     RCK(ensure_packs(ctx));
+    return RH_OK;
+}
+
+// Uploads the tokens, targets and the embedding backward's index (ix must
+// stay alive until the stream has drained) and enqueues the training forward
+// whose caches the backward reads; records it as the kept forward.
+int enqueue_kept_forward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
+                         float softcap, TokenIndex& ix) {
     TrainState* T = ctx->train;
     hipStream_t st = ctx->stream;
-    // positions of each distinct token, in increasing order (embedding backward)
+    const size_t M = (size_t)batch * seq;
     std::map<uint32_t, std::vector<int>> pos;
     for (size_t i = 0; i < M; ++i) pos[tokens[i]].push_back((int)i);
-    std::vector<uint32_t> utok;
-    std::vector<int> start{0}, idx;
     for (auto& kv : pos) {
-        utok.push_back(kv.first);
-        idx.insert(idx.end(), kv.second.begin(), kv.second.end());
-        start.push_back((int)idx.size());
+        ix.utok.push_back(kv.first);
+        ix.idx.insert(ix.idx.end(), kv.second.begin(), kv.second.end());
+        ix.start.push_back((int)ix.idx.size());
     }
     HCK(hipMemcpyAsync(ctx->d_tok, tokens, M * sizeof(uint32_t), hipMemcpyHostToDevice, st));
     HCK(hipMemcpyAsync(ctx->d_tgt, targets, M * sizeof(uint32_t), hipMemcpyHostToDevice, st));
-    HCK(hipMemcpyAsync(T->utok, utok.data(), utok.size() * sizeof(uint32_t), hipMemcpyHostToDevice, st));
-    HCK(hipMemcpyAsync(T->ustart, start.data(), start.size() * sizeof(int), hipMemcpyHostToDevice, st));
-    HCK(hipMemcpyAsync(T->uidx, idx.data(), idx.size() * sizeof(int), hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(T->utok, ix.utok.data(), ix.utok.size() * sizeof(uint32_t), hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(T->ustart, ix.start.data(), ix.start.size() * sizeof(int), hipMemcpyHostToDevice, st));
+    HCK(hipMemcpyAsync(T->uidx, ix.idx.data(), ix.idx.size() * sizeof(int), hipMemcpyHostToDevice, st));
+    T->fwd_softcap = softcap;
+    T->fwd_B = batch;
+    T->fwd_S = seq;
+    T->fwd_nuniq = (int)ix.utok.size();
+    T->fwd_tokens.assign(tokens, tokens + M);
+    T->fwd_epoch = ctx->work_epoch;
+    T->fwd_id += 1;
     RCK(enqueue_forward_train(ctx, batch, seq));
-    {
-        const int rc = enqueue_backward(ctx, batch, seq, loss_scale, (int)utok.size());
-        if (rc != RH_OK) {  // leave no weight-gradient work behind a failed call
-            (void)hipStreamSynchronize(T->side);
-            return rc;
-        }
-    }
-    if (mean_loss_out)
-        HCK(hipMemcpyAsync(mean_loss_out, ctx->mean, batch * sizeof(float), hipMemcpyDeviceToHost, st));
+    return RH_OK;
+}
+
+// The backward of the kept forward, accumulating into the gradients.
+int enqueue_kept_backward(rh_ctx* ctx, float loss_scale) {
+    TrainState* T = ctx->train;
+    const int rc = enqueue_backward(ctx, T->fwd_B, T->fwd_S, loss_scale, T->fwd_nuniq);
+    if (rc != RH_OK) (void)hipStreamSynchronize(T->side);  // leave no weight-gradient work behind
+    return rc;
+}
+
+int forward_backward_impl(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
+                          float softcap, float loss_scale, float* mean_loss_out) {
+    RCK(prepare_train(ctx, tokens, targets, batch, seq, softcap));
+    if (!(loss_scale > 0.f) || !std::isfinite(loss_scale)) return fail(ctx, RH_EINVAL, "loss_scale must be > 0");
+    TokenIndex ix;
+    RCK(enqueue_kept_forward(ctx, tokens, targets, batch, seq, softcap, ix));
+    RCK(enqueue_kept_backward(ctx, loss_scale));
+    hipStream_t st = ctx->stream;
+    if (mean_loss_out) HCK(hipMemcpyAsync(mean_loss_out, ctx->mean, batch * sizeof(float), hipMemcpyDeviceToHost, st));
     HCK(hipStreamSynchronize(st));
     return check_err_flag(ctx);
 }
+
+}  // namespace
+
+struct rh_forward_result {
+    const rh_ctx* ctx;
+    uint64_t id;
+};
+
+extern "C" {
+
+int rh_forward_backward(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
+                        float loss_scale, float* mean_loss_out) {
+    if (!ctx) return RH_EINVAL;
+    return forward_backward_impl(ctx, tokens, targets, batch, seq, ctx->cfg.softcap, loss_scale, mean_loss_out);
+}
+
+int rh_forward_train(rh_ctx* ctx, const uint32_t* tokens, const uint32_t* targets, int batch, int seq,
+                     float softcap, float* mean_loss_out, rh_forward_result** out) {
+    if (!out) return fail(ctx, RH_EINVAL, "null argument");
+    *out = nullptr;
+    RCK(prepare_train(ctx, tokens, targets, batch, seq, softcap));
+    auto* r = new (std::nothrow) rh_forward_result{ctx, 0};
+    if (!r) return fail(ctx, RH_ENOMEM, "out of host memory");
+    TokenIndex ix;
+    int rc = enqueue_kept_forward(ctx, tokens, targets, batch, seq, softcap, ix);
+    hipStream_t st = ctx->stream;
+    if (rc == RH_OK && mean_loss_out &&
+        hipMemcpyAsync(mean_loss_out, ctx->mean, batch * sizeof(float), hipMemcpyDeviceToHost, st) != hipSuccess)
+        rc = fail(ctx, RH_EDEVICE, "hipMemcpyAsync of the losses failed");
+    if (hipStreamSynchronize(st) != hipSuccess && rc == RH_OK) rc = fail(ctx, RH_EDEVICE, "stream synchronize failed");
+    if (rc == RH_OK) rc = check_err_flag(ctx);
+    if (rc != RH_OK) {
+        ctx->train->fwd_id += 1;  // nothing may consume a failed forward
+        delete r;
+        return rc;
+    }
+    r->id = ctx->train->fwd_id;
+    *out = r;
+    return RH_OK;
+}
+
+int rh_backward(rh_ctx* ctx, const rh_forward_result* fwd, const uint32_t* tokens, float softcap, float loss_scale,
+                float* grad_norm_out) {
+    if (!ctx || !fwd || !tokens) return fail(ctx, RH_EINVAL, "null argument");
+    if (!(loss_scale > 0.f) || !std::isfinite(loss_scale)) return fail(ctx, RH_EINVAL, "loss_scale must be > 0");
+    TrainState* T = ctx->train;
+    if (fwd->ctx != ctx || !T || fwd->id != T->fwd_id || T->fwd_epoch != ctx->work_epoch)
+        return fail(ctx, RH_ESTATE,
+                    "the forward result is stale: another forward, prefill or validation has run on this "
+                    "context since it was made, or it belongs to another context");
+    if (softcap != T->fwd_softcap) return fail(ctx, RH_EINVAL, "softcap differs from the forward's");
+    if (!std::equal(T->fwd_tokens.begin(), T->fwd_tokens.end(), tokens))
+        return fail(ctx, RH_EINVAL, "tokens differ from the forward's input tokens");
+    HCK(hipSetDevice(ctx->device));
+    RCK(ensure_packs(ctx));  // the weights may have changed since the forward
+    RCK(enqueue_kept_backward(ctx, loss_scale));
+    HCK(hipStreamSynchronize(ctx->stream));
+    if (grad_norm_out) RCK(rh_grad_norm(ctx, grad_norm_out));
+    return RH_OK;
+}
+
+void rh_forward_result_free(rh_forward_result* fwd) { delete fwd; }
 
 int rh_read_grads_f32(rh_ctx* ctx, float* dembed, float* dgamma_final, float* const* layer_grads) {
     if (!ctx) return RH_EINVAL;

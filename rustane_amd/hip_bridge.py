@@ -113,6 +113,12 @@ def lib():
     L.rh_init_weights_normal.argtypes = [ctxp, ctypes.c_uint64, ctypes.c_float]
     L.rh_forward.argtypes = [ctxp, _u32p, _u32p, ctypes.c_int, ctypes.c_int, _f32p, _f32p, _f32p]
     L.rh_forward_backward.argtypes = [ctxp, _u32p, _u32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, _f32p]
+    L.rh_forward_train.argtypes = [ctxp, _u32p, _u32p, ctypes.c_int, ctypes.c_int, ctypes.c_float, _f32p,
+                                   ctypes.POINTER(ctypes.c_void_p)]
+    L.rh_backward.argtypes = [ctxp, ctypes.c_void_p, _u32p, ctypes.c_float, ctypes.c_float, _f32p]
+    L.rh_forward_result_free.argtypes = [ctypes.c_void_p]
+    L.rh_forward_result_free.restype = None
+    L.rh_set_fp32_masters.argtypes = [ctxp, ctypes.c_int]
     L.rh_zero_grads.argtypes = [ctxp]
     L.rh_train_config_default.argtypes = [ctypes.POINTER(RhTrainConfig)]
     L.rh_train_config_default.restype = None
@@ -187,6 +193,26 @@ class ForwardOut:
     mean_loss: np.ndarray | None     # [B]
 
 
+class ForwardResult:
+    """ForwardResult (full_model.rs:120-129): a handle to a training forward's
+    caches, which stay on the device; rh_forward_result_free on release."""
+
+    def __init__(self, h: ctypes.c_void_p, tokens: np.ndarray):
+        self.h = h
+        self.tokens = tokens
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().rh_forward_result_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Context:
     """One rh_ctx: a device, a stream, fp16 weights, KV cache and workspaces."""
 
@@ -230,6 +256,10 @@ class Context:
         ptrs = (_f32p * len(flat))(*[_f(t) for t in flat])
         self._ck(lib().rh_load_weights_f32(self.h, _f(keep[0]), _f(keep[1]), ptrs), "rh_load_weights_f32")
 
+    def set_fp32_masters(self, keep: bool = True):
+        """Keep (or drop) fp32 master weights on the device (rh_set_fp32_masters)."""
+        self._ck(lib().rh_set_fp32_masters(self.h, int(keep)), "rh_set_fp32_masters")
+
     def read_weights(self):
         c = self.cfg
         D, F, V, L = c.dim, c.hidden, c.vocab, c.nlayers
@@ -255,6 +285,31 @@ class Context:
         self._ck(lib().rh_forward_backward(self.h, _u(tokens), _u(tg), B, S, float(loss_scale), _f(ml)),
                  "rh_forward_backward")
         return ml
+
+    def forward_train(self, tokens, targets, softcap: float = 0.0):
+        """full_model::forward -> ForwardResult: the training forward with its
+        caches kept on the device; returns (ForwardResult, mean losses [B])."""
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        if tokens.ndim == 1:
+            tokens = tokens[None]
+        B, S = tokens.shape
+        tg = np.ascontiguousarray(targets, np.uint32).reshape(B, S)
+        ml = np.empty((B,), np.float32)
+        h = ctypes.c_void_p()
+        self._ck(lib().rh_forward_train(self.h, _u(tokens), _u(tg), B, S, float(softcap), _f(ml), ctypes.byref(h)),
+                 "rh_forward_train")
+        return ForwardResult(h, tokens), ml
+
+    def backward(self, fwd: "ForwardResult", tokens=None, softcap: float = 0.0, loss_scale: float = 1.0,
+                 want_norm: bool = True):
+        """full_model::backward(&fwd, tokens, softcap, loss_scale, grads):
+        accumulates the gradients; returns the accumulated gradients' L2 norm
+        (None when want_norm is False)."""
+        tok = fwd.tokens if tokens is None else np.ascontiguousarray(tokens, np.uint32)
+        norm = ctypes.c_float()
+        self._ck(lib().rh_backward(self.h, fwd.h, _u(tok), float(softcap), float(loss_scale),
+                                   ctypes.byref(norm) if want_norm else None), "rh_backward")
+        return norm.value if want_norm else None
 
     def zero_grads(self):
         self._ck(lib().rh_zero_grads(self.h), "rh_zero_grads")

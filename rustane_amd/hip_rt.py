@@ -36,6 +36,12 @@ def rt():
         R.hipEventDestroy.argtypes = [vp]
         R.hipGetErrorString.argtypes = [ctypes.c_int]
         R.hipGetErrorString.restype = ctypes.c_char_p
+        R.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+        R.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+        R.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, ctypes.c_char_p, sz]
+        R.hipGraphLaunch.argtypes = [vp, vp]
+        R.hipGraphExecDestroy.argtypes = [vp]
+        R.hipGraphDestroy.argtypes = [vp]
         _rt = R
     return _rt
 
@@ -113,3 +119,48 @@ def copy_d2d(dst: "DeviceArray", src: "DeviceArray", nbytes: int):
 
 def synchronize():
     _ck(rt().hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+CAPTURE_THREAD_LOCAL = 1  # hipStreamCaptureModeThreadLocal
+
+
+class Graph:
+    """A HIP graph captured from the work `fn` enqueues on `stream` (run
+    once, under capture; nothing executes until launch)."""
+
+    def __init__(self, stream: int, fn):
+        R = rt()
+        self.exec, self.stream = None, stream
+        _ck(R.hipStreamBeginCapture(stream, CAPTURE_THREAD_LOCAL), "hipStreamBeginCapture")
+        err = None
+        try:
+            fn()
+        except Exception as e:  # end the capture before reporting
+            err = e
+        g = ctypes.c_void_p()
+        rc = R.hipStreamEndCapture(stream, ctypes.byref(g))
+        if err is not None:
+            if g.value:
+                R.hipGraphDestroy(g)
+            raise err
+        _ck(rc, "hipStreamEndCapture")
+        ex = ctypes.c_void_p()
+        rc = R.hipGraphInstantiate(ctypes.byref(ex), g, None, None, 0)
+        R.hipGraphDestroy(g)
+        _ck(rc, "hipGraphInstantiate")
+        self.exec = ex.value
+
+    def launch(self):
+        _ck(rt().hipGraphLaunch(self.exec, self.stream), "hipGraphLaunch")
+
+    def close(self):
+        if self.exec:
+            rt().hipStreamSynchronize(self.stream)
+            rt().hipGraphExecDestroy(self.exec)
+            self.exec = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

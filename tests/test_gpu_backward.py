@@ -7,7 +7,11 @@ see identical parameters).  The GPU runs the GEMMs on fp16 operands with fp32
 accumulation, so the bar is a tolerance: per gradient tensor, cosine >= 0.999
 and max |error| <= 3e-2 x max |gradient| (the reference's own backward checks
 are looser: phase4_pretraining_checks.rs compares ANE and CPU gradients by
-cosine > 0.9).  Losses agree to 1e-3 relative."""
+cosine > 0.9).  Losses agree to 1e-3 relative.
+
+The two-call form (rh_forward_train -> ForwardResult, then rh_backward, as
+full_model::forward / full_model::backward) gives the fused call's gradients
+bit for bit."""
 import numpy as np
 import pytest
 
@@ -166,3 +170,68 @@ def test_backward_model_widths_match_oracle(orc, name):
     np.testing.assert_allclose(ml, oml, rtol=LOSS_RTOL)
     worst = _check_grads(g, og)
     print(f"[result] {name}: worst max-err ratio {worst:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("softcap", [0.0, 30.0])
+def test_forward_then_backward_equals_fused_call(softcap):
+    """full_model::forward -> ForwardResult, full_model::backward(&fwd)
+    (crates/engine/tests/phase4_training.rs:61-72) against rh_forward_backward:
+    losses, gradients and, after a second backward of the same forward, the
+    accumulated gradients are bit-identical; the returned norm is
+    rh_grad_norm's."""
+    cfg = small_cfg(dim=256, hidden=512, heads=2, hd=128, nlayers=2, vocab=1000, seq=64)
+    w = random_gammas(ModelWeights.normal(cfg, seed=231, std=0.05), seed=232)
+    tok, tgt = tokens_uniform(233, cfg.vocab, 2, cfg.seq)
+    print(f"[case] forward_train + backward vs forward_backward, softcap {softcap}", flush=True)
+    with hb.Context(cfg.to_rh(softcap), 0, 2, 0) as c:
+        c.load_weights(w.embed, w.gamma_final, [lw.tensors() for lw in w.layers])
+        ml_fused = c.forward_backward(tok, tgt, 256.0)
+        g1 = c.read_grads()
+        n1 = c.grad_norm()
+        c.forward_backward(tok, tgt, 256.0)
+        g2 = c.read_grads()
+    with hb.Context(cfg.to_rh(), 0, 2, 0) as c:  # the context's own softcap stays 0
+        c.load_weights(w.embed, w.gamma_final, [lw.tensors() for lw in w.layers])
+        fwd, ml = c.forward_train(tok, tgt, softcap=softcap)
+        np.testing.assert_array_equal(ml, ml_fused)
+        n = c.backward(fwd, tok, softcap=softcap, loss_scale=256.0)
+        assert n == n1
+        for (name, a, _), (_, b, _) in zip(_pairs(c.read_grads(), _Ref(g1)), _pairs(g1, _Ref(g1))):
+            np.testing.assert_array_equal(a, b, err_msg=name)
+        c.backward(fwd, softcap=softcap, loss_scale=256.0)
+        for (name, a, _), (_, b, _) in zip(_pairs(c.read_grads(), _Ref(g2)), _pairs(g2, _Ref(g2))):
+            np.testing.assert_array_equal(a, b, err_msg=name)
+        fwd.close()
+
+
+def test_backward_refuses_stale_or_mismatched_forward():
+    cfg = small_cfg(dim=256, hidden=512, heads=2, hd=128, nlayers=1, vocab=512, seq=32)
+    w = ModelWeights.normal(cfg, seed=234, std=0.05)
+    tok, tgt = tokens_uniform(235, cfg.vocab, 1, cfg.seq)
+    print("[case] stale and mismatched forward results", flush=True)
+    with hb.Context(cfg.to_rh(), 0, 1, 64) as c:
+        c.load_weights(w.embed, w.gamma_final, [lw.tensors() for lw in w.layers])
+        fwd, _ = c.forward_train(tok, tgt)
+        other = tok.copy()
+        other[0, 3] = (other[0, 3] + 1) % cfg.vocab
+        for kw, code in [(dict(tokens=other), hb.RH_EINVAL), (dict(softcap=5.0), hb.RH_EINVAL)]:
+            with pytest.raises(hb.HipBridgeError) as e:
+                c.backward(fwd, **kw)
+            assert e.value.code == code
+        c.backward(fwd, want_norm=False)  # still valid after the refused calls
+        for run in (lambda: c.forward(tok, tgt), lambda: c.prefill(tok[:, :10]),
+                    lambda: c.forward_train(tok, tgt)[0].close()):
+            fwd.close()
+            fwd, _ = c.forward_train(tok, tgt)
+            run()
+            with pytest.raises(hb.HipBridgeError) as e:
+                c.backward(fwd)
+            assert e.value.code == hb.RH_ESTATE
+        fwd.close()
+
+
+class _Ref:
+    """Adapts a read_grads() triple to _pairs' second argument."""
+
+    def __init__(self, g):
+        self.embed, self.gamma_final, self.layers = g

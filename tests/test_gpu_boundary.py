@@ -68,6 +68,7 @@ def test_fp32_load_and_trained_checkpoint_round_trip_exactly(tmp_path):
     p = str(tmp_path / "trained.bin")
     print("[case] fp32 masters: load, train two steps, save, reload", flush=True)
     with hb.Context(cfg.to_rh(), 0, 2, 0) as c:
+        c.set_fp32_masters(True)
         _load(c, w)
         e, gf, layers = c.read_weights()
         np.testing.assert_array_equal(e, w.embed)
@@ -81,6 +82,7 @@ def test_fp32_load_and_trained_checkpoint_round_trip_exactly(tmp_path):
         trained = c.read_weights()
         c.save_checkpoint(p, 2)
     with hb.Context(cfg.to_rh(), 0, 2, 0) as c2:
+        c2.set_fp32_masters(True)
         assert c2.load_checkpoint(p) == 2
         back = c2.read_weights()
     for x, y in zip([trained[0], trained[1]] + [t for lw in trained[2] for t in lw],
@@ -99,6 +101,7 @@ def test_update_after_fp32_load_starts_from_exact_masters(orc):
     tc = hb.train_config()
     otc = orc.TrainConfig()
     with hb.Context(cfg.to_rh(), 0, 1, 0) as c:
+        c.set_fp32_masters(True)
         _load(c, w)
         c.forward_backward(tok, tgt, loss_scale=256.0)
         ge, gg, gl = c.read_grads()
@@ -113,6 +116,40 @@ def test_update_after_fp32_load_starts_from_exact_masters(orc):
     for got, want in zip([e1, g1] + [t for lw in l1 for t in lw],
                          [ow.embed, ow.gamma_final] + [t for lw in ow.layers for t in lw]):
         np.testing.assert_array_equal(got, want)
+
+
+def test_fp32_masters_are_opt_in():
+    """Without rh_set_fp32_masters an fp32 load keeps only the fp16 device
+    weights (read back widened); with it the load is exact; dropping them
+    returns to fp16 reads; once an optimizer state exists they cannot be
+    dropped."""
+    cfg = small_cfg(dim=256, hidden=512, heads=2, hd=128, nlayers=1, vocab=512, seq=32)
+    w = ModelWeights.normal(cfg, seed=211, std=0.05, fp16_round=False)
+    r16 = lambda a: a.astype(np.float16).astype(np.float32)
+    tok, tgt = tokens_uniform(212, cfg.vocab, 1, cfg.seq)
+    print("[case] fp32 masters opt-in", flush=True)
+    with hb.Context(cfg.to_rh(), 0, 1, 0) as c:
+        _load(c, w)
+        e, _, layers = c.read_weights()
+        np.testing.assert_array_equal(e, r16(w.embed))
+        np.testing.assert_array_equal(layers[0][6], r16(w.layers[0].w2))
+        c.set_fp32_masters(True)
+        e, _, _ = c.read_weights()  # the masters start as the fp16 weights widened
+        np.testing.assert_array_equal(e, r16(w.embed))
+        _load(c, w)
+        e, _, layers = c.read_weights()
+        np.testing.assert_array_equal(e, w.embed)
+        np.testing.assert_array_equal(layers[0][4], w.layers[0].w1)
+        c.set_fp32_masters(False)
+        e, _, _ = c.read_weights()
+        np.testing.assert_array_equal(e, r16(w.embed))
+        c.set_fp32_masters(True)
+        _load(c, w)
+        c.forward_backward(tok, tgt, loss_scale=256.0)
+        c.update_weights(1, 1e-3, hb.train_config(), 1.0 / 256)
+        with pytest.raises(hb.HipBridgeError) as ex:
+            c.set_fp32_masters(False)
+        assert ex.value.code == hb.RH_ESTATE
 
 
 def test_decode_graph_survives_rope_regrowth(orc):

@@ -88,8 +88,8 @@ def _check_fp16_bar(tag, got, lg32, lg16):
     g_rms, f_rms = _rms(dev), _rms(ref)
     g_max, f_max = float(np.abs(dev).max()), float(np.abs(ref).max())
     print(f"[result] {tag}: vs fp32 oracle rms {g_rms:.3e} max {g_max:.3e}; fp16-operand oracle vs fp32 "
-          f"rms {f_rms:.3e} max {f_max:.3e}; GPU vs fp16-operand oracle max {np.abs(got - lg16).max():.3e}",
-          flush=True)
+          f"rms {f_rms:.3e} max {f_max:.3e}; GPU vs fp16-operand oracle rms {_rms(got - lg16):.3e} "
+          f"max {np.abs(got - lg16).max():.3e}", flush=True)
     assert g_rms <= FP16_FACTOR * f_rms
     assert g_max <= FP16_FACTOR * f_max
 
