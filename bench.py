@@ -76,7 +76,8 @@ def main():
                     help="decode with eager launches instead of graph replay (profilers that "
                          "cannot follow graph capture)")
     ap.add_argument("--vendor-gemm", action="store_true",
-                    help="only time hipBLASLt (torch.mm) at the 7B batch-1 prefill GEMM shapes, for reference")
+                    help="only time hipBLASLt (torch.mm) at the 7B prefill GEMM shapes of batch 1, 4 and 16, "
+                         "for reference")
     ap.add_argument("--no-graphs", action="store_true",
                     help="eager launches everywhere, prefill included (profilers that cannot follow "
                          "graph capture)")
@@ -188,11 +189,18 @@ def main():
         e_ms, _, ek_ms, ek_n, _, _ = run_prefill(eb, max(3, args.steps // max(1, eb // 2)), 1)
         esteps = max(3, args.steps // max(1, eb // 2))
         efl = E.prefill_flops(cfg, cfg.seq, eb)
+        ew13_us = (ek_ms / ek_n) * 1e3 if ek_n else None
+        ew13_tf = efl["w13_per_launch"] / (ew13_us * 1e-6) / 1e12 if ew13_us else None
         extra_lines[f"B{eb}"] = {
             "tok_s": eb * cfg.seq * esteps / (e_ms / 1e3),
             "ms_per_step": e_ms / esteps,
             "forward_mfma_frac": efl["total"] / (e_ms / esteps / 1e3) / 1e12 / PEAK_FP16_TFLOPS,
-            "w13_gemm_us": (ek_ms / ek_n) * 1e3 if ek_n else None,
+            "w13_gemm_us": ew13_us,
+            "roofline": None if ew13_tf is None else {
+                "bound": "mfma", "kernel": "gemm_kernel<..., EPI_SWIGLU> (W1|W3 GEMM + SwiGLU)",
+                "achieved": round(ew13_tf, 1), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(ew13_tf / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                "flops_per_launch": efl["w13_per_launch"], "mean_launch_us": round(ew13_us, 2)},
         }
         log(f"[bench] prefill B={eb}: {extra_lines[f'B{eb}']}")
 
@@ -651,37 +659,39 @@ def cpu_baseline_decode(cfg, args, steps=4):
                       f"({t_step * 1e3:.0f} ms per token)"}
 
 
-def run_vendor_gemm(iters=30):
-    """hipBLASLt through torch.mm at the 7B batch-1 prefill GEMM shapes (M = 512
-    tokens, fp16 operands, fp16 output, weights [N, K] as the library stores
-    them), each weight rotated over more than 1 GiB of copies so every launch
-    reads it from HBM past the 256 MB last-level cache, as the forward does.
-    A reference point for the library's GEMMs, which also fuse their
-    epilogues (RoPE and the cache scatter, SwiGLU, residual + RMSNorm)."""
+def run_vendor_gemm(iters=30, rows=(512, 2048, 8192)):
+    """hipBLASLt through torch.mm at the 7B prefill GEMM shapes for batch 1,
+    4 and 16 of 512 tokens (M = 512, 2048, 8192; fp16 operands, fp16 output,
+    weights [N, K] as the library stores them), each weight rotated over more
+    than 1 GiB of copies so every launch reads it from HBM past the 256 MB
+    last-level cache, as the forward does.  A reference point for the
+    library's GEMMs, which also fuse their epilogues (RoPE and the cache
+    scatter, SwiGLU, residual + RMSNorm)."""
     import torch
-    shapes = {"QKV": (512, 12288, 4096), "W1|W3": (512, 22016, 4096), "W2": (512, 4096, 11008),
-              "Wo": (512, 4096, 4096), "logits": (512, 32000, 4096)}
+    shapes = {"QKV": (12288, 4096), "W1|W3": (22016, 4096), "W2": (4096, 11008), "Wo": (4096, 4096),
+              "logits": (32000, 4096)}
     out = {}
-    for name, (M, N, K) in shapes.items():
-        g = torch.Generator(device="cuda").manual_seed(5)
-        a = torch.randn(M, K, device="cuda", dtype=torch.float16, generator=g)
-        nrot = (1 << 30) // (N * K * 2) + 2
-        ws = [torch.randn(N, K, device="cuda", dtype=torch.float16, generator=g) for _ in range(nrot)]
-        for w in ws[:2]:
-            torch.mm(a, w.t())
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(iters):
-            torch.mm(a, ws[i % nrot].t())
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / iters
-        tf = 2.0 * M * N * K / us / 1e6
-        out[name] = {"M": M, "N": N, "K": K, "us": round(us, 2), "tflops": round(tf, 1),
-                     "mfma_frac": round(tf / PEAK_FP16_TFLOPS, 4)}
-        log(f"[bench] hipBLASLt {name} {M}x{N}x{K}: {us:.2f} us, {tf:.0f} TFLOP/s")
-        del ws
+    for M in rows:
+        for name, (N, K) in shapes.items():
+            g = torch.Generator(device="cuda").manual_seed(5)
+            a = torch.randn(M, K, device="cuda", dtype=torch.float16, generator=g)
+            nrot = (1 << 30) // (N * K * 2) + 2
+            ws = [torch.randn(N, K, device="cuda", dtype=torch.float16, generator=g) for _ in range(nrot)]
+            for w in ws[:2]:
+                torch.mm(a, w.t())
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(iters):
+                torch.mm(a, ws[i % nrot].t())
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / iters
+            tf = 2.0 * M * N * K / us / 1e6
+            out[f"{name} M{M}"] = {"M": M, "N": N, "K": K, "us": round(us, 2), "tflops": round(tf, 1),
+                                   "mfma_frac": round(tf / PEAK_FP16_TFLOPS, 4)}
+            log(f"[bench] hipBLASLt {name} {M}x{N}x{K}: {us:.2f} us, {tf:.0f} TFLOP/s")
+            del ws
     return out
 
 

@@ -503,7 +503,20 @@ __global__ __launch_bounds__(Tl::NT) void gemm_kernel(GemmArgs a, int P, long lo
     typename Tl::Acc acc;
     if constexpr (MODE == MODE_DP) {
         const int t = xcd_remap(blockIdx.x, nbN * nbM);
-        const int nb = t / nbM, mb = t - nb * nbM;
+        // Consecutive tiles (run together on one XCD) walk groups of up to
+        // 8 M-tiles x every N panel, M fastest: the 32 tiles an XCD runs at
+        // a time then share 4 weight panels and 8 activation row blocks in
+        // its L2, instead of one panel and 32 row blocks (7B batch 16: QKV
+        // 785 -> 753 us, W2 870 -> 746 us, prefill 108.4 -> 101.5 ms).
+        int nb, mb;
+        if (nbM <= 8) {
+            nb = t / nbM;
+            mb = t - nb * nbM;
+        } else {
+            const int g = t / (8 * nbN), r = t - g * 8 * nbN, gm = min(8, nbM - g * 8);
+            mb = g * 8 + r % gm;
+            nb = r / gm;
+        }
         if constexpr (EPI == EPI_SILU_BWD && Tl::kM16 && Tl::NA * Tl::NB <= 12) {
             // The saved h1, h3 of this lane's outputs are loaded before the k
             // loop, so they arrive under it instead of stalling the epilogue

@@ -225,13 +225,16 @@ def test_qkv_rope_scatter(lib, name):
 
 
 @pytest.mark.parametrize("out_of_place", [False, True])
-@pytest.mark.parametrize("cfg,K", [(0, 1024), (0, 8192), (16, 1024), (9, 1024)])
-def test_residual_then_rmsnorm(lib, cfg, K, out_of_place):
+@pytest.mark.parametrize("cfg,K,M", [(0, 1024, 300), (0, 8192, 300), (16, 1024, 300), (9, 1024, 300),
+                                     (16, 1024, 2100)])
+def test_residual_then_rmsnorm(lib, cfg, K, M, out_of_place):
     """cfg 0 at these shapes takes split-K (K 1024: 128x128 tiles, K 8192:
     256x128) with the summing row kernel; 16 / 9 are one block per tile and
-    stream-K followed by the plain RMSNorm kernel.  Out of place the residual
-    is read from its own buffer and the output buffer starts as garbage."""
-    M, N, eps, alpha = 300, 1024, 1e-5, 0.25
+    stream-K followed by the plain RMSNorm kernel (one row per block; from
+    2048 rows on, 8 rows per block -- M 2100 ends in a partial block).  Out
+    of place the residual is read from its own buffer and the output buffer
+    starts as garbage."""
+    N, eps, alpha = 1024, 1e-5, 0.25
     x, w, y = operands(7, M, N, K)
     rng = np.random.default_rng(8)
     x0 = rng.standard_normal((M, N)).astype(np.float32)
