@@ -24,7 +24,12 @@
 // 1/rms -- the RMSNorm (rmsnorm::forward_channel_first, cpu/rmsnorm.rs:149-183)
 // with no launch of its own (rs_part / ssq_out): rmsnorm(x) * gamma . W =
 // (1/rms) * ((x * gamma) . W), rounded to fp16 before instead of after the
-// 1/rms factor.
+// 1/rms factor.  The fp16 input is x * gamma * XG_SCALE (a power of two, so
+// the scaling is exact) and the consumer multiplies by 1/(rms * XG_SCALE):
+// the unnormalised residual then stays finite up to |x * gamma| = 2^20
+// instead of fp16's 65504, while values down to 2^-10 keep full fp16
+// precision (smaller ones, subnormal after the scale, are off by at most
+// 2^-21 in absolute terms).
 //
 // NORM: the input is the fp32 residual stream and the block applies the
 // RMSNorm itself (rmsnorm::forward_channel_first, cpu/rmsnorm.rs:149-183)
@@ -36,6 +41,8 @@
 
 namespace rh {
 namespace {
+
+constexpr float XG_SCALE = 1.0f / 16.0f;
 
 template <int EPI, int RT, int NW, int DEPTH, bool NORM>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
@@ -191,7 +198,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
             float ss = 0.f;  // token r's slices, in order
 #pragma unroll
             for (int q = 0; q < 16; ++q) ss += s_sq[q][r];
-            const float rs = 1.0f / sqrtf(ss * (1.0f / (float)K) + a.eps);
+            const float rs = 1.0f / sqrtf(ss * (1.0f / (float)K) + a.eps) * (1.0f / XG_SCALE);
 #pragma unroll
             for (int t = 0; t < RT; ++t) acc[t] *= rs;
         }
@@ -252,7 +259,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
                 if (live) {
                     const f32x4 gm = *(const f32x4*)(a.gnext + n);
                     *(f16x4*)(a.xg_out + (size_t)tok * N + n) =
-                        f16x4{(f16)(x[0] * gm[0]), (f16)(x[1] * gm[1]), (f16)(x[2] * gm[2]), (f16)(x[3] * gm[3])};
+                        f16x4{(f16)(x[0] * gm[0] * XG_SCALE), (f16)(x[1] * gm[1] * XG_SCALE),
+                              (f16)(x[2] * gm[2] * XG_SCALE), (f16)(x[3] * gm[3] * XG_SCALE)};
                 }
                 float ss = (x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]);
                 ss += __shfl_xor(ss, 16, RH_WAVE);  // the token's 4 lane groups, in a fixed order

@@ -141,6 +141,40 @@ def test_decode_nonunit_gammas(orc, dim, batch):
             assert err <= LOGIT_ATOL, (p, err)
 
 
+def test_decode_large_residual_matches_forward(orc):
+    """Residual entries up to 3e4 (an embedding U(-3e4, 3e4), fp16-exact)
+    times gammas up to 6 (|x * gamma| past fp16's 65504) at 16 sequences of
+    dim 2048, where the residual GEMVs hand the next GEMV fp16(x * gamma)
+    scaled by a power of two and the sums of squares: decode logits equal the
+    forward's at every position (relative to the logits' scale, which the
+    tied embedding sets near 1e6)."""
+    cfg = small_cfg(dim=2048, hidden=1024, heads=16, hd=128, nlayers=2, vocab=1024, seq=40)
+    w = ModelWeights.normal(cfg, seed=56)
+    rng = np.random.default_rng(57)
+    w.embed = rng.uniform(-3e4, 3e4, w.embed.shape).astype(np.float16).astype(np.float32)
+    D = cfg.dim
+    for lw in w.layers:
+        lw.gamma1 = rng.uniform(2.0, 6.0, D).astype(np.float32)
+        lw.gamma2 = rng.uniform(2.0, 6.0, D).astype(np.float32)
+    w.gamma_final = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    batch = 16
+    tok, tgt = tokens_uniform(58, cfg.vocab, batch, cfg.seq)
+    print("[case] decode with |x * gamma| beyond fp16, dim 2048, batch 16", flush=True)
+    with _ctx(cfg, w, batch, 64) as c:
+        out = c.forward(tok, tgt)
+        lg = out.logits
+        scale = float(np.abs(lg).max())
+        assert np.isfinite(lg).all() and scale > 1e5
+        nxt, last = c.prefill(tok[:, :32], want_logits=True)
+        assert np.abs(last - lg[:, 31]).max() <= 2e-3 * scale
+        for p in range(32, 40):
+            nxt, dl = c.decode_step(tok[:, p], want_logits=True)
+            assert np.isfinite(dl).all(), p
+            err = float(np.abs(dl - lg[:, p]).max()) / scale
+            print(f"[result] position {p}: max|dlogit| / max|logit| {err:.2e}", flush=True)
+            assert err <= 2e-3, (p, err)
+
+
 def test_decode_tiny_config_hd64(orc):
     from rustane_amd.engine import tiny_config
     cfg = tiny_config()

@@ -23,7 +23,7 @@ more -- plus cosine >= 0.9999 and the mean loss within 1e-4 relative
 Absolute bound against the fp16-operand oracle.  No single rounding point
 sets the full-depth drift: at 7B, 32 layers, rounding one point alone moves
 the logits by RMS 3.6e-3 (the QKV operand), 2.4e-3 (k; the W1|W3 operand),
-2.3e-3 (q), 1.7e-3 (v, attention output, gate), 1.1e-3 (P) and ~1e-4 (the
+2.3e-3 (q), 1.7e-3 (v, attention output, gate), 1.1e-3 (P) and 2.7e-4 (the
 logits operand), adding in quadrature to the 6.3e-3 of all nine together
 (tests/fp16_drift_by_point.py).  The GPU and the fp16-operand oracle round
 the same operands of values that differ in fp32 summation order, so at
