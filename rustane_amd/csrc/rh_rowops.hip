@@ -115,46 +115,62 @@ __global__ __launch_bounds__(256) void rmsnorm_frag_kernel(const float* x, const
 // RMSNorm into fragment order for many rows: 8 rows per block (8 waves,
 // wave w owns row r0 + w) so the block writes whole 128-byte lines of every
 // fragment (8 rows x 16 bytes per k group) instead of one row's scattered
-// 16-byte lane slots.  Pass 1: each wave sums its row's squares (lane l owns
-// columns 8l + 512p).  Pass 2: the block's half of the 16-row fragment
-// block -- lane l of a wave covers fragment 2i + l/32, k group (l/8) % 4, row
-// l % 8 -- re-reading x from the cache.  (One row per block: 83.6 us for
-// 8192 x 4096 at 7B batch 16, about 2.4 TB/s.)
+// 16-byte lane slots.  Pass 1: each wave loads its row once into registers
+// (lane l owns columns 8l + 512p, every load issued before the first add),
+// sums the squares, and writes the normalised fp16 row into LDS.  Pass 2:
+// the block's half of the 16-row fragment block -- lane l of a wave covers
+// fragment 2i + l/32, k group (l/8) % 4, row l % 8 -- from LDS.  (One row
+// per block: 83.6 us for 8192 x 4096 at 7B batch 16, about 2.4 TB/s; reading
+// the row twice from memory: 50 us.)
 __global__ __launch_bounds__(512) void rmsnorm_frag8_kernel(const float* x, const float* gamma, f16* out, int M,
                                                             int D, float eps) {
-    __shared__ float rinv[8];
+    extern __shared__ __attribute__((aligned(16))) f16 srow[];  // [8][D]
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r0 = blockIdx.x * 8, row = r0 + w;
     if (row < M) {
         const float* xr = x + (size_t)row * D;
-        float ss = 0.f;
-#pragma unroll 4
-        for (int i = 8 * lane; i < D; i += 512) {
-            const f32x4 v0 = *(const f32x4*)(xr + i), v1 = *(const f32x4*)(xr + i + 4);
+        f32x4 v[16][2];  // D <= 8192: 16 passes of 512 columns
 #pragma unroll
-            for (int e = 0; e < 4; ++e) ss += v0[e] * v0[e] + v1[e] * v1[e];
+        for (int p = 0; p < 16; ++p) {
+            const int i = 8 * lane + 512 * p;
+            if (i < D) {
+                v[p][0] = *(const f32x4*)(xr + i);
+                v[p][1] = *(const f32x4*)(xr + i + 4);
+            }
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int p = 0; p < 16; ++p) {
+            if (8 * lane + 512 * p < D) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ss += v[p][0][e] * v[p][0][e] + v[p][1][e] * v[p][1][e];
+            }
         }
         ss = wave_sum(ss);
-        if (lane == 0) rinv[w] = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
+        const float rs = 1.0f / sqrtf(ss * (1.0f / (float)D) + eps);
+#pragma unroll
+        for (int p = 0; p < 16; ++p) {
+            const int i = 8 * lane + 512 * p;
+            if (i < D) {
+                const f32x4 g0 = *(const f32x4*)(gamma + i), g1 = *(const f32x4*)(gamma + i + 4);
+                f16x8 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    o[e] = (f16)(v[p][0][e] * rs * g0[e]);
+                    o[e + 4] = (f16)(v[p][1][e] * rs * g1[e]);
+                }
+                *(f16x8*)&srow[(size_t)w * D + i] = o;
+            }
+        }
     }
     __syncthreads();
     const int r = lane & 7, kq = (lane >> 3) & 3, half = lane >> 5;
     const int m = r0 + r;
     if (m >= M) return;
-    const float rs = rinv[r];
-    const float* xr = x + (size_t)m * D;
     const int nf = D / 32;
     for (int j = 2 * w + half; j < nf; j += 16) {
         const int k = 32 * j + 8 * kq;
-        const f32x4 v0 = *(const f32x4*)(xr + k), v1 = *(const f32x4*)(xr + k + 4);
-        const f32x4 g0 = *(const f32x4*)(gamma + k), g1 = *(const f32x4*)(gamma + k + 4);
-        f16x8 o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            o[e] = (f16)(v0[e] * rs * g0[e]);
-            o[e + 4] = (f16)(v1[e] * rs * g1[e]);
-        }
-        *(f16x8*)(out + frag_off(m, k, D)) = o;
+        *(f16x8*)(out + frag_off(m, k, D)) = *(const f16x8*)&srow[(size_t)r * D + k];
     }
 }
 
@@ -399,8 +415,8 @@ hipError_t launch_rmsnorm(const float* x, const float* gamma, f16* out, int rows
     if (frag) {
         if (D % 128 != 0 || D > 8192) return hipErrorInvalidValue;  // whole fragments; 4 passes of 8 columns
         if (rows >= 2048) {  // enough 8-row blocks to fill the chip
-            hipLaunchKernelGGL(rmsnorm_frag8_kernel, dim3((rows + 7) / 8), dim3(512), 0, st, x, gamma, out, rows,
-                               D, eps);
+            hipLaunchKernelGGL(rmsnorm_frag8_kernel, dim3((rows + 7) / 8), dim3(512), (size_t)8 * D * sizeof(f16),
+                               st, x, gamma, out, rows, D, eps);
             return hipGetLastError();
         }
         hipLaunchKernelGGL(rmsnorm_frag_kernel, dim3(rows), dim3(256), 0, st, x, gamma, out, D, eps);
