@@ -199,8 +199,9 @@ def main():
             "roofline": None if ew13_tf is None else {
                 "bound": "mfma", "kernel": "gemm_kernel<..., EPI_SWIGLU> (W1|W3 GEMM + SwiGLU)",
                 "achieved": round(ew13_tf, 1), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ew13_tf / PEAK_FP16_TFLOPS, 4), "traffic": None,
-                "flops_per_launch": efl["w13_per_launch"], "mean_launch_us": round(ew13_us, 2)},
+                "frac": round(ew13_tf / PEAK_FP16_TFLOPS, 4), "traffic": measured_traffic(args.config, eb, cfg.seq),
+                "flops_per_launch": efl["w13_per_launch"], "mean_launch_us": round(ew13_us, 2),
+                "traffic_source": "rocprofv3 FETCH_SIZE/WRITE_SIZE passes recorded in profiles/"},
         }
         log(f"[bench] prefill B={eb}: {extra_lines[f'B{eb}']}")
 
