@@ -182,8 +182,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
             return mx;
         };
         float mloc = (k0 + KB > q0 || k0 + KB > S) ? block_max(std::true_type{}) : block_max(std::false_type{});
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, RH_WAVE));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, RH_WAVE));
+        mloc = xrow_max4(mloc);
         mloc *= scale_log2;
         if (__any(mloc > m_run + 8.0f)) {
             const float m_new = fmaxf(m_run, mloc);
@@ -213,8 +212,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const f16* __restrict
             for (int j = 0; j < NHT; ++j) o[j] = mfma16(vf[c][j], pf[c], o[j]);
     }
     }
-    float lt = l_run + __shfl_xor(l_run, 16, RH_WAVE);
-    lt += __shfl_xor(lt, 32, RH_WAVE);
+    const float lt = xrow_sum4(l_run);
     if (qi < S) {
         // Log-sum-exp of the scaled scores in the log2 domain, for the
         // backward pass: P[q][k] = exp2(score * scale_log2 - lse[q]).
@@ -408,8 +406,7 @@ __global__ __launch_bounds__(256 * NG) void attn_prefill_dma_kernel(const f16* _
             return mx;
         };
         float mloc = (k0 + KB > q0 || k0 + KB > S) ? block_max(std::true_type{}) : block_max(std::false_type{});
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, RH_WAVE));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, RH_WAVE));
+        mloc = xrow_max4(mloc);
         mloc *= scale_log2;
         if (__any(mloc > m_run + 8.0f)) {
             const float m_new = fmaxf(m_run, mloc);
@@ -476,8 +473,7 @@ __global__ __launch_bounds__(256 * NG) void attn_prefill_dma_kernel(const f16* _
             for (int e = 0; e < 4; ++e) o[j][e] = o[j][e] * c0 + xo[(w * 32 + 4 * j + e) * 64 + lane] * c1;
         m_run = mm;
     }
-    float lt = l_run + __shfl_xor(l_run, 16, RH_WAVE);
-    lt += __shfl_xor(lt, 32, RH_WAVE);
+    const float lt = xrow_sum4(l_run);
     if (qi < S) {
         if (lse && g == 0) lse[bh * S + qi] = m_run + log2f(lt);
         const float inv = 1.0f / lt;

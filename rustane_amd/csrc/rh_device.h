@@ -23,6 +23,39 @@ __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// Max / sum over the four lanes l, l ^ 16, l ^ 32, l ^ 48 of a wave (the
+// lanes sharing l % 16), on gfx950's row-swap VALU ops instead of LDS-crossbar
+// shuffles.  With a = b = v, v_permlane16_swap a, b leaves lane l holding
+// (v[l & ~16], v[l | 16]) and v_permlane32_swap a, b (v[l & 31], v[(l & 31) +
+// 32]) (checked on the device), so both lanes of a pair combine the same
+// operands in the same order and all four lanes end with the same bits; the
+// sum equals v + shfl_xor(v, 16), then + shfl_xor(., 32), bit for bit.  The
+// swaps are written as inline assembly: the compiler's builtins for them fold
+// a swap of two equal values to those values, which drops the data movement
+// between rows.  The s_nop covers the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ void swap_rows16(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void swap_halves32(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float xrow_max4(float v) {
+    float a = v, b = v;
+    swap_rows16(a, b);
+    a = fmaxf(a, b);
+    b = a;
+    swap_halves32(a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float xrow_sum4(float v) {
+    float a = v, b = v;
+    swap_rows16(a, b);
+    a = a + b;
+    b = a;
+    swap_halves32(a, b);
+    return a + b;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, RH_WAVE);

@@ -262,9 +262,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
                         f16x4{(f16)(x[0] * gm[0] * XG_SCALE), (f16)(x[1] * gm[1] * XG_SCALE),
                               (f16)(x[2] * gm[2] * XG_SCALE), (f16)(x[3] * gm[3] * XG_SCALE)};
                 }
-                float ss = (x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]);
-                ss += __shfl_xor(ss, 16, RH_WAVE);  // the token's 4 lane groups, in a fixed order
-                ss += __shfl_xor(ss, 32, RH_WAVE);
+                // the token's 4 lane groups, in a fixed order
+                const float ss = xrow_sum4((x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]));
                 if (g == 0) a.ssq_out[(size_t)blockIdx.x * 16 + r] = ss;
             }
         } else {  // GV_QKV
