@@ -600,16 +600,35 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict_
             step(it + 1, kb, vb);
         }
     }
-    // merge the SL slots of the wave (lanes with equal j)
+    // merge the SL slots of the wave (lanes with equal j): each step combines
+    // lane pairs (l, l ^ off) as (lower lane, upper lane), so both lanes of a
+    // pair compute the same expression; off 16 and 32 move their operands with
+    // the row-swap VALU ops, smaller offsets with shuffles
 #pragma unroll
     for (int off = LPP; off < 64; off <<= 1) {
-        const float om = __shfl_xor(m, off, RH_WAVE), ol = __shfl_xor(l, off, RH_WAVE);
-        const float nm = fmaxf(m, om);
-        const float ca = m == -INFINITY ? 0.f : __expf(m - nm);
-        const float cb = om == -INFINITY ? 0.f : __expf(om - nm);
-        l = l * ca + ol * cb;
+        float mp[2], lp[2], op[8][2];
+        auto pair = [&](float v, float (&pr)[2]) {
+            if (off == 16 || off == 32) {
+                pr[0] = v; pr[1] = v;
+                if (off == 16) swap_rows16(pr[0], pr[1]);
+                else swap_halves32(pr[0], pr[1]);
+            } else {
+                const float x = __shfl_xor(v, off, RH_WAVE);
+                const bool lo = (lane & off) == 0;
+                pr[0] = lo ? v : x;
+                pr[1] = lo ? x : v;
+            }
+        };
+        pair(m, mp);
+        pair(l, lp);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = o[e] * ca + __shfl_xor(o[e], off, RH_WAVE) * cb;
+        for (int e = 0; e < 8; ++e) pair(o[e], op[e]);
+        const float nm = fmaxf(mp[0], mp[1]);
+        const float ca = mp[0] == -INFINITY ? 0.f : __expf(mp[0] - nm);
+        const float cb = mp[1] == -INFINITY ? 0.f : __expf(mp[1] - nm);
+        l = lp[0] * ca + lp[1] * cb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = op[e][0] * ca + op[e][1] * cb;
         m = nm;
     }
     if (slot == 0) {
