@@ -262,24 +262,23 @@ __global__ __launch_bounds__(256 * NG) void attn_prefill_dma_kernel(const f16* _
     constexpr int TILE = KB * HD;  // halves of one K or V block (16 KB)
     static_assert(NS == 2 || NS == 3, "2 or 3 stages");
     static_assert(NG == 1 || (NG == 2 && NS == 2), "two groups run the 2-stage pipeline");
-    // one LDS array per stage and operand: the compiler's wait-count pass then
-    // knows a stage's reads do not alias the DMA filling another stage (one
-    // array would make it drain every DMA before the first read)
-    __shared__ __attribute__((aligned(1024))) f16 sK0[NG * TILE], sV0[NG * TILE], sK1[NG * TILE], sV1[NG * TILE],
-        sK2[TILE], sV2[TILE];
-    auto kbuf = [&](auto I) -> f16* {
-        if constexpr (decltype(I)::value == 0) return sK0;
-        else if constexpr (decltype(I)::value == 1) return sK1;
-        else return sK2;
-    };
-    auto vbuf = [&](auto I) -> f16* {
-        if constexpr (decltype(I)::value == 0) return sV0;
-        else if constexpr (decltype(I)::value == 1) return sV1;
-        else return sV2;
-    };
+    // One LDS array per stage, operand and group, each addressed from its
+    // start: the compiler's wait-count pass then knows a stage's reads do not
+    // alias the DMA filling another stage.  (With one array it drains every
+    // DMA before the first read; with a group's stages at an offset inside a
+    // shared array it drains the DMA just issued for the next key block
+    // before each transposing V read.)
+    __shared__ __attribute__((aligned(1024))) f16 sK0[TILE], sV0[TILE], sK1[TILE], sV1[TILE], sK2[TILE], sV2[TILE];
+    f16 *gK0 = sK0, *gV0 = sV0, *gK1 = sK1, *gV1 = sV1;  // group 1's stages (NG == 2)
+    if constexpr (NG == 2) {
+        __shared__ __attribute__((aligned(1024))) f16 tK0[TILE], tV0[TILE], tK1[TILE], tV1[TILE];
+        gK0 = tK0; gV0 = tV0; gK1 = tK1; gV1 = tV1;
+    }
 
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r = lane & 15;
-    const int w = (tid >> 6) & 3, grp = NG == 1 ? 0 : tid >> 8;  // wave within its group, group
+    // wave within its group, group (scalar, so the group's branches are uniform)
+    const int w = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);
+    const int grp = NG == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid >> 8);
     const int nqt = (S + 63) / 64;
     // 1-D grid: the query tiles of one (sequence, head) are consecutive
     // logical tiles, which xcd_remap puts on one XCD, so that XCD's L2 serves
@@ -308,155 +307,179 @@ __global__ __launch_bounds__(256 * NG) void attn_prefill_dma_kernel(const f16* _
 
     const int kend = min(S, q0 + 64);
     const int nkb = (kend + KB - 1) / KB;
-    // Wave w moves 1 KB units w, w + 4, w + 8, w + 12 of the K block and of the
-    // V block (8 DMA instructions per stage); unit i holds rows 4i..4i+3, lane L
-    // row 4i + L/16 and stored chunk L%16.  Keys past the sequence read the
-    // last row (masked below).
-    auto issue = [&](int kb, auto ST) {
-        const int k0 = kb * KB;
-        f16* dk = kbuf(ST) + grp * TILE;
-        f16* dv = vbuf(ST) + grp * TILE;
+    // The group's k loop, instantiated per group so that every stage buffer
+    // it names is a compile-time choice of array.
+    auto group_loop = [&](auto G) {
+        constexpr int GI = decltype(G)::value;
+        auto kbuf = [&](auto I) -> f16* {
+            if constexpr (decltype(I)::value == 0) return GI ? gK0 : sK0;
+            else if constexpr (decltype(I)::value == 1) return GI ? gK1 : sK1;
+            else return sK2;
+        };
+        auto vbuf = [&](auto I) -> f16* {
+            if constexpr (decltype(I)::value == 0) return GI ? gV0 : sV0;
+            else if constexpr (decltype(I)::value == 1) return GI ? gV1 : sV1;
+            else return sV2;
+        };
+        // Wave w moves 1 KB units w, w + 4, w + 8, w + 12 of the K block and of the
+        // V block (8 DMA instructions per stage); unit i holds rows 4i..4i+3, lane L
+        // row 4i + L/16 and stored chunk L%16.  Keys past the sequence read the
+        // last row (masked below).
+        auto issue = [&](int kb, auto ST) {
+            const int k0 = kb * KB;
+            f16* dk = kbuf(ST);
+            f16* dv = vbuf(ST);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int i = w + 4 * t, row = 4 * i + (lane >> 4);
-            const size_t key = (size_t)min(k0 + row, S - 1);
-            __builtin_amdgcn_global_load_lds((const void*)(Kb + key * HD + 8 * ((lane & 15) ^ swz_k(row))),
-                                             (__attribute__((address_space(3))) void*)(dk + i * 512), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((const void*)(Vb + key * HD + 8 * ((lane & 15) ^ swz_v(row))),
-                                             (__attribute__((address_space(3))) void*)(dv + i * 512), 16, 0, 0);
-        }
-    };
-    if (grp < nkb) issue(grp, std::integral_constant<int, 0>{});  // nkb >= 1
-    if constexpr (NS == 3)
-        if (nkb > 1) issue(1, std::integral_constant<int, 1>{});
-
-    // one key block on stage ST (a compile-time buffer choice); with two
-    // groups, kb is this group's block (kb >= nkb: a barrier-only step)
-    auto step = [&](int kb, auto ST) {
-        constexpr int cur = decltype(ST)::value;
-        const int k0 = kb * KB;
-        // this wave's 8 DMAs of stage kb have landed when at most 8 per stage
-        // issued after it are outstanding; the barrier publishes every wave's
-        // and retires every wave's reads of stage kb - 1, whose buffer the
-        // next issue refills
-        const int ahead = min(NS - 2, nkb - 1 - kb);
-        if (ahead >= 2) wait_vm<16>();
-        else if (ahead == 1) wait_vm<8>();
-        else wait_vm<0>();
-        lds_barrier();
-        if (kb + NG * (NS - 1) < nkb) issue(kb + NG * (NS - 1), std::integral_constant<int, (cur + NS - 1) % NS>{});
-        if (NG > 1 && kb >= nkb) return;  // group-uniform
-        const f16* sK = kbuf(ST) + grp * TILE;
-        const f16* sV = vbuf(ST) + grp * TILE;
-
-        f16x8 kf[2][2][NKK];
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const int krow = 32 * c + 8 * (r >> 2) + 4 * u + (r & 3);
-#pragma unroll
-                for (int kk = 0; kk < NKK; ++kk)
-                    kf[c][u][kk] = *(const f16x8*)&sK[krow * HD + 8 * ((4 * kk + g) ^ swz_k(krow))];
+            for (int t = 0; t < 4; ++t) {
+                const int i = w + 4 * t, row = 4 * i + (lane >> 4);
+                const size_t key = (size_t)min(k0 + row, S - 1);
+                __builtin_amdgcn_global_load_lds((const void*)(Kb + key * HD + 8 * ((lane & 15) ^ swz_k(row))),
+                                                 (__attribute__((address_space(3))) void*)(dk + i * 512), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(Vb + key * HD + 8 * ((lane & 15) ^ swz_v(row))),
+                                                 (__attribute__((address_space(3))) void*)(dv + i * 512), 16, 0, 0);
             }
-        __builtin_amdgcn_sched_barrier(0);
-        f32x4 sc[2][2];
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int u = 0; u < 2; ++u) sc[c][u] = f32x4{};
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk)
+        };
+        if (GI < nkb) issue(GI, std::integral_constant<int, 0>{});  // nkb >= 1
+        if constexpr (NS == 3)
+            if (nkb > 1) issue(1, std::integral_constant<int, 1>{});
+
+        // one key block on stage ST (a compile-time buffer choice); with two
+        // groups, kb is this group's block (kb >= nkb: a barrier-only step)
+        auto step = [&](int kb, auto ST) {
+            constexpr int cur = decltype(ST)::value;
+            const int k0 = kb * KB;
+            // this wave's 8 DMAs of stage kb have landed when at most 8 per stage
+            // issued after it are outstanding; the barrier publishes every wave's
+            // and retires every wave's reads of stage kb - 1, whose buffer the
+            // next issue refills
+            const int ahead = min(NS - 2, nkb - 1 - kb);
+            if (ahead >= 2) wait_vm<16>();
+            else if (ahead == 1) wait_vm<8>();
+            else wait_vm<0>();
+            lds_barrier();
+            if (kb + NG * (NS - 1) < nkb) issue(kb + NG * (NS - 1), std::integral_constant<int, (cur + NS - 1) % NS>{});
+            if (NG > 1 && kb >= nkb) return;  // group-uniform
+            const f16* sK = kbuf(ST);
+            const f16* sV = vbuf(ST);
+
+            f16x8 kf[2][2][NKK];
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int u = 0; u < 2; ++u) sc[c][u] = mfma16(kf[c][u][kk], qf[kk], sc[c][u]);
-        __builtin_amdgcn_sched_barrier(0);
-        f16x8 vf[2][NHT];
+                for (int u = 0; u < 2; ++u) {
+                    const int krow = 32 * c + 8 * (r >> 2) + 4 * u + (r & 3);
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int j = 0; j < NHT; ++j) {
-                const int ch = 2 * j + ((lane & 3) >> 1);
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int key = 32 * c + 8 * g + 4 * hh + (r >> 2);
-                    const f16* a = &sV[key * HD + 8 * (ch ^ swz_v(key)) + 4 * (lane & 1)];
-                    const s16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) s16x4*)a);
-                    const f16x4 tv = __builtin_bit_cast(f16x4, t);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) vf[c][j][4 * hh + e] = tv[e];
+                    for (int kk = 0; kk < NKK; ++kk)
+                        kf[c][u][kk] = *(const f16x8*)&sK[krow * HD + 8 * ((4 * kk + g) ^ swz_k(krow))];
                 }
+            __builtin_amdgcn_sched_barrier(0);
+            f32x4 sc[2][2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) sc[c][u] = f32x4{};
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk)
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) sc[c][u] = mfma16(kf[c][u][kk], qf[kk], sc[c][u]);
+            __builtin_amdgcn_sched_barrier(0);
+            f16x8 vf[2][NHT];
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int j = 0; j < NHT; ++j) {
+                    const int ch = 2 * j + ((lane & 3) >> 1);
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int key = 32 * c + 8 * g + 4 * hh + (r >> 2);
+                        const f16* a = &sV[key * HD + 8 * (ch ^ swz_v(key)) + 4 * (lane & 1)];
+                        const s16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (__attribute__((address_space(3))) s16x4*)a);
+                        const f16x4 tv = __builtin_bit_cast(f16x4, t);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) vf[c][j][4 * hh + e] = tv[e];
+                    }
+                }
+            __builtin_amdgcn_sched_barrier(0);
+            const int lim = min(qi, S - 1) - k0 - 8 * g;
+            auto block_max = [&](auto diag) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+#pragma unroll
+                    for (int u = 0; u < 2; ++u)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            if constexpr (decltype(diag)::value)
+                                if (32 * c + 4 * u + i > lim) sc[c][u][i] = -INFINITY;
+                            mx = fmaxf(mx, sc[c][u][i]);
+                        }
+                return mx;
+            };
+            float mloc = (k0 + KB > q0 || k0 + KB > S) ? block_max(std::true_type{}) : block_max(std::false_type{});
+            mloc = xrow_max4(mloc);
+            mloc *= scale_log2;
+            if (__any(mloc > m_run + 8.0f)) {
+                const float m_new = fmaxf(m_run, mloc);
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                l_run *= alpha;
+#pragma unroll
+                for (int j = 0; j < NHT; ++j) o[j] *= alpha;
+                m_run = m_new;
             }
-        __builtin_amdgcn_sched_barrier(0);
-        const int lim = min(qi, S - 1) - k0 - 8 * g;
-        auto block_max = [&](auto diag) {
-            float mx = -INFINITY;
+            float psum = 0.f;
+            f16x8 pf[2];
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        if constexpr (decltype(diag)::value)
-                            if (32 * c + 4 * u + i > lim) sc[c][u][i] = -INFINITY;
-                        mx = fmaxf(mx, sc[c][u][i]);
+                        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[c][u][i], scale_log2, -m_run));
+                        psum += p;
+                        pf[c][4 * u + i] = (f16)p;
                     }
-            return mx;
+            l_run += psum;
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int j = 0; j < NHT; ++j) o[j] = mfma16(vf[c][j], pf[c], o[j]);
         };
-        float mloc = (k0 + KB > q0 || k0 + KB > S) ? block_max(std::true_type{}) : block_max(std::false_type{});
-        mloc = xrow_max4(mloc);
-        mloc *= scale_log2;
-        if (__any(mloc > m_run + 8.0f)) {
-            const float m_new = fmaxf(m_run, mloc);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run *= alpha;
-#pragma unroll
-            for (int j = 0; j < NHT; ++j) o[j] *= alpha;
-            m_run = m_new;
+        if constexpr (NG == 1) {
+            for (int kb0 = 0; kb0 < nkb; kb0 += NS) {
+                step(kb0, std::integral_constant<int, 0>{});
+                if (kb0 + 1 < nkb) step(kb0 + 1, std::integral_constant<int, 1>{});
+                if constexpr (NS == 3)
+                    if (kb0 + 2 < nkb) step(kb0 + 2, std::integral_constant<int, 2>{});
+            }
+        } else {
+            // both groups take ceil(nkb / 2) steps (block-uniform count)
+            const int nst = (nkb + 1) / 2;
+            for (int s0 = 0; s0 < nst; s0 += 2) {
+                step(2 * s0 + GI, std::integral_constant<int, 0>{});
+                if (s0 + 1 < nst) step(2 * (s0 + 1) + GI, std::integral_constant<int, 1>{});
+            }
         }
-        float psum = 0.f;
-        f16x8 pf[2];
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int u = 0; u < 2; ++u)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[c][u][i], scale_log2, -m_run));
-                    psum += p;
-                    pf[c][4 * u + i] = (f16)p;
-                }
-        l_run += psum;
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-            for (int j = 0; j < NHT; ++j) o[j] = mfma16(vf[c][j], pf[c], o[j]);
     };
     if constexpr (NG == 1) {
-        for (int kb0 = 0; kb0 < nkb; kb0 += NS) {
-            step(kb0, std::integral_constant<int, 0>{});
-            if (kb0 + 1 < nkb) step(kb0 + 1, std::integral_constant<int, 1>{});
-            if constexpr (NS == 3)
-                if (kb0 + 2 < nkb) step(kb0 + 2, std::integral_constant<int, 2>{});
-        }
+        group_loop(std::integral_constant<int, 0>{});
     } else {
-        // both groups take ceil(nkb / 2) steps (block-uniform count)
-        const int nst = (nkb + 1) / 2;
-        for (int s0 = 0; s0 < nst; s0 += 2) {
-            step(2 * s0 + grp, std::integral_constant<int, 0>{});
-            if (s0 + 1 < nst) step(2 * (s0 + 1) + grp, std::integral_constant<int, 1>{});
-        }
+        if (grp == 0) group_loop(std::integral_constant<int, 0>{});
+        else group_loop(std::integral_constant<int, 1>{});
         // group 1 hands (m, l, o) to group 0 through the (now idle) stage buffers
         lds_barrier();
-        float* xo = (float*)sK0;  // [4 waves][32 values][64 lanes]: 32 KB
+        // o of hd tiles 0..3 in sK0, 4..7 in sK1: [4 waves][16 values][64 lanes]
+        auto xo = [&](int j, int e) -> float& {
+            return ((float*)(j < NHT / 2 ? sK0 : sK1))[(w * 16 + 4 * (j % (NHT / 2)) + e) * 64 + lane];
+        };
         float* xm = (float*)sV0;  // [4 waves][2][64 lanes]
         if (grp == 1) {
 #pragma unroll
             for (int j = 0; j < NHT; ++j)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) xo[(w * 32 + 4 * j + e) * 64 + lane] = o[j][e];
+                for (int e = 0; e < 4; ++e) xo(j, e) = o[j][e];
             xm[(w * 2) * 64 + lane] = m_run;
             xm[(w * 2 + 1) * 64 + lane] = l_run;
         }
@@ -470,7 +493,7 @@ __global__ __launch_bounds__(256 * NG) void attn_prefill_dma_kernel(const f16* _
 #pragma unroll
         for (int j = 0; j < NHT; ++j)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[j][e] = o[j][e] * c0 + xo[(w * 32 + 4 * j + e) * 64 + lane] * c1;
+            for (int e = 0; e < 4; ++e) o[j][e] = o[j][e] * c0 + xo(j, e) * c1;
         m_run = mm;
     }
     const float lt = xrow_sum4(l_run);
