@@ -16,11 +16,6 @@
 namespace rh {
 namespace {
 
-int grid_for(size_t n, int per) {
-    const size_t g = (n + per - 1) / per;
-    return (int)(g > 65535 ? 65535 : (g ? g : 1));
-}
-
 // Softmax cross-entropy gradient of one logits row (cross_entropy.rs:58-96
 // without the 1/S, which kappa carries): dl = (softmax - onehot) * unit, times
 // 1 - (z/c)^2 when the logits z were softcapped (full_model.rs:608-615), fp16
