@@ -542,6 +542,12 @@ __device__ __forceinline__ float row_sum_dpp(float v) {
 // LDS once at the end.  Positions past the wave's range read a clamped
 // (valid) row and are masked; a chunk past the current position stores an
 // empty partial (m = -inf, l = 0, o = 0).
+// Offset of element (token b, column c) of a decode output with C columns:
+// row-major, or fragment order (frag) for the decode GEMV's x_frag input.
+__device__ __forceinline__ size_t dec_out_off(int b, int c, int C, int frag) {
+    return frag ? frag_off(b, c, C) : (size_t)b * C + c;
+}
+
 template <int HD, int NP>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict__ Q,
                                                           const f16* __restrict__ Kc,
@@ -549,7 +555,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict_
                                                           const int* __restrict__ pos,
                                                           float* part_m, float* part_l,
                                                           float* part_o, f16* out, int H, int ctx,
-                                                          int per_fixed, float scale) {
+                                                          int per_fixed, float scale, int out_frag) {
     constexpr int LPP = HD / 8, SL = 64 / LPP, STEP = SL * NP;
     __shared__ float sm_[4], sl_[4];
     __shared__ float so_[4][HD];
@@ -670,7 +676,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict_
             O += so_[v][tid] * c;
         }
         if (nch == 1) {
-            out[bh * HD + tid] = (f16)(O / L);
+            out[dec_out_off(b, h * HD + tid, H * HD, out_frag)] = (f16)(O / L);
         } else {
             const size_t pidx = bh * nch + chunk;
             part_o[pidx * HD + tid] = O;
@@ -685,7 +691,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const f16* __restrict_
 // empty chunks carry m = -inf, l = 0, o = 0.
 template <int MAXCH>
 __global__ void attn_merge_kernel(const float* part_m, const float* part_l, const float* part_o,
-                                  f16* out, int H, int HD, int nch) {
+                                  f16* out, int H, int HD, int nch, int out_frag) {
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const size_t bh = (size_t)b * H + h;
     const float* pm = part_m + bh * nch;
@@ -716,7 +722,7 @@ __global__ void attn_merge_kernel(const float* part_m, const float* part_l, cons
         }
         M = Mn;
     }
-    out[bh * HD + d] = (f16)(o / l);
+    out[dec_out_off(b, h * HD + d, H * HD, out_frag)] = (f16)(o / l);
 }
 
 }  // namespace
@@ -760,8 +766,10 @@ int attn_decode_chunks(int B, int H, int ctx) {
 
 hipError_t launch_attn_decode(const f16* q, const f16* k, const f16* v, const int* pos,
                               float* part_m, float* part_l, float* part_o, f16* out, int B, int H,
-                              int hd, int ctx, hipStream_t st, int nch) {
+                              int hd, int ctx, hipStream_t st, int nch, bool out_frag) {
     if (B < 1 || H < 1 || ctx < 1) return hipErrorInvalidValue;
+    if (out_frag && (B > 16 || (H * hd) % 128 != 0)) return hipErrorInvalidValue;
+    const int of = out_frag ? 1 : 0;
     int per = 0;  // whole context split over nch chunks (forced nch: tuning)
     if (nch <= 0) {
         nch = attn_decode_chunks(B, H, ctx);
@@ -771,17 +779,17 @@ hipError_t launch_attn_decode(const f16* q, const f16* k, const f16* v, const in
     const float scale = 1.0f / sqrtf((float)hd);
     if (hd == 128)
         hipLaunchKernelGGL((attn_decode_kernel<128, 8>), grid, dim3(256), 0, st, q, k, v, pos, part_m, part_l,
-                           part_o, out, H, ctx, per, scale);
+                           part_o, out, H, ctx, per, scale, of);
     else if (hd == 64)
         hipLaunchKernelGGL((attn_decode_kernel<64, 4>), grid, dim3(256), 0, st, q, k, v, pos, part_m, part_l,
-                           part_o, out, H, ctx, per, scale);
+                           part_o, out, H, ctx, per, scale, of);
     else
         return hipErrorInvalidValue;
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || nch == 1) return e;
     // one round of loads covers contexts up to 32 * ATTN_DEC_CHUNK positions
     hipLaunchKernelGGL((attn_merge_kernel<32>), dim3(H, B), dim3(hd), 0, st, part_m, part_l, part_o, out, H, hd,
-                       nch);
+                       nch, of);
     return hipGetLastError();
 }
 

@@ -44,7 +44,7 @@ namespace {
 
 constexpr float XG_SCALE = 1.0f / 16.0f;
 
-template <int EPI, int RT, int NW, int DEPTH, bool NORM>
+template <int EPI, int RT, int NW, int DEPTH, bool NORM, bool XF = false>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
     __shared__ f32x4 sred[NW][RT][64];
     extern __shared__ __attribute__((aligned(16))) f16 sx[];  // NORM: normalised rows [B][K]
@@ -65,6 +65,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
     const bool xvalid = r < a.B;
     const int xrow = xvalid ? r : 0;
     const f16* xp = a.X + (size_t)xrow * K + 8 * g;
+    const f16* xf = a.X + lane * 8;  // XF (x_frag): lane l's 16 bytes of each 1 KB fragment
 
     f32x4 acc[RT];
 #pragma unroll
@@ -89,7 +90,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
             if constexpr (NORM)
                 xr[u] = *(const f16x8*)&sx[xrow * K + off + 32 * u + 8 * g];
             else
-                xr[u] = *(const f16x8*)(xp + off + 32 * u);
+                xr[u] = *(const f16x8*)(XF ? xf + (size_t)(off >> 7) * 2048 + 512 * u : xp + off + 32 * u);
         }
     };
     auto mac = [&](const f16x8 (&wr)[RT][4], const f16x8 (&xr)[4], bool live) {
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
         f16x4 gv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) gv[e] = (f16)(silu_f(acc[0][e]) * acc[1][e]);
-        *(f16x4*)(a.out_f16 + (size_t)tok * a.ldo + f) = gv;
+        *(f16x4*)(a.out_f16 + (a.out_frag ? frag_off(tok, f, a.ldo) : (size_t)tok * a.ldo + f)) = gv;
     } else {
         const int n = rows[0] + 4 * g;
         float v0 = acc[0][0], v1 = acc[0][1], v2 = acc[0][2], v3 = acc[0][3];
@@ -258,7 +259,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GemvArgs a) {
             if (a.ssq_out) {  // the next RMSNorm's input and partial sums (all 64 lanes)
                 if (live) {
                     const f32x4 gm = *(const f32x4*)(a.gnext + n);
-                    *(f16x4*)(a.xg_out + (size_t)tok * N + n) =
+                    *(f16x4*)(a.xg_out + (a.out_frag ? frag_off(tok, n, N) : (size_t)tok * N + n)) =
                         f16x4{(f16)(x[0] * gm[0] * XG_SCALE), (f16)(x[1] * gm[1] * XG_SCALE),
                               (f16)(x[2] * gm[2] * XG_SCALE), (f16)(x[3] * gm[3] * XG_SCALE)};
                 }
@@ -369,7 +370,10 @@ hipError_t launch_one(const GemvArgs& a, int nblk, hipStream_t st) {
             return hipSuccess;
         }
     }
-    hipLaunchKernelGGL((gemv_kernel<EPI, RT, NW, DEPTH, false>), dim3(nblk), dim3(NW * 64), 0, st, a);
+    if (a.x_frag)
+        hipLaunchKernelGGL((gemv_kernel<EPI, RT, NW, DEPTH, false, true>), dim3(nblk), dim3(NW * 64), 0, st, a);
+    else
+        hipLaunchKernelGGL((gemv_kernel<EPI, RT, NW, DEPTH, false>), dim3(nblk), dim3(NW * 64), 0, st, a);
     return hipSuccess;
 }
 
@@ -413,6 +417,10 @@ hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t st) {
     if (a.xres && (epi == GV_RESID || !a.gamma || !gemv_norm_fits(a.B, a.K))) return hipErrorInvalidValue;
     if (a.ssq_out && (epi != GV_RESID || !a.xg_out || !a.gnext)) return hipErrorInvalidValue;
     if (a.rs_part && (epi == GV_RESID || a.xres || a.rs_n < 1 || a.rs_n > 512)) return hipErrorInvalidValue;
+    if (a.x_frag && a.xres) return hipErrorInvalidValue;  // the in-kernel norm reads xres, not X
+    // fragment-order outputs: whole 128-column chunks (GV_RESID's xg_out, GV_SWIGLU's gate)
+    if (a.out_frag && !((epi == GV_RESID && a.N % 128 == 0) || (epi == GV_SWIGLU && a.ldo % 128 == 0)))
+        return hipErrorInvalidValue;
     const int v = a.cfg > 0 ? a.cfg : pick_variant(epi, a);
     if (v > kNumVariants) return hipErrorInvalidValue;
     const int nblk = (a.N + 15) / 16;

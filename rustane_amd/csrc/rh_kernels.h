@@ -103,11 +103,12 @@ hipError_t launch_attn_prefill(const f16* q, const f16* k, const f16* v, f16* ou
 // split into nch = attn_decode_chunks(B, H, ctx) chunks per (b, h) (a
 // positive nch forces that many equal chunks: tuning); with more than one,
 // per-chunk partials (m, l, o[hd]) go to part_* ([B][H][nch] entries) and a
-// merge kernel writes out.
+// merge kernel writes out.  out_frag: out in fragment order (frag_off over
+// H*hd columns, 16 rows), the decode GEMV's x_frag input.
 constexpr int ATTN_DEC_CHUNK = 128;
 hipError_t launch_attn_decode(const f16* q, const f16* k, const f16* v, const int* pos,
                               float* part_m, float* part_l, float* part_o, f16* out, int B, int H,
-                              int hd, int ctx, hipStream_t st, int nch = 0);
+                              int hd, int ctx, hipStream_t st, int nch = 0, bool out_frag = false);
 int attn_decode_chunks(int B, int H, int ctx);
 
 // ---------------- decode GEMV (B <= 16 tokens) ----------------
@@ -144,9 +145,20 @@ struct GemvArgs {
     // and scales the accumulators before the epilogue.
     const float* rs_part;
     int rs_n;
+    // Fragment-order activations (frag_off, 16 rows; rows >= B are read and
+    // their results dropped, so the buffer must hold 16 rows): x_frag for X,
+    // out_frag for the fp16 rows a later GEMV reads (GV_RESID's xg_out,
+    // GV_SWIGLU's gate).  Every X load then reads 1 KB contiguous, where
+    // row-major X of more than 8 tokens touches 16 cache lines per load.
+    bool x_frag, out_frag;
 };
 // W is fp16 [N, K] in fragment order (frag_off), rows padded to a multiple of 16.
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t st);
+// Decode batches whose GEMV inputs (attention output, gate, x * gamma) go in
+// fragment order, 16 rows: with row-major rows every X load of more than 8
+// tokens touches 16 cache lines instead of 8 (W2 GEMV at 16 tokens 19.1 ->
+// 17.2 us, flat in the token count).
+constexpr bool gemv_frag_inputs(int B) { return B > 8; }
 int gemv_num_variants();
 constexpr size_t GEMV_NORM_LDS = 32768;  // bytes of normalised rows a block may stage
 bool gemv_norm_fits(int B, int K);

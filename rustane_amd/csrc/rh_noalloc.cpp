@@ -57,11 +57,12 @@ size_t layout(const rh_ctx* ctx, int B, bool own_logits, unsigned char* base, rh
         off += align256(bytes);
         return p;
     };
+    const size_t R = rh::gemv_frag_inputs(B) ? 16 : (size_t)B;  // fragment-order inputs hold 16 rows
     b->dx = (float*)take((size_t)B * D * 4);
-    b->dxn = (f16*)take((size_t)B * D * 2);
+    b->dxn = (f16*)take(R * D * 2);
     b->dq = (f16*)take((size_t)B * D * 2);
-    b->dattn = (f16*)take((size_t)B * D * 2);
-    b->dgate = (f16*)take((size_t)B * F * 2);
+    b->dattn = (f16*)take(R * D * 2);
+    b->dgate = (f16*)take(R * F * 2);
     b->dlogits = own_logits ? (float*)take((size_t)B * V * 4) : nullptr;
     b->pm = (float*)take(part * 4);
     b->pl = (float*)take(part * 4);

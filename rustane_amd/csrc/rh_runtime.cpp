@@ -260,6 +260,7 @@ int rhrt::enqueue_decode_step(rh_ctx* ctx, int B, const DecodeBufs& b) {
     const int D = c.dim, F = c.hidden;
     const float alpha = 1.0f / std::sqrt(2.0f * (float)c.nlayers);
     const bool fuse_norm = rh::gemv_norm_fits(B, D);
+    const bool xfrag = rh::gemv_frag_inputs(B);  // fp16 GEMV inputs in fragment order
     hipStream_t st = ctx->stream;
     // Input of a normed GEMV.  Small B: the GEMV normalises x itself (xres +
     // gamma).  Larger B: the residual GEMV before it left fp16(x * gamma) in
@@ -272,14 +273,15 @@ int rhrt::enqueue_decode_step(rh_ctx* ctx, int B, const DecodeBufs& b) {
         } else if (xg) {
             g.X = b.dxn; g.rs_part = b.ssq; g.rs_n = D / 16; g.eps = c.rms_eps;
         } else {
-            LCK(rh::launch_rmsnorm(b.dx, gamma, b.dxn, B, D, c.rms_eps, st));
+            LCK(rh::launch_rmsnorm(b.dx, gamma, b.dxn, B, D, c.rms_eps, st, xfrag));
             g.X = b.dxn;
         }
+        g.x_frag = xfrag && !fuse_norm;
         return RH_OK;
     };
     auto produce = [&](rh::GemvArgs& g, const float* gnext) {
         if (fuse_norm || !b.ssq) return;
-        g.xg_out = b.dxn; g.gnext = gnext; g.ssq_out = b.ssq;
+        g.xg_out = b.dxn; g.gnext = gnext; g.ssq_out = b.ssq; g.out_frag = xfrag;
         xg = true;
     };
     LCK(rh::launch_embed(b.tok_in, ctx->embed, b.dx, B, D, c.vocab, ctx->d_err, st));
@@ -295,20 +297,20 @@ int rhrt::enqueue_decode_step(rh_ctx* ctx, int B, const DecodeBufs& b) {
         RCK(timed(ctx, RH_K_GEMV_QKV, [&] { return rh::launch_gemv(rh::GV_QKV, g, st); }));
         RCK(timed(ctx, RH_K_DECODE_ATTN, [&] {
             return rh::launch_attn_decode(b.dq, kc, vc, b.state, b.pm, b.pl, b.po, b.dattn, B, c.heads,
-                                          c.head_dim, ctx->max_ctx, st);
+                                          c.head_dim, ctx->max_ctx, st, 0, xfrag);
         }));
         g = rh::GemvArgs{};
-        g.W = W.wo; g.X = b.dattn; g.B = B; g.N = D; g.K = D;
+        g.W = W.wo; g.X = b.dattn; g.B = B; g.N = D; g.K = D; g.x_frag = xfrag;
         g.out_f32 = b.dx; g.ldo = D; g.alpha = alpha;
         produce(g, W.g2);
         RCK(timed(ctx, RH_K_GEMV_WO, [&] { return rh::launch_gemv(rh::GV_RESID, g, st); }));
         g = rh::GemvArgs{};
         RCK(normed(g, W.g2));
         g.W = W.w13; g.B = B; g.N = 2 * F; g.K = D;
-        g.out_f16 = b.dgate; g.ldo = F;
+        g.out_f16 = b.dgate; g.ldo = F; g.out_frag = xfrag;
         RCK(timed(ctx, RH_K_GEMV_W13, [&] { return rh::launch_gemv(rh::GV_SWIGLU, g, st); }));
         g = rh::GemvArgs{};
-        g.W = W.w2; g.X = b.dgate; g.B = B; g.N = D; g.K = F;
+        g.W = W.w2; g.X = b.dgate; g.B = B; g.N = D; g.K = F; g.x_frag = xfrag;
         g.out_f32 = b.dx; g.ldo = D; g.alpha = alpha;
         produce(g, l + 1 < c.nlayers ? ctx->L[l + 1].g1 : ctx->gfinal);
         RCK(timed(ctx, RH_K_GEMV_W2, [&] { return rh::launch_gemv(rh::GV_RESID, g, st); }));

@@ -4,9 +4,11 @@ Two contexts hold the same weights and the same prefilled KV cache; one
 steps with rh_decode_step (host buffers, the context's own decode buffers,
 graph replay), the other with rh_decode_step_noalloc (device buffers, the
 library's fixed scratch array, eager launches).  Greedy ids must be equal and
-logits within the fp16 bar.  Two calls in a row: batch 8 (the RMSNorm row
-kernel path), then a fresh prefill at batch 2 (the norm fused into the
-GEMVs), so the second call runs on scratch the first one left behind.
+logits within the fp16 bar.  Two calls in a row: batch 12 at dim 2048 (the
+first RMSNorm of a step as a row kernel, the others from the residual GEMVs,
+and the GEMV inputs in 16-row fragment order), then a fresh prefill at batch
+2 (the norm fused into the GEMVs, row-major inputs), so the second call runs
+on scratch the first one left behind.
 
 The step is also captured into a HIP graph on the context stream and
 replayed: each replay reads and advances the context's device-side
@@ -39,15 +41,15 @@ def _noalloc_step(c, tok, want_logits=True):
 
 
 def test_noalloc_step_matches_decode_step():
-    cfg = ModelConfig(512, 1024, 4, 4, 128, 64, 2, 1000)
+    cfg = ModelConfig(2048, 1024, 16, 16, 128, 64, 2, 1000)
     w = random_gammas(ModelWeights.normal(cfg, seed=91, std=0.05), seed=92)
     tensors = [lw.tensors() for lw in w.layers]
-    ref = hb.Context(cfg.to_rh(), 0, 8, 256)
-    noa = hb.Context(cfg.to_rh(), 0, 8, 256)
+    ref = hb.Context(cfg.to_rh(), 0, 12, 256)
+    noa = hb.Context(cfg.to_rh(), 0, 12, 256)
     try:
         for c in (ref, noa):
             c.load_weights(w.embed, w.gamma_final, tensors)
-        for call, (B, P) in enumerate([(8, 140), (2, 37)]):
+        for call, (B, P) in enumerate([(12, 140), (2, 37)]):
             print(f"[case] noalloc call {call}: batch {B}, prompt {P}", flush=True)
             prompt, _ = tokens_uniform(93 + call, cfg.vocab, B, P)
             n_ref, _ = ref.prefill(prompt)
@@ -111,7 +113,7 @@ def _weights(cfg, seed):
     return w, [lw.tensors() for lw in w.layers]
 
 
-@pytest.mark.parametrize("B", [1, 6])
+@pytest.mark.parametrize("B", [1, 6, 12])
 def test_captured_noalloc_step_replays_advance(B):
     """A graph of one allocation-free step with in_tok == out_tok, replayed
     n times with eager work and synchronisations in between, equals n eager
