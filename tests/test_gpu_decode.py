@@ -175,14 +175,17 @@ def test_decode_large_residual_matches_forward(orc):
             assert err <= 2e-3, (p, err)
 
 
-def test_decode_tiny_config_hd64(orc):
+@pytest.mark.parametrize("batch", [1, 12])
+def test_decode_tiny_config_hd64(orc, batch):
+    """hd 64; at 12 sequences the attention output and the gate reach the Wo
+    and W2 GEMVs in 16-row fragment order (the merge kernel writes it)."""
     from rustane_amd.engine import tiny_config
     cfg = tiny_config()
     cfg.seq = 72
     w = ModelWeights.normal(cfg, seed=49)
-    tok, tgt = tokens_uniform(50, cfg.vocab, 1, cfg.seq)
+    tok, tgt = tokens_uniform(50, cfg.vocab, batch, cfg.seq)
     lg, _, _ = orc.forward(oracle_cfg(orc, cfg), oracle_weights(orc, w), tok, tgt)
-    with _ctx(cfg, w, 1, 80) as c:
+    with _ctx(cfg, w, batch, 80) as c:
         c.prefill(tok[:, :64])
         for p in range(64, 72):
             _, dl = c.decode_step(tok[:, p], want_logits=True)
