@@ -148,17 +148,19 @@ struct GemvArgs {
     // Fragment-order activations (frag_off, 16 rows; rows >= B are read and
     // their results dropped, so the buffer must hold 16 rows): x_frag for X,
     // out_frag for the fp16 rows a later GEMV reads (GV_RESID's xg_out,
-    // GV_SWIGLU's gate).  Every X load then reads 1 KB contiguous, where
-    // row-major X of more than 8 tokens touches 16 cache lines per load.
+    // GV_SWIGLU's gate).  Every X load then reads 1 KB contiguous (8 cache
+    // lines), where a row-major one touches a line per live token.
     bool x_frag, out_frag;
 };
 // W is fp16 [N, K] in fragment order (frag_off), rows padded to a multiple of 16.
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t st);
 // Decode batches whose GEMV inputs (attention output, gate, x * gamma) go in
-// fragment order, 16 rows: with row-major rows every X load of more than 8
-// tokens touches 16 cache lines instead of 8 (W2 GEMV at 16 tokens 19.1 ->
-// 17.2 us, flat in the token count).
-constexpr bool gemv_frag_inputs(int B) { return B > 8; }
+// fragment order, 16 rows.  A row-major X load touches one cache line per
+// live token (lane row r reads token r; rows past B reread token 0), a
+// fragment-order one always 8: standalone, the W2 GEMV takes 15.9 us
+// row-major up to 8 tokens, then 0.45 us more per token (17.2 at 11, 19.1 at
+// 16), and 17.2 us in fragment order at any count.
+constexpr bool gemv_frag_inputs(int B) { return B >= 12; }
 int gemv_num_variants();
 constexpr size_t GEMV_NORM_LDS = 32768;  // bytes of normalised rows a block may stage
 bool gemv_norm_fits(int B, int K);
